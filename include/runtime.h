@@ -1,0 +1,143 @@
+#ifndef QVELOX_RUNTIME_H
+#define QVELOX_RUNTIME_H
+/* libredshift_hip: the full-attention path of the qvelox runtime for AMD
+ * Instinct MI355X (gfx950).
+ *
+ * The first part keeps the reference's C ABI byte for byte (src/runtime.h:9-74
+ * of the reference); qv_test_attention has its full semantics and the entry
+ * points outside the attention path are exported so that the reference's
+ * ctypes loader (qvelox/runtime.py:6-22) resolves them, but return -1 with a
+ * message.  The second part adds device-pointer, stream-ordered entry points
+ * for the raw attention core on the paged KV cache. */
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* Synchronous kernel validation ABI. All pointers refer to host memory.
+ * Returns 0 on success, -1 on failure. qv_error() describes the last failure
+ * on the calling thread, until its next ABI call. Caller owns buffer lengths.
+ * These entry points include allocation and transfers: do not time them as
+ * model inference. Batch sizes are 1..8. */
+/* Replaces qv_error, src/runtime.cu:79 (thread-local message, "" after success). */
+const char *qv_error(void);
+/* Exported for loader compatibility (src/runtime.cu:81-114): quantized
+ * projections are not part of this library; always returns -1. */
+int qv_test_mm(float *out, const void *weights, const float *x,
+               int kind, int batch, int width, int rows);
+int qv_test_mm_fast(float *out, const void *weights, const float *x,
+               int kind, int batch, int width, int rows);
+/* Exported for loader compatibility (src/runtime.cu:116-129); returns -1. */
+int qv_test_norm(float *out, const float *x, const float *weights,
+                 int batch, int width, float epsilon);
+/* Exported for loader compatibility (src/runtime.cu:131-165); returns -1. */
+int qv_test_delta(float *out, float *state, float *history,
+                  const float *qkv, const float *gate,
+                  const float *alpha, const float *beta,
+                  const float *conv, const float *decay,
+                  const float *bias, const float *norm,
+                  int batch, int key_heads, int value_heads, int dim,
+                  float epsilon);
+
+/* Fixed model attention: 24 query heads, 4 KV heads, head dimension 256.
+ * out: [batch,24,256]; q_gate: [batch,24,512]; key/value: [batch,4,256];
+ * q_norm/k_norm: [256]. Caches (in/out) hold IEEE float16 bits as
+ * [position+batch,4,256]. Only the prefix [0,position) is read from host.
+ * 0 <= position and position+batch <= 139264.
+ * Replaces qv_test_attention, src/runtime.cu:167-197 (same validation order:
+ * batch, epsilon, position, null pointers, all before any buffer is read). */
+int qv_test_attention(float *out, void *key_cache, void *value_cache,
+                      const float *q_gate, const float *key, const float *value,
+                      const float *q_norm, const float *k_norm,
+                      int batch, int position, float epsilon);
+
+/* Model ABI (src/runtime.h:47-74 of the reference). The model session needs
+ * the quantized projections and recurrent layers, which are not part of this
+ * library: every call returns -1 (qv_create also stores NULL in *handle) and
+ * qv_destroy does nothing. Declared so the header stays a drop-in. */
+int qv_create(void **handle, const char *path, int context, float epsilon);
+int qv_upload(void *handle, int slot, uint64_t offset, uint64_t length);
+int qv_evaluate(void *handle, const int *tokens, int batch, float *out);
+int qv_verify(void *handle, const int *tokens, int batch, float *out);
+int qv_commit(void *handle, int accepted);
+int qv_advance(void *handle, const int *tokens, int batch, int *next);
+int qv_reset(void *handle);
+int qv_checkpoint(void *handle);
+int qv_restore(void *handle);
+int qv_position(void *handle, int *position);
+void qv_destroy(void *handle);
+
+/* ------------------------------------------------------------------------
+ * Device ABI (additive; no counterpart in the reference, whose kernels are
+ * reachable only through the host-pointer test entry and the model session).
+ * All pointers are device memory on the current HIP device, 16-byte aligned.
+ * `stream` is a hipStream_t (NULL = the null stream). Calls only enqueue work:
+ * they return before it runs and do not synchronize. Returns 0 or -1 with
+ * qv_error() set; validation happens before anything is enqueued.
+ *
+ * KV cache: per KV head a contiguous run of `capacity` tokens (a multiple of
+ * 32) in 32-token pages laid out in matrix-core operand order; K and V are
+ * separate allocations of qv_kv_bytes() bytes each. Element type is 16-bit
+ * (fp16 or bf16, chosen by the caller per call).
+ * Query row t (0-based) of a call at `position` sees keys 0..position+t.
+ * ---------------------------------------------------------------------- */
+#define QV_F16 1
+#define QV_BF16 2
+
+/* Bytes of one K (or V) cache: kv_heads * capacity * head_dim * 2. */
+int qv_kv_bytes(uint64_t *bytes, int kv_heads, int head_dim, int capacity);
+/* Copy token-major rows [count][kv_heads][head_dim] (16-bit) into the pages
+ * of tokens first..first+count-1; either K or V side may be NULL. */
+int qv_kv_pack(void *k_pages, void *v_pages, const void *k_rows, const void *v_rows,
+               int kv_heads, int head_dim, int capacity, int first, int count,
+               void *stream);
+/* Inverse of qv_kv_pack. */
+int qv_kv_unpack(void *k_rows, void *v_rows, const void *k_pages, const void *v_pages,
+                 int kv_heads, int head_dim, int capacity, int first, int count,
+                 void *stream);
+
+/* Workspace bytes that qv_attention needs for this shape on the current
+ * device (split-K partials). */
+int qv_attention_workspace(uint64_t *bytes, int q_heads, int kv_heads, int head_dim,
+                           int tokens, int position);
+/* Raw causal GQA attention core, the reference's attention / attention_tiled
+ * (src/kernels.cu:435-456,466-503) without prepare and gate, generalised to
+ * q_heads/kv_heads/head_dim/scale: out[t][h] = softmax_p(q[t][h] . k[p][h/G] *
+ * scale, p <= position+t) . v[p][h/G], G = q_heads/kv_heads.
+ * q, out: [tokens][q_heads][head_dim] of `dtype`; fp32 softmax and
+ * accumulation. head_dim 128 or 256; G <= 16; 1 <= tokens;
+ * position+tokens <= capacity. Split-K over all CUs plus a log-sum-exp
+ * combine; work = qv_attention_split then qv_attention_combine. */
+int qv_attention(void *out, const void *q, const void *k_pages, const void *v_pages,
+                 int dtype, int q_heads, int kv_heads, int head_dim,
+                 int tokens, int position, int capacity, float scale,
+                 void *workspace, uint64_t workspace_bytes, void *stream);
+/* The two phases of qv_attention for one token chunk (G*tokens <= 16), for
+ * callers that time or schedule them separately. */
+int qv_attention_split(const void *q, const void *k_pages, const void *v_pages,
+                       int dtype, int q_heads, int kv_heads, int head_dim,
+                       int tokens, int position, int capacity, float scale,
+                       void *workspace, uint64_t workspace_bytes, void *stream);
+int qv_attention_combine(void *out, int dtype, int q_heads, int kv_heads, int head_dim,
+                         int tokens, int position, const void *workspace,
+                         uint64_t workspace_bytes, void *stream);
+
+/* Workspace bytes of qv_attention_fused for this batch/position. */
+int qv_attention_fused_workspace(uint64_t *bytes, int batch, int position);
+/* Device-side drop-in for the reference's k_attention (src/kernels.cu:575-580)
+ * on the paged fp16 cache: RMSNorm + RoPE of q/k, fp16 append of k/v at
+ * position..position+batch-1, causal GQA attention (scale 1/16), times
+ * sigmoid(gate). Shapes as qv_test_attention, all float32 device buffers;
+ * the caches are fp16 pages with 24/4/256 geometry. */
+int qv_attention_fused(float *out, void *k_pages, void *v_pages,
+                       const float *q_gate, const float *key, const float *value,
+                       const float *q_norm, const float *k_norm,
+                       int batch, int position, int capacity, float epsilon,
+                       void *workspace, uint64_t workspace_bytes, void *stream);
+
+#ifdef __cplusplus
+}
+#endif
+#endif

@@ -1,0 +1,137 @@
+"""Torch-tensor front end for the device ABI of libredshift_hip.
+
+torch only supplies device memory and the stream; every computation runs in
+the HIP library.  All calls are stream-ordered on torch's current stream.
+"""
+import ctypes as ct
+
+import torch
+
+from .runtime import QV_BF16, QV_F16, check, library
+
+PAGE_TOKENS = 32
+# Query rows (group * tokens) per KV head that one split/combine pair serves.
+MAX_CHUNK_ROWS = 16
+
+
+def dtype_code(dtype):
+    if dtype == torch.float16:
+        return QV_F16
+    if dtype == torch.bfloat16:
+        return QV_BF16
+    raise ValueError(f'unsupported KV dtype {dtype}: use float16 or bfloat16')
+
+
+def round_capacity(tokens):
+    """Smallest page-aligned capacity holding `tokens` tokens."""
+    return -(-tokens // PAGE_TOKENS) * PAGE_TOKENS
+
+
+def _stream():
+    return ct.c_void_p(torch.cuda.current_stream().cuda_stream)
+
+
+def _ptr(t):
+    return ct.c_void_p(t.data_ptr())
+
+
+class PagedKV:
+    """K and V caches of one attention layer in the library's page layout:
+    per KV head, `capacity` tokens in 32-token pages (include/runtime.h)."""
+
+    def __init__(self, kv_heads, head_dim, capacity, dtype=torch.float16, device='cuda'):
+        lib = library()
+        size = ct.c_uint64()
+        check(lib, lib.qv_kv_bytes(ct.byref(size), kv_heads, head_dim, capacity))
+        self.kv_heads, self.head_dim, self.capacity, self.dtype = kv_heads, head_dim, capacity, dtype
+        self.k = torch.empty(size.value // 2, dtype=dtype, device=device)
+        self.v = torch.empty(size.value // 2, dtype=dtype, device=device)
+
+    def pack(self, k_rows, v_rows, first=0):
+        """Write token-major rows [count][kv_heads][head_dim] at tokens first..."""
+        lib = library()
+        k_rows = k_rows.to(self.dtype).contiguous()
+        v_rows = v_rows.to(self.dtype).contiguous()
+        assert k_rows.shape == v_rows.shape and k_rows.shape[1:] == (self.kv_heads, self.head_dim)
+        check(lib, lib.qv_kv_pack(_ptr(self.k), _ptr(self.v), _ptr(k_rows), _ptr(v_rows),
+                                  self.kv_heads, self.head_dim, self.capacity, first,
+                                  k_rows.shape[0], _stream()))
+        return self
+
+    def unpack(self, first, count):
+        """Token-major copies [count][kv_heads][head_dim] of tokens first..."""
+        lib = library()
+        k_rows = torch.empty((count, self.kv_heads, self.head_dim), dtype=self.dtype, device=self.k.device)
+        v_rows = torch.empty_like(k_rows)
+        check(lib, lib.qv_kv_unpack(_ptr(k_rows), _ptr(v_rows), _ptr(self.k), _ptr(self.v),
+                                    self.kv_heads, self.head_dim, self.capacity, first, count,
+                                    _stream()))
+        return k_rows, v_rows
+
+
+def attention_workspace_bytes(q_heads, kv_heads, head_dim, tokens, position):
+    lib = library()
+    size = ct.c_uint64()
+    check(lib, lib.qv_attention_workspace(ct.byref(size), q_heads, kv_heads, head_dim, tokens, position))
+    return size.value
+
+
+def workspace(nbytes, device='cuda'):
+    return torch.empty(max(int(nbytes), 256), dtype=torch.uint8, device=device)
+
+
+def attention(q, cache, position, scale, out=None, ws=None):
+    """Raw causal GQA attention: q [tokens][q_heads][head_dim] (cache dtype),
+    row t sees keys 0..position+t of `cache` (a PagedKV)."""
+    lib = library()
+    q = q.contiguous()
+    tokens, q_heads, head_dim = q.shape
+    if out is None:
+        out = torch.empty_like(q)
+    if ws is None:
+        ws = workspace(attention_workspace_bytes(q_heads, cache.kv_heads, head_dim, tokens, position), q.device)
+    check(lib, lib.qv_attention(_ptr(out), _ptr(q), _ptr(cache.k), _ptr(cache.v), dtype_code(q.dtype),
+                                q_heads, cache.kv_heads, head_dim, tokens, position, cache.capacity,
+                                float(scale), _ptr(ws), ws.numel(), _stream()))
+    return out
+
+
+def attention_split(q, cache, position, scale, ws):
+    """Phase 1 of `attention` for one chunk (split-K partials into ws)."""
+    lib = library()
+    tokens, q_heads, head_dim = q.shape
+    check(lib, lib.qv_attention_split(_ptr(q), _ptr(cache.k), _ptr(cache.v), dtype_code(q.dtype),
+                                      q_heads, cache.kv_heads, head_dim, tokens, position,
+                                      cache.capacity, float(scale), _ptr(ws), ws.numel(), _stream()))
+
+
+def attention_combine(out, cache, position, ws):
+    """Phase 2 of `attention` for one chunk (log-sum-exp combine into out)."""
+    lib = library()
+    tokens, q_heads, head_dim = out.shape
+    check(lib, lib.qv_attention_combine(_ptr(out), dtype_code(out.dtype), q_heads, cache.kv_heads,
+                                        head_dim, tokens, position, _ptr(ws), ws.numel(), _stream()))
+
+
+def fused_workspace_bytes(batch, position):
+    lib = library()
+    size = ct.c_uint64()
+    check(lib, lib.qv_attention_fused_workspace(ct.byref(size), batch, position))
+    return size.value
+
+
+def attention_fused(q_gate, key, value, q_norm, k_norm, cache, position, epsilon, out=None, ws=None):
+    """Device-side fused attention of the fixed 24/4/256 model (the reference's
+    k_attention): prepares q/k, appends k/v at position.., attends and gates.
+    All inputs float32 device tensors; `cache` is an fp16 PagedKV(4, 256, ...)."""
+    lib = library()
+    batch = q_gate.shape[0]
+    if out is None:
+        out = torch.empty((batch, 24, 256), dtype=torch.float32, device=q_gate.device)
+    if ws is None:
+        ws = workspace(fused_workspace_bytes(batch, position), q_gate.device)
+    tensors = [t.contiguous() for t in (q_gate, key, value, q_norm, k_norm)]
+    check(lib, lib.qv_attention_fused(_ptr(out), _ptr(cache.k), _ptr(cache.v),
+                                      *[_ptr(t) for t in tensors], batch, position, cache.capacity,
+                                      float(epsilon), _ptr(ws), ws.numel(), _stream()))
+    return out

@@ -1,0 +1,75 @@
+"""Build libredshift_hip.so in-tree with hipcc for gfx950 only.
+
+Usage: ``python -m redshift_amd.build`` (or ``__graft_entry__.build()``).
+Objects go to ``redshift_amd/_build/``, the library to
+``redshift_amd/lib/libredshift_hip.so``.  Every call recompiles.
+"""
+import os
+import shutil
+import subprocess
+import sys
+from concurrent.futures import ThreadPoolExecutor
+from pathlib import Path
+
+PACKAGE = Path(__file__).resolve().parent
+ROOT = PACKAGE.parent
+SOURCES = ['abi.cpp', 'attention.hip', 'kv.hip']
+LIBRARY = PACKAGE / 'lib' / 'libredshift_hip.so'
+ARCH = 'gfx950'
+
+# Packed-FP32 instructions are kept out of every code object: hipcc would
+# otherwise form v_pk_{add,mul,fma}_f32 from ordinary float code.
+COMMON_FLAGS = [
+    '-O3', '-std=c++17', '-fPIC', f'--offload-arch={ARCH}',
+    '-Xclang', '-target-feature', '-Xclang', '-packed-fp32-ops',
+    '-Wall', '-Wno-unused-result',
+    f'-I{ROOT / "include"}', f'-I{PACKAGE / "csrc"}',
+]
+
+
+def hipcc():
+    path = shutil.which('hipcc') or '/opt/rocm/bin/hipcc'
+    if not Path(path).exists():
+        raise RuntimeError('hipcc not found: the HIP toolchain is required to build libredshift_hip')
+    return path
+
+
+def _run(cmd):
+    result = subprocess.run(cmd, capture_output=True, text=True)
+    # The host pass does not know the packed-fp32 target feature; that
+    # warning is expected and dropped.
+    noise = "'-packed-fp32-ops' is not a recognized feature"
+    stderr = '\n'.join(line for line in result.stderr.splitlines() if noise not in line)
+    if result.returncode != 0:
+        raise RuntimeError(f'command failed ({result.returncode}): {" ".join(cmd)}\n{stderr}')
+    return stderr
+
+
+def build(verbose=False, jobs=None):
+    """Compile every source and link the shared library; returns its path."""
+    compiler = hipcc()
+    objdir = PACKAGE / '_build'
+    objdir.mkdir(exist_ok=True)
+    LIBRARY.parent.mkdir(exist_ok=True)
+    jobs = jobs or min(len(SOURCES), os.cpu_count() or 1)
+
+    def compile_one(name):
+        src = PACKAGE / 'csrc' / name
+        obj = objdir / (name + '.o')
+        cmd = [compiler, '-x', 'hip', *COMMON_FLAGS, '-c', str(src), '-o', str(obj)]
+        return obj, _run(cmd)
+
+    with ThreadPoolExecutor(jobs) as pool:
+        results = list(pool.map(compile_one, SOURCES))
+    for obj, stderr in results:
+        if verbose and stderr:
+            print(stderr, file=sys.stderr)
+    tmp = LIBRARY.with_suffix('.so.tmp')
+    _run([compiler, '-shared', '-fPIC', f'--offload-arch={ARCH}', *[str(o) for o, _ in results],
+          '-o', str(tmp)])
+    os.replace(tmp, LIBRARY)
+    return LIBRARY
+
+
+if __name__ == '__main__':
+    print(build(verbose='-v' in sys.argv))

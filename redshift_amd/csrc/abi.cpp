@@ -1,0 +1,379 @@
+// extern "C" entry points of libredshift_hip (declared in include/runtime.h).
+//
+// Error convention of the reference (src/runtime.cu:10-18,51-63): every entry
+// point runs inside call(), which turns any C++ exception into -1 and a
+// thread-local message; qv_error() returns "" after a success.
+#include "runtime.h"
+
+#include <cmath>
+#include <cstdio>
+#include <cstring>
+#include <limits>
+
+#include "kernels.hpp"
+
+namespace {
+
+thread_local char last_error[512] = {};
+
+template <class Function>
+int call(Function function) noexcept {
+    last_error[0] = '\0';
+    try {
+        function();
+        return 0;
+    } catch (const std::exception &error) {
+        std::snprintf(last_error, sizeof(last_error), "%s", error.what());
+    } catch (...) {
+        std::snprintf(last_error, sizeof(last_error), "unknown native error");
+    }
+    return -1;
+}
+
+using rs::check;
+using rs::require;
+
+// Owns one device allocation; frees it on every exit path.
+class DeviceBuffer {
+    void *data_ = nullptr;
+public:
+    explicit DeviceBuffer(size_t size) {
+        if (size) check(hipMalloc(&data_, size));
+    }
+    ~DeviceBuffer() {
+        if (data_) (void)hipFree(data_);
+    }
+    DeviceBuffer(const DeviceBuffer &) = delete;
+    DeviceBuffer &operator=(const DeviceBuffer &) = delete;
+    void *data() const { return data_; }
+    float *floats() const { return static_cast<float *>(data_); }
+};
+
+void upload(void *device, const void *host, size_t size) {
+    if (size) check(hipMemcpy(device, host, size, hipMemcpyHostToDevice));
+}
+void download(void *host, const void *device, size_t size) {
+    if (size) check(hipMemcpy(host, device, size, hipMemcpyDeviceToHost));
+}
+
+// Same checks and messages as src/runtime.cu:65-71.
+void batch_size(int batch) {
+    require(batch >= 1 && batch <= 8, "batch must be between 1 and 8");
+}
+void epsilon_value(float epsilon) {
+    require(std::isfinite(epsilon) && epsilon > 0, "epsilon must be finite and positive");
+}
+
+size_t align256(size_t n) { return (n + 255) & ~size_t(255); }
+
+bool aligned16(const void *p) { return (reinterpret_cast<uintptr_t>(p) & 15) == 0; }
+
+rs::Dtype dtype_of(int dtype) {
+    require(dtype == QV_F16 || dtype == QV_BF16, "dtype must be QV_F16 or QV_BF16");
+    return dtype == QV_BF16 ? rs::Dtype::BF16 : rs::Dtype::F16;
+}
+
+void geometry(int kv_heads, int head_dim, int capacity) {
+    require(kv_heads >= 1 && kv_heads <= 256, "kv_heads must be in 1..256");
+    require(head_dim == 128 || head_dim == 256, "head_dim must be 128 or 256");
+    require(capacity >= rs::kPageTokens && capacity % rs::kPageTokens == 0,
+            "capacity must be a positive multiple of 32 tokens");
+}
+
+rs::Shape attention_shape(int q_heads, int kv_heads, int head_dim, int tokens,
+                          int position, int capacity) {
+    require(kv_heads >= 1 && q_heads >= kv_heads && q_heads % kv_heads == 0,
+            "q_heads must be a positive multiple of kv_heads");
+    require(q_heads / kv_heads <= rs::kMaxRows, "at most 16 query heads per KV head");
+    require(head_dim == 128 || head_dim == 256, "head_dim must be 128 or 256");
+    require(tokens >= 1, "tokens must be positive");
+    require(position >= 0, "position must be non-negative");
+    return rs::Shape{q_heads, kv_heads, head_dim, tokens, position, capacity};
+}
+
+void fits_cache(const rs::Shape &s) {
+    geometry(s.kv_heads, s.head_dim, s.capacity);
+    require((long long)s.position + s.tokens <= s.capacity, "position+tokens exceeds the cache capacity");
+}
+
+// Run split + combine over token chunks of at most kMaxRows query rows per
+// KV head; every chunk reuses the workspace in stream order.
+void run_attention(const rs::Shape &s, rs::Dtype dtype, bool precise, float scale,
+                   const void *q, size_t q_elem, const void *k_pages, const void *v_pages,
+                   void *workspace, void *out, size_t out_elem, const float *gate,
+                   hipStream_t stream) {
+    const int ct = rs::chunk_tokens(s);
+    const size_t row = (size_t)s.q_heads * s.head_dim;
+    for (int t0 = 0; t0 < s.tokens; t0 += ct) {
+        rs::Shape c = s;
+        c.position = s.position + t0;
+        c.tokens = std::min(ct, s.tokens - t0);
+        const rs::SplitPlan plan = rs::plan_split(c, c.tokens, precise);
+        rs::launch_split(c, plan, dtype, precise, scale,
+                         static_cast<const char *>(q) + t0 * row * q_elem, k_pages, v_pages,
+                         workspace, stream);
+        rs::launch_combine(c, plan, dtype, workspace,
+                           static_cast<char *>(out) + t0 * row * out_elem,
+                           gate ? gate + (size_t)t0 * 2 * row : nullptr, stream);
+    }
+}
+
+[[noreturn]] void not_in_library(const char *name) {
+    char message[200];
+    std::snprintf(message, sizeof(message),
+                  "%s is not part of libredshift_hip, which implements the attention path only", name);
+    throw std::runtime_error(message);
+}
+
+}  // namespace
+
+extern "C" const char *qv_error(void) { return last_error; }
+
+extern "C" int qv_test_mm(float *, const void *, const float *, int, int, int, int) {
+    return call([] { not_in_library("qv_test_mm"); });
+}
+extern "C" int qv_test_mm_fast(float *, const void *, const float *, int, int, int, int) {
+    return call([] { not_in_library("qv_test_mm_fast"); });
+}
+extern "C" int qv_test_norm(float *, const float *, const float *, int, int, float) {
+    return call([] { not_in_library("qv_test_norm"); });
+}
+extern "C" int qv_test_delta(float *, float *, float *, const float *, const float *,
+                             const float *, const float *, const float *, const float *,
+                             const float *, const float *, int, int, int, int, float) {
+    return call([] { not_in_library("qv_test_delta"); });
+}
+
+extern "C" int qv_test_attention(float *out, void *key_cache, void *value_cache,
+                                 const float *q_gate, const float *key, const float *value,
+                                 const float *q_norm, const float *k_norm,
+                                 int batch, int position, float epsilon) {
+    return call([&] {
+        // Validation order of src/runtime.cu:172-176; nothing is read before it.
+        batch_size(batch);
+        epsilon_value(epsilon);
+        require(position >= 0 && position <= rs::kModelCapacity - batch,
+                "attention context exceeds 139264");
+        require(out && key_cache && value_cache && q_gate && key && value && q_norm && k_norm,
+                "null attention buffer");
+        constexpr int H = rs::kModelQHeads, HKV = rs::kModelKvHeads, D = rs::kModelHeadDim;
+        const int n = position + batch;
+        const int capacity = (n + rs::kPageTokens - 1) / rs::kPageTokens * rs::kPageTokens;
+        const rs::Shape shape{H, HKV, D, batch, position, capacity};
+        const size_t out_bytes = (size_t)batch * H * D * sizeof(float);
+        const size_t kv_bytes = (size_t)batch * HKV * D * sizeof(float);
+        const size_t row_bytes = (size_t)HKV * D * sizeof(uint16_t);
+        const size_t page_bytes = (size_t)HKV * capacity * D * sizeof(uint16_t);
+        DeviceBuffer k_pages(page_bytes), v_pages(page_bytes);
+        DeviceBuffer k_rows((size_t)n * row_bytes), v_rows((size_t)n * row_bytes);
+        DeviceBuffer qg(2 * out_bytes), k(kv_bytes), v(kv_bytes);
+        DeviceBuffer qn(D * sizeof(float)), kn(D * sizeof(float));
+        DeviceBuffer q(out_bytes), output(out_bytes);
+        DeviceBuffer workspace(rs::attention_workspace_bytes(shape, true));
+        hipStream_t stream = nullptr;
+        // Host -> device: only the prefix [0, position) of each cache.
+        upload(k_rows.data(), key_cache, (size_t)position * row_bytes);
+        upload(v_rows.data(), value_cache, (size_t)position * row_bytes);
+        upload(qg.data(), q_gate, 2 * out_bytes);
+        upload(k.data(), key, kv_bytes);
+        upload(v.data(), value, kv_bytes);
+        upload(qn.data(), q_norm, D * sizeof(float));
+        upload(kn.data(), k_norm, D * sizeof(float));
+        rs::launch_pack(k_pages.data(), v_pages.data(), k_rows.data(), v_rows.data(), HKV, D,
+                        capacity, 0, position, stream);
+        rs::launch_prepare(q.floats(), k_pages.data(), v_pages.data(), qg.floats(), k.floats(),
+                           v.floats(), qn.floats(), kn.floats(), batch, position, capacity,
+                           epsilon, stream);
+        run_attention(shape, rs::Dtype::F16, true, 1.0f / 16.0f, q.data(), sizeof(float),
+                      k_pages.data(), v_pages.data(), workspace.data(), output.data(),
+                      sizeof(float), qg.floats(), stream);
+        rs::launch_unpack(k_rows.data(), v_rows.data(), k_pages.data(), v_pages.data(), HKV, D,
+                          capacity, 0, n, stream);
+        check(hipGetLastError());
+        check(hipDeviceSynchronize());
+        // Device -> host: out and both whole caches [0, position+batch).
+        download(out, output.data(), out_bytes);
+        download(key_cache, k_rows.data(), (size_t)n * row_bytes);
+        download(value_cache, v_rows.data(), (size_t)n * row_bytes);
+    });
+}
+
+// ---- model session ABI: not part of this library ---------------------------
+extern "C" int qv_create(void **handle, const char *, int, float) {
+    return call([&] {
+        if (handle) *handle = nullptr;
+        not_in_library("qv_create (model session)");
+    });
+}
+extern "C" int qv_upload(void *, int, uint64_t, uint64_t) {
+    return call([] { not_in_library("qv_upload (model session)"); });
+}
+extern "C" int qv_evaluate(void *, const int *, int, float *) {
+    return call([] { not_in_library("qv_evaluate (model session)"); });
+}
+extern "C" int qv_verify(void *, const int *, int, float *) {
+    return call([] { not_in_library("qv_verify (model session)"); });
+}
+extern "C" int qv_commit(void *, int) {
+    return call([] { not_in_library("qv_commit (model session)"); });
+}
+extern "C" int qv_advance(void *, const int *, int, int *) {
+    return call([] { not_in_library("qv_advance (model session)"); });
+}
+extern "C" int qv_reset(void *) { return call([] { not_in_library("qv_reset (model session)"); }); }
+extern "C" int qv_checkpoint(void *) {
+    return call([] { not_in_library("qv_checkpoint (model session)"); });
+}
+extern "C" int qv_restore(void *) { return call([] { not_in_library("qv_restore (model session)"); }); }
+extern "C" int qv_position(void *, int *) {
+    return call([] { not_in_library("qv_position (model session)"); });
+}
+extern "C" void qv_destroy(void *) {}
+
+// ---- device ABI -----------------------------------------------------------
+extern "C" int qv_kv_bytes(uint64_t *bytes, int kv_heads, int head_dim, int capacity) {
+    return call([&] {
+        require(bytes != nullptr, "null bytes output");
+        geometry(kv_heads, head_dim, capacity);
+        *bytes = (uint64_t)kv_heads * capacity * head_dim * sizeof(uint16_t);
+    });
+}
+
+static void kv_convert_args(const void *k_pages, const void *v_pages, const void *k_rows,
+                            const void *v_rows, int kv_heads, int head_dim, int capacity,
+                            int first, int count) {
+    geometry(kv_heads, head_dim, capacity);
+    require(first >= 0 && count >= 0 && (long long)first + count <= capacity,
+            "token range outside the cache capacity");
+    require((k_pages && k_rows) || (v_pages && v_rows), "null KV buffer");
+    require(!k_pages == !k_rows && !v_pages == !v_rows, "each side needs both pages and rows");
+}
+
+extern "C" int qv_kv_pack(void *k_pages, void *v_pages, const void *k_rows, const void *v_rows,
+                          int kv_heads, int head_dim, int capacity, int first, int count,
+                          void *stream) {
+    return call([&] {
+        kv_convert_args(k_pages, v_pages, k_rows, v_rows, kv_heads, head_dim, capacity, first, count);
+        rs::launch_pack(k_pages, v_pages, k_rows, v_rows, kv_heads, head_dim, capacity, first,
+                        count, static_cast<hipStream_t>(stream));
+    });
+}
+
+extern "C" int qv_kv_unpack(void *k_rows, void *v_rows, const void *k_pages, const void *v_pages,
+                            int kv_heads, int head_dim, int capacity, int first, int count,
+                            void *stream) {
+    return call([&] {
+        kv_convert_args(k_pages, v_pages, k_rows, v_rows, kv_heads, head_dim, capacity, first, count);
+        rs::launch_unpack(k_rows, v_rows, k_pages, v_pages, kv_heads, head_dim, capacity, first,
+                          count, static_cast<hipStream_t>(stream));
+    });
+}
+
+extern "C" int qv_attention_workspace(uint64_t *bytes, int q_heads, int kv_heads, int head_dim,
+                                      int tokens, int position) {
+    return call([&] {
+        require(bytes != nullptr, "null bytes output");
+        const rs::Shape s = attention_shape(q_heads, kv_heads, head_dim, tokens, position, 0);
+        *bytes = rs::attention_workspace_bytes(s, false);
+    });
+}
+
+static void raw_buffers(const void *out, const void *q, const void *k_pages, const void *v_pages,
+                        const void *workspace) {
+    require(q && k_pages && v_pages && workspace && out, "null attention buffer");
+    require(aligned16(q) && aligned16(k_pages) && aligned16(v_pages) && aligned16(workspace) &&
+            aligned16(out), "attention buffers must be 16-byte aligned");
+}
+
+extern "C" int qv_attention(void *out, const void *q, const void *k_pages, const void *v_pages,
+                            int dtype, int q_heads, int kv_heads, int head_dim,
+                            int tokens, int position, int capacity, float scale,
+                            void *workspace, uint64_t workspace_bytes, void *stream) {
+    return call([&] {
+        const rs::Dtype dt = dtype_of(dtype);
+        const rs::Shape s = attention_shape(q_heads, kv_heads, head_dim, tokens, position, capacity);
+        fits_cache(s);
+        require(std::isfinite(scale), "scale must be finite");
+        raw_buffers(out, q, k_pages, v_pages, workspace);
+        require(workspace_bytes >= rs::attention_workspace_bytes(s, false), "workspace too small");
+        run_attention(s, dt, false, scale, q, 2, k_pages, v_pages, workspace, out, 2, nullptr,
+                      static_cast<hipStream_t>(stream));
+    });
+}
+
+extern "C" int qv_attention_split(const void *q, const void *k_pages, const void *v_pages,
+                                  int dtype, int q_heads, int kv_heads, int head_dim,
+                                  int tokens, int position, int capacity, float scale,
+                                  void *workspace, uint64_t workspace_bytes, void *stream) {
+    return call([&] {
+        const rs::Dtype dt = dtype_of(dtype);
+        const rs::Shape s = attention_shape(q_heads, kv_heads, head_dim, tokens, position, capacity);
+        fits_cache(s);
+        require(tokens <= rs::chunk_tokens(s), "qv_attention_split takes one chunk: group*tokens <= 16");
+        require(std::isfinite(scale), "scale must be finite");
+        raw_buffers(workspace, q, k_pages, v_pages, workspace);
+        const rs::SplitPlan plan = rs::plan_split(s, tokens, false);
+        require(workspace_bytes >= rs::plan_bytes(s, plan), "workspace too small");
+        rs::launch_split(s, plan, dt, false, scale, q, k_pages, v_pages, workspace,
+                         static_cast<hipStream_t>(stream));
+    });
+}
+
+extern "C" int qv_attention_combine(void *out, int dtype, int q_heads, int kv_heads, int head_dim,
+                                    int tokens, int position, const void *workspace,
+                                    uint64_t workspace_bytes, void *stream) {
+    return call([&] {
+        const rs::Dtype dt = dtype_of(dtype);
+        const rs::Shape s = attention_shape(q_heads, kv_heads, head_dim, tokens, position, 0);
+        require(tokens <= rs::chunk_tokens(s), "qv_attention_combine takes one chunk: group*tokens <= 16");
+        require(out && workspace, "null attention buffer");
+        require(aligned16(out) && aligned16(workspace), "attention buffers must be 16-byte aligned");
+        const rs::SplitPlan plan = rs::plan_split(s, tokens, false);
+        require(workspace_bytes >= rs::plan_bytes(s, plan), "workspace too small");
+        rs::launch_combine(s, plan, dt, workspace, out, nullptr, static_cast<hipStream_t>(stream));
+    });
+}
+
+static size_t fused_workspace(int batch, int position) {
+    constexpr int H = rs::kModelQHeads, HKV = rs::kModelKvHeads, D = rs::kModelHeadDim;
+    const rs::Shape s{H, HKV, D, batch, position, 0};
+    return align256((size_t)batch * H * D * sizeof(float)) + rs::attention_workspace_bytes(s, true);
+}
+
+extern "C" int qv_attention_fused_workspace(uint64_t *bytes, int batch, int position) {
+    return call([&] {
+        require(bytes != nullptr, "null bytes output");
+        batch_size(batch);
+        require(position >= 0 && position <= rs::kModelCapacity - batch,
+                "attention context exceeds 139264");
+        *bytes = fused_workspace(batch, position);
+    });
+}
+
+extern "C" int qv_attention_fused(float *out, void *k_pages, void *v_pages,
+                                  const float *q_gate, const float *key, const float *value,
+                                  const float *q_norm, const float *k_norm,
+                                  int batch, int position, int capacity, float epsilon,
+                                  void *workspace, uint64_t workspace_bytes, void *stream) {
+    return call([&] {
+        batch_size(batch);
+        epsilon_value(epsilon);
+        require(position >= 0 && position <= rs::kModelCapacity - batch,
+                "attention context exceeds 139264");
+        require(out && k_pages && v_pages && q_gate && key && value && q_norm && k_norm && workspace,
+                "null attention buffer");
+        constexpr int H = rs::kModelQHeads, HKV = rs::kModelKvHeads, D = rs::kModelHeadDim;
+        const rs::Shape s{H, HKV, D, batch, position, capacity};
+        fits_cache(s);
+        require(aligned16(q_gate) && aligned16(workspace) && aligned16(k_pages) && aligned16(v_pages),
+                "attention buffers must be 16-byte aligned");
+        require(workspace_bytes >= fused_workspace(batch, position), "workspace too small");
+        hipStream_t st = static_cast<hipStream_t>(stream);
+        float *q = static_cast<float *>(workspace);
+        void *partials = static_cast<char *>(workspace) + align256((size_t)batch * H * D * sizeof(float));
+        rs::launch_prepare(q, k_pages, v_pages, q_gate, key, value, q_norm, k_norm, batch, position,
+                           capacity, epsilon, st);
+        run_attention(s, rs::Dtype::F16, true, 1.0f / 16.0f, q, sizeof(float), k_pages, v_pages,
+                      partials, out, sizeof(float), q_gate, st);
+    });
+}

@@ -1,0 +1,68 @@
+// Host-side launchers shared by the C-ABI layer (abi.cpp) and the kernel
+// translation units.  All launches are asynchronous on the given stream.
+#pragma once
+#include "common.hpp"
+
+namespace rs {
+
+enum class Dtype { F16 = 1, BF16 = 2 };
+
+// Geometry of one raw attention call: `tokens` query tokens whose first token
+// sits at `position`; row t (0-based) sees keys 0 .. position + t.
+struct Shape {
+    int q_heads, kv_heads, head_dim, tokens, position, capacity;
+    int group() const { return q_heads / kv_heads; }
+    int n_keys() const { return position + tokens; }
+};
+
+// The split-K decomposition chosen for one launch of the partial kernel.
+struct SplitPlan {
+    int nqt;        // 16-row query tiles per KV head (rows = group * tokens)
+    int rows;       // valid query rows per KV head
+    int n_blocks;   // 32-key blocks per KV head
+    int splits;     // workgroups per KV head
+};
+
+// Largest number of query rows (group * tokens) per KV head that one launch of
+// the split kernel holds; longer token runs are processed in chunks.
+constexpr int kMaxRows = 16;
+
+int device_cu_count();
+SplitPlan plan_split(const Shape &s, int chunk_tokens, bool precise);
+// Tokens per chunk for a shape (chunk_tokens * group <= kMaxRows).
+int chunk_tokens(const Shape &s);
+// Workspace bytes for qv_attention on this shape (largest chunk).
+size_t attention_workspace_bytes(const Shape &s, bool precise);
+
+// Split-K partial kernel over the pages of every KV head.  q is 16-bit of
+// `dtype` ([tokens][q_heads][D]) or, when `precise`, float32.
+// Partial buffers of one plan: o [kv_heads][splits][rows][D], then m and l
+// [kv_heads][splits][2][rows], all float32.
+size_t plan_bytes(const Shape &s, const SplitPlan &p);
+void launch_split(const Shape &s, const SplitPlan &plan, Dtype dtype, bool precise,
+                  float scale, const void *q, const void *k_pages, const void *v_pages,
+                  void *workspace, hipStream_t stream);
+// Log-sum-exp combine of the partials into out.  Raw mode writes `dtype`
+// [tokens][q_heads][D]; fused mode (gate != nullptr) writes float32 and
+// multiplies by sigmoid(gate), gate being q_gate[t][h][D + d] (row stride 2D).
+void launch_combine(const Shape &s, const SplitPlan &plan, Dtype dtype,
+                    const void *workspace, void *out, const float *gate,
+                    hipStream_t stream);
+
+// Token-major rows [count][kv_heads][D] <-> pages, for tokens first..first+count.
+void launch_pack(void *k_pages, void *v_pages, const void *k_rows, const void *v_rows,
+                 int kv_heads, int head_dim, int capacity, int first, int count,
+                 hipStream_t stream);
+void launch_unpack(void *k_rows, void *v_rows, const void *k_pages, const void *v_pages,
+                   int kv_heads, int head_dim, int capacity, int first, int count,
+                   hipStream_t stream);
+
+// RMSNorm + RoPE of q and k, fp16 append of k and v into the pages at
+// position..position+batch-1 (the reference's attn_prepare semantics for the
+// fixed 24/4/256 model).  Writes the prepared q as float32 [batch][24][256].
+void launch_prepare(float *q, void *k_pages, void *v_pages, const float *q_gate,
+                    const float *key, const float *value, const float *q_norm,
+                    const float *k_norm, int batch, int position, int capacity,
+                    float epsilon, hipStream_t stream);
+
+}  // namespace rs

@@ -1,0 +1,127 @@
+// KV page maintenance: token-major <-> page conversion, and the fused prepare
+// step (RMSNorm + RoPE of q and k, fp16 append of k and v into the pages).
+#include "kernels.hpp"
+
+#include <cmath>
+
+namespace rs {
+namespace {
+
+// Elementwise move of 16-bit values between token-major rows
+// [count][kv_heads][D] (token first+t at row t) and the page layout.
+template <bool IS_V, bool TO_PAGES>
+__global__ __launch_bounds__(256)
+void convert_pages(unsigned short *pages, unsigned short *rows, int kv_heads, int D,
+                   size_t head_stride, int first, size_t total) {
+    for (size_t e = (size_t)blockIdx.x * blockDim.x + threadIdx.x; e < total;
+         e += (size_t)gridDim.x * blockDim.x) {
+        const int d = (int)(e % D);
+        const size_t th = e / D;
+        const int h = (int)(th % kv_heads);
+        const int token = first + (int)(th / kv_heads);
+        const size_t off = (size_t)h * head_stride +
+                           (IS_V ? v_page_offset(token, d, D) : k_page_offset(token, d, D));
+        if (TO_PAGES) pages[off] = rows[e];
+        else rows[e] = pages[off];
+    }
+}
+
+template <bool TO_PAGES>
+void convert(void *k_pages, void *v_pages, const void *k_rows, const void *v_rows,
+             int kv_heads, int head_dim, int capacity, int first, int count,
+             hipStream_t stream) {
+    const size_t total = (size_t)count * kv_heads * head_dim;
+    if (!total) return;
+    const size_t stride = (size_t)capacity * head_dim;
+    const unsigned blocks = (unsigned)std::min<size_t>((total + 255) / 256, 65536);
+    if (k_pages && k_rows) {
+        hipLaunchKernelGGL((convert_pages<false, TO_PAGES>), dim3(blocks), dim3(256), 0, stream,
+                           static_cast<unsigned short *>(k_pages),
+                           const_cast<unsigned short *>(static_cast<const unsigned short *>(k_rows)),
+                           kv_heads, head_dim, stride, first, total);
+        check(hipGetLastError());
+    }
+    if (v_pages && v_rows) {
+        hipLaunchKernelGGL((convert_pages<true, TO_PAGES>), dim3(blocks), dim3(256), 0, stream,
+                           static_cast<unsigned short *>(v_pages),
+                           const_cast<unsigned short *>(static_cast<const unsigned short *>(v_rows)),
+                           kv_heads, head_dim, stride, first, total);
+        check(hipGetLastError());
+    }
+}
+
+// One workgroup per (head, token): heads 0..23 are query heads, 24..27 the KV
+// heads (the reference's attn_prepare grid, src/kernels.cu:416-434).
+// RMSNorm over 256 dims with gamma, then rotate pairs (i, i+32), i < 32, by
+// (position+t) * 1e7^(-i/32).  The angle and its sine/cosine are evaluated in
+// double precision (the reference rounds the angle to fp32, which at position
+// 139,263 is off by up to 2^-7 rad); the rotation itself is fp32.
+__global__ __launch_bounds__(256)
+void prepare_kernel(float *q, _Float16 *k_pages, _Float16 *v_pages, const float *q_gate,
+                    const float *key, const float *value, const float *q_norm,
+                    const float *k_norm, int position, size_t head_stride, float epsilon) {
+    constexpr int D = kModelHeadDim, H = kModelQHeads, HKV = kModelKvHeads;
+    const int h = blockIdx.x, t = blockIdx.y, i = threadIdx.x;
+    const bool is_q = h < H;
+    const int kh = h - H;
+    const float *src = is_q ? q_gate + ((size_t)t * H + h) * 2 * D : key + ((size_t)t * HKV + kh) * D;
+    const float *gamma = is_q ? q_norm : k_norm;
+    __shared__ float row[D];
+    __shared__ float red[D / kWave];
+    const float x = src[i];
+    const float ss = wave_sum(x * x);
+    if ((i & (kWave - 1)) == 0) red[i / kWave] = ss;
+    __syncthreads();
+    float total = 0.f;
+#pragma unroll
+    for (int w = 0; w < D / kWave; ++w) total += red[w];
+    const float inv = rsqrtf(total / D + epsilon);
+    row[i] = x * inv * gamma[i];
+    __syncthreads();
+    if (i < 32) {
+        const double theta = (double)(position + t) * pow(10000000.0, -(double)i / 32.0);
+        double sd, cd;
+        sincos(theta, &sd, &cd);
+        const float c = (float)cd, s = (float)sd;
+        const float a = row[i], b = row[i + 32];
+        row[i] = a * c - b * s;
+        row[i + 32] = a * s + b * c;
+    }
+    __syncthreads();
+    if (is_q) {
+        q[((size_t)t * H + h) * D + i] = row[i];
+    } else {
+        const int token = position + t;
+        k_pages[(size_t)kh * head_stride + k_page_offset(token, i, D)] = (_Float16)row[i];
+        v_pages[(size_t)kh * head_stride + v_page_offset(token, i, D)] =
+            (_Float16)value[((size_t)t * HKV + kh) * D + i];
+    }
+}
+
+}  // namespace
+
+void launch_pack(void *k_pages, void *v_pages, const void *k_rows, const void *v_rows,
+                 int kv_heads, int head_dim, int capacity, int first, int count,
+                 hipStream_t stream) {
+    convert<true>(k_pages, v_pages, k_rows, v_rows, kv_heads, head_dim, capacity, first, count, stream);
+}
+
+void launch_unpack(void *k_rows, void *v_rows, const void *k_pages, const void *v_pages,
+                   int kv_heads, int head_dim, int capacity, int first, int count,
+                   hipStream_t stream) {
+    convert<false>(const_cast<void *>(k_pages), const_cast<void *>(v_pages), k_rows, v_rows,
+                   kv_heads, head_dim, capacity, first, count, stream);
+}
+
+void launch_prepare(float *q, void *k_pages, void *v_pages, const float *q_gate,
+                    const float *key, const float *value, const float *q_norm,
+                    const float *k_norm, int batch, int position, int capacity,
+                    float epsilon, hipStream_t stream) {
+    hipLaunchKernelGGL(prepare_kernel, dim3(kModelQHeads + kModelKvHeads, batch),
+                       dim3(kModelHeadDim), 0, stream, q, static_cast<_Float16 *>(k_pages),
+                       static_cast<_Float16 *>(v_pages), q_gate, key, value, q_norm, k_norm,
+                       position, (size_t)capacity * kModelHeadDim, epsilon);
+    check(hipGetLastError());
+}
+
+}  // namespace rs

@@ -1,0 +1,239 @@
+"""GPU parity tests of libredshift_hip against the CPU oracle.
+
+Ports of the reference's attention tests (tests/test_cuda.py:72-87,201-273)
+through the drop-in host-pointer entry qv_test_attention, with the same
+tolerances, and raw-core parity on the seeded workloads through the device
+ABI: max-abs <= 2e-3 and relative-L2 <= 1e-3 against the float64 oracle.
+"""
+import ctypes as ct
+
+import numpy as np
+import pytest
+
+from oracle import attention_ref as ref
+from oracle import kat
+from redshift_amd import attention as A
+from redshift_amd import layout
+from redshift_amd.workloads import WORKLOADS, Workload, make_inputs, to_float
+
+pytestmark = pytest.mark.gpu
+
+MAX_ABS, REL_L2 = 2e-3, 1e-3
+
+
+def ptr(a):
+    return a.ctypes.data_as(ct.c_void_p)
+
+
+def f32(a):
+    return np.ascontiguousarray(a, np.float32)
+
+
+def assert_close(actual, expected, tolerance):
+    """tests/test_cuda.py:65-70: |a - e| <= tol * (1 + |e|) and finite."""
+    actual = np.asarray(actual, np.float64).reshape(-1)
+    expected = np.asarray(expected, np.float64).reshape(-1)
+    assert actual.shape == expected.shape
+    assert np.all(np.isfinite(actual))
+    bad = np.abs(actual - expected) > tolerance * (1 + np.abs(expected))
+    assert not bad.any(), f'{bad.sum()} mismatches, first at {np.argmax(bad)}: ' \
+                          f'{actual[np.argmax(bad)]} vs {expected[np.argmax(bad)]}'
+
+
+def assert_parity(actual, expected, max_abs=MAX_ABS, rel_l2=REL_L2):
+    actual = np.asarray(actual, np.float64)
+    expected = np.asarray(expected, np.float64)
+    assert np.all(np.isfinite(actual))
+    err = np.abs(actual - expected).max()
+    rel = np.linalg.norm(actual - expected) / np.linalg.norm(expected)
+    assert err <= max_abs and rel <= rel_l2, (err, rel)
+
+
+def run_test_attention(lib, prefix_k, prefix_v, q_gate, key, value, q_norm, k_norm, batch, position, eps):
+    """Call qv_test_attention with host buffers; returns (out, kc, vc)."""
+    n = position + batch
+    kc = np.zeros(n * 1024, np.float16)
+    vc = np.zeros(n * 1024, np.float16)
+    kc[:position * 1024] = np.asarray(prefix_k, np.float16).reshape(-1)
+    vc[:position * 1024] = np.asarray(prefix_v, np.float16).reshape(-1)
+    out = np.zeros(batch * 6144, np.float32)
+    args = [f32(q_gate), f32(key), f32(value), f32(q_norm), f32(k_norm)]
+    rc = lib.qv_test_attention(ptr(out), ptr(kc), ptr(vc), *[ptr(a) for a in args], batch, position, eps)
+    assert rc == 0, lib.qv_error()
+    return out, kc, vc
+
+
+def test_attention_cpu_prefix_causality_and_chunking(lib, gpu):
+    """tests/test_cuda.py:201-235."""
+    c = kat.sine_wave_case()
+    batch, position = c['batch'], c['position']
+    expected = ref.fused_attention(c['key_cache'], c['value_cache'], c['q_gate'], c['key'], c['value'],
+                                   c['q_norm'], c['k_norm'], batch, position, c['epsilon'])
+    out, kc, vc = run_test_attention(lib, c['key_cache'], c['value_cache'], c['q_gate'], c['key'],
+                                     c['value'], c['q_norm'], c['k_norm'], batch, position, c['epsilon'])
+    assert_close(out, expected[0], 3e-4)
+    assert_close(kc, expected[1], 2e-3)
+    assert_close(vc, expected[2], 0)
+    np.testing.assert_array_equal(kc[:position * 1024].view(np.uint16),
+                                  c['key_cache'].reshape(-1).view(np.uint16))
+    # Sequential evaluation cannot see the later tokens in the chunk.
+    seq_k, seq_v = c['key_cache'], c['value_cache']
+    sequential = []
+    for t in range(batch):
+        row, seq_k, seq_v = run_test_attention(
+            lib, seq_k, seq_v, c['q_gate'][t], c['key'][t], c['value'][t], c['q_norm'], c['k_norm'],
+            1, position + t, c['epsilon'])
+        sequential.append(row)
+    assert_close(out, np.concatenate(sequential), 3e-5)
+    np.testing.assert_array_equal(kc.view(np.uint16), seq_k.view(np.uint16))
+    np.testing.assert_array_equal(vc.view(np.uint16), seq_v.view(np.uint16))
+
+
+@pytest.mark.parametrize('position,batch', [(2047, 3), (32767, 1), (139263, 1)])
+def test_attention_long_context_against_closed_form(lib, gpu, position, batch):
+    """tests/test_cuda.py:237-273 (position 139,263 + 1 = the 139,264 capacity)."""
+    c = kat.long_context_case(position, batch)
+    out, kc, vc = run_test_attention(lib, c['key_cache'], c['value_cache'], c['q_gate'], c['key'],
+                                     c['value'], c['q_norm'], c['k_norm'], batch, position, c['epsilon'])
+    assert_close(out, c['expected'], 3e-5)
+    n = position * 1024
+    np.testing.assert_array_equal(kc[:n].view(np.uint16), c['key_cache'].reshape(-1).view(np.uint16))
+    np.testing.assert_array_equal(vc[:n].view(np.uint16), c['value_cache'].reshape(-1).view(np.uint16))
+
+
+def test_error_is_cleared_after_a_successful_call(lib, gpu):
+    """tests/test_cuda.py:85-87."""
+    one = np.ones(1, np.float32)
+    assert lib.qv_test_attention(*([ptr(one)] * 8), 8, 139257, 1e-6) == -1
+    assert lib.qv_error()
+    c = kat.sine_wave_case(batch=1, position=0)
+    run_test_attention(lib, c['key_cache'], c['value_cache'], c['q_gate'], c['key'], c['value'],
+                       c['q_norm'], c['k_norm'], 1, 0, 1e-6)
+    assert lib.qv_error() == b''
+
+
+# ---- raw core on the paged cache ------------------------------------------
+
+def to_torch(x, dtype, torch):
+    if dtype == 'bf16':
+        return torch.from_numpy(np.ascontiguousarray(x).view(np.int16)).view(torch.bfloat16).cuda()
+    return torch.from_numpy(np.ascontiguousarray(x, np.float16)).cuda()
+
+
+def make_cache(k, v, w, torch, capacity=None, fill_nan=False):
+    dtype = torch.bfloat16 if w.dtype == 'bf16' else torch.float16
+    cache = A.PagedKV(w.kv_heads, w.head_dim, capacity or A.round_capacity(w.keys), dtype)
+    if fill_nan:
+        cache.k.fill_(float('nan'))
+        cache.v.fill_(float('nan'))
+    cache.pack(to_torch(k, w.dtype, torch), to_torch(v, w.dtype, torch))
+    return cache
+
+
+def gpu_attention(w, q, k, v, torch, **kw):
+    cache = make_cache(k, v, w, torch, **kw)
+    out = A.attention(to_torch(q, w.dtype, torch), cache, w.position, w.scale)
+    torch.cuda.synchronize()
+    return out.float().cpu().numpy().astype(np.float64)
+
+
+@pytest.mark.parametrize('name', ['decode_4k', 'verify8_16k', 'decode_139k'])
+def test_raw_attention_workloads(gpu, name):
+    w = WORKLOADS[name]
+    q, k, v, _ = make_inputs(w)
+    got = gpu_attention(w, q, k, v, gpu)
+    want = ref.gqa_attention(q, k, v, w.position, w.scale)
+    assert_parity(got, want)
+
+
+def test_raw_attention_cpu_plumbing_shape(gpu):
+    """8/2/128 on fp16-rounded inputs (the cache stores 16-bit values); the
+    oracle runs on exactly those rounded values."""
+    w = WORKLOADS['cpu_plumbing']
+    q, k, v, _ = make_inputs(w)
+    w16 = Workload(**{**w.__dict__, 'dtype': 'f16'})
+    q, k, v = (x.astype(np.float16) for x in (q, k, v))
+    assert_parity(gpu_attention(w16, q, k, v, gpu), ref.gqa_attention(q, k, v, w.position, w.scale))
+
+
+def test_raw_attention_prefill_shape_sampled_rows(gpu):
+    """2048 bf16 queries on 8192 keys; the oracle checks 24 sampled rows.
+    bf16 output rounding alone is ~1.6e-3 relative RMS, so the relative-L2
+    bound applies to the oracle rounded to bf16; max-abs uses the unrounded
+    oracle."""
+    w = WORKLOADS['prefill_2k']
+    q, k, v, _ = make_inputs(w)
+    got = gpu_attention(w, q, k, v, gpu)
+    rows = np.unique(np.concatenate([[0, 1, 2047], np.linspace(3, 2046, 21).astype(int)]))
+    want = ref.gqa_attention(to_float(q, 'bf16'), to_float(k, 'bf16'), to_float(v, 'bf16'),
+                             w.position, w.scale, rows=rows)
+    from redshift_amd.workloads import f32_to_bf16_bits
+    want_bf16 = to_float(f32_to_bf16_bits(want.astype(np.float32)), 'bf16')
+    assert np.abs(got[rows] - want).max() <= MAX_ABS
+    assert_parity(got[rows], want_bf16)
+
+
+@pytest.mark.parametrize('T,position', [(1, 0), (1, 31), (1, 32), (2, 30), (3, 5), (5, 1000),
+                                        (8, 0), (8, 4089), (7, 139257)])
+def test_raw_attention_edges_and_stale_pages(gpu, T, position):
+    """Ragged last page, first page, capacity boundary; pages past the last
+    key hold NaN, which must never reach the result."""
+    w = Workload('edge', 24, 4, 256, T, position, 1 / 16, 'f16', 100 + T, 1.0, 0.5)
+    q, k, v, _ = make_inputs(w)
+    got = gpu_attention(w, q, k, v, gpu, fill_nan=True)
+    assert_parity(got, ref.gqa_attention(q, k, v, w.position, w.scale))
+
+
+def test_raw_attention_grouped_equals_sequential(gpu):
+    w = Workload('group', 24, 4, 256, 8, 777, 1 / 16, 'f16', 9, 1.0, 0.5)
+    q, k, v, _ = make_inputs(w)
+    torch = gpu
+    cache = make_cache(k, v, w, torch)
+    qt = to_torch(q, 'f16', torch)
+    grouped = A.attention(qt, cache, w.position, w.scale).float()
+    sequential = torch.cat([A.attention(qt[t:t + 1], cache, w.position + t, w.scale).float()
+                            for t in range(w.tokens)])
+    torch.cuda.synchronize()
+    assert torch.allclose(grouped, sequential, atol=2e-3, rtol=0)
+    assert_parity(grouped.cpu().numpy(), ref.gqa_attention(q, k, v, w.position, w.scale))
+
+
+@pytest.mark.parametrize('head_dim', [128, 256])
+def test_pages_round_trip_bitwise(gpu, head_dim):
+    torch = gpu
+    rng = np.random.default_rng(head_dim)
+    n, capacity, heads = 77, 96, 3
+    bits = rng.integers(0, 1 << 16, size=(2, n, heads, head_dim), dtype=np.uint16)
+    k_rows = torch.from_numpy(bits[0].view(np.int16)).cuda().view(torch.float16)
+    v_rows = torch.from_numpy(bits[1].view(np.int16)).cuda().view(torch.float16)
+    cache = A.PagedKV(heads, head_dim, capacity, torch.float16)
+    cache.pack(k_rows[:40], v_rows[:40], first=0).pack(k_rows[40:], v_rows[40:], first=40)
+    k2, v2 = cache.unpack(0, n)
+    torch.cuda.synchronize()
+    np.testing.assert_array_equal(k2.view(torch.int16).cpu().numpy().view(np.uint16), bits[0])
+    np.testing.assert_array_equal(v2.view(torch.int16).cpu().numpy().view(np.uint16), bits[1])
+    # The pack kernel agrees with the host description of the layout.
+    pk = cache.k.view(torch.int16).cpu().numpy().view(np.uint16)
+    pv = cache.v.view(torch.int16).cpu().numpy().view(np.uint16)
+    off_k = layout.k_offsets(n, head_dim)
+    off_v = layout.v_offsets(n, head_dim)
+    for h in range(heads):
+        np.testing.assert_array_equal(pk[h * capacity * head_dim + off_k], bits[0][:, h, :])
+        np.testing.assert_array_equal(pv[h * capacity * head_dim + off_v], bits[1][:, h, :])
+
+
+def test_fused_device_path_matches_oracle(gpu):
+    torch = gpu
+    c = kat.sine_wave_case(batch=8, position=300)
+    position, batch = c['position'], c['batch']
+    expected = ref.fused_attention(c['key_cache'], c['value_cache'], c['q_gate'], c['key'], c['value'],
+                                   c['q_norm'], c['k_norm'], batch, position, c['epsilon'])
+    cache = A.PagedKV(4, 256, A.round_capacity(position + batch), torch.float16)
+    cache.pack(torch.from_numpy(c['key_cache']).cuda(), torch.from_numpy(c['value_cache']).cuda())
+    dev = [torch.from_numpy(f32(c[name])).cuda() for name in ('q_gate', 'key', 'value', 'q_norm', 'k_norm')]
+    out = A.attention_fused(*dev, cache, position, c['epsilon'])
+    kc, vc = cache.unpack(0, position + batch)
+    torch.cuda.synchronize()
+    assert_close(out.cpu().numpy(), expected[0], 3e-4)
+    assert_close(kc.float().cpu().numpy(), expected[1], 2e-3)
+    assert_close(vc.float().cpu().numpy(), expected[2], 0)

@@ -1,0 +1,147 @@
+"""C-ABI checks that need no GPU: the header compiles as C11 with -Werror and
+keeps the reference's prototypes (tests/test_native_abi.py:11-29 of the
+reference), the library exports every declared symbol, and argument
+validation rejects bad calls before any buffer is read or any HIP call is made
+(tests/test_cuda.py:72-87)."""
+import ctypes as ct
+import math
+import re
+import shutil
+import subprocess
+
+import pytest
+
+from redshift_amd.runtime import DEFAULT_LIBRARY, QV_BF16, QV_F16
+
+from conftest import ROOT
+
+HEADER = ROOT / 'include' / 'runtime.h'
+
+
+def declared_functions():
+    text = re.sub(r'/\*.*?\*/', '', HEADER.read_text(), flags=re.S)
+    return sorted(set(re.findall(r'\b(qv_\w+)\s*\(', text)))
+
+
+@pytest.mark.skipif(not shutil.which('cc'), reason='a C compiler is required')
+def test_public_header_is_usable_from_c(tmp_path):
+    source = '''
+#include "runtime.h"
+int main(void) {
+    const char *(*error)(void) = qv_error;
+    int (*mm)(float *, const void *, const float *, int, int, int, int) = qv_test_mm;
+    int (*norm)(float *, const float *, const float *, int, int, float) = qv_test_norm;
+    int (*verify)(void *, const int *, int, float *) = qv_verify;
+    int (*commit)(void *, int) = qv_commit;
+    int (*attention)(float *, void *, void *, const float *, const float *, const float *,
+                     const float *, const float *, int, int, float) = qv_test_attention;
+    int (*raw)(void *, const void *, const void *, const void *, int, int, int, int, int, int,
+               int, float, void *, uint64_t, void *) = qv_attention;
+    return error == 0 || mm == 0 || norm == 0 || verify == 0 || commit == 0 ||
+           attention == 0 || raw == 0;
+}
+'''
+    path = tmp_path / 'abi.c'
+    path.write_text(source)
+    result = subprocess.run(['cc', '-std=c11', '-Wall', '-Wextra', '-Werror', '-fsyntax-only',
+                             f'-I{HEADER.parent}', str(path)], capture_output=True, text=True)
+    assert result.returncode == 0, result.stderr
+
+
+def test_library_exports_every_declared_function(lib):
+    names = declared_functions()
+    assert 'qv_test_attention' in names and 'qv_attention' in names
+    for name in names:
+        assert hasattr(lib, name), name
+    # the reference loader's required set (qvelox/runtime.py:18-21)
+    for name in ('qv_error', 'qv_test_mm', 'qv_test_mm_fast', 'qv_test_norm', 'qv_test_delta',
+                 'qv_test_attention'):
+        assert hasattr(lib, name)
+
+
+def test_library_is_built_for_gfx950_only():
+    text = subprocess.run(['strings', str(DEFAULT_LIBRARY)], capture_output=True, text=True).stdout
+    targets = set(re.findall(r'amdgcn-amd-amdhsa--(gfx\w+)', text))
+    assert targets == {'gfx950'}, targets
+
+
+def floats(values):
+    return (ct.c_float * len(values))(*values)
+
+
+def test_rejects_invalid_attention_arguments_before_accessing_buffers(lib):
+    value = floats([1.])
+    # tests/test_cuda.py:85 of the reference: batch 8 at position 139257 overflows.
+    assert lib.qv_test_attention(*([value] * 8), 8, 139257, 1e-6) == -1
+    assert lib.qv_error() == b'attention context exceeds 139264'
+    for batch in (0, 9, -1):
+        assert lib.qv_test_attention(*([value] * 8), batch, 0, 1e-6) == -1
+        assert lib.qv_error() == b'batch must be between 1 and 8'
+    for epsilon in (0., -1., math.nan, math.inf):
+        assert lib.qv_test_attention(*([value] * 8), 1, 0, epsilon) == -1
+        assert lib.qv_error() == b'epsilon must be finite and positive'
+    assert lib.qv_test_attention(*([value] * 8), 1, -1, 1e-6) == -1
+    assert lib.qv_error() == b'attention context exceeds 139264'
+    for i in range(8):
+        args = [value] * 8
+        args[i] = None
+        assert lib.qv_test_attention(*args, 1, 0, 1e-6) == -1
+        assert lib.qv_error() == b'null attention buffer'
+    # batch is checked before epsilon, epsilon before position (src/runtime.cu:172-174)
+    assert lib.qv_test_attention(*([value] * 8), 9, 139264, math.nan) == -1
+    assert lib.qv_error() == b'batch must be between 1 and 8'
+    assert lib.qv_test_attention(*([value] * 8), 1, 139264, math.nan) == -1
+    assert lib.qv_error() == b'epsilon must be finite and positive'
+
+
+def test_out_of_path_entry_points_fail_with_a_message(lib):
+    value = floats([1.])
+    assert lib.qv_test_mm(value, value, value, 8, 1, 32, 1) == -1
+    assert b'not part of libredshift_hip' in lib.qv_error()
+    assert lib.qv_test_mm_fast(value, value, value, 8, 1, 32, 1) == -1
+    assert lib.qv_test_norm(value, value, value, 1, 1, 1e-6) == -1
+    assert lib.qv_test_delta(*([value] * 11), 1, 1, 1, 32, 1e-6) == -1
+    handle = ct.c_void_p(1234)
+    assert lib.qv_create(ct.byref(handle), b'model.gguf', 2048, 1e-6) == -1
+    assert handle.value is None
+    assert lib.qv_commit(None, 0) == -1 and lib.qv_error()
+    lib.qv_destroy(None)
+
+
+def test_kv_bytes_and_geometry_validation(lib):
+    size = ct.c_uint64()
+    assert lib.qv_kv_bytes(ct.byref(size), 4, 256, 139264) == 0
+    assert size.value == 4 * 139264 * 256 * 2
+    assert lib.qv_error() == b''
+    assert lib.qv_kv_bytes(ct.byref(size), 4, 256, 100) == -1
+    assert b'multiple of 32' in lib.qv_error()
+    assert lib.qv_kv_bytes(ct.byref(size), 4, 192, 128) == -1
+    assert b'head_dim' in lib.qv_error()
+    assert lib.qv_kv_bytes(None, 4, 256, 128) == -1
+
+
+def test_device_entry_points_validate_before_touching_the_device(lib):
+    p = ct.c_void_p(4096)   # never dereferenced: every call below fails validation
+    ws = ct.c_uint64(1 << 20)
+    args = dict(q_heads=24, kv_heads=4, head_dim=256, tokens=1, position=4095, capacity=4096)
+
+    def call(dtype=QV_F16, scale=0.0625, out=p, **kw):
+        a = {**args, **kw}
+        return lib.qv_attention(out, p, p, p, dtype, a['q_heads'], a['kv_heads'], a['head_dim'],
+                                a['tokens'], a['position'], a['capacity'], scale, p, ws, None)
+
+    assert call(dtype=7) == -1 and b'dtype' in lib.qv_error()
+    assert call(q_heads=25) == -1 and b'multiple of kv_heads' in lib.qv_error()
+    assert call(head_dim=64) == -1 and b'head_dim' in lib.qv_error()
+    assert call(tokens=0) == -1 and b'tokens' in lib.qv_error()
+    assert call(position=4096) == -1 and b'capacity' in lib.qv_error()
+    assert call(capacity=4100) == -1 and b'multiple of 32' in lib.qv_error()
+    assert call(scale=math.inf) == -1 and b'scale' in lib.qv_error()
+    assert call(out=None) == -1 and lib.qv_error() == b'null attention buffer'
+    assert call(out=ct.c_void_p(4098)) == -1 and b'aligned' in lib.qv_error()
+    assert call(dtype=QV_BF16, q_heads=24 * 17, kv_heads=1) == -1 and b'16 query heads' in lib.qv_error()
+    assert lib.qv_kv_pack(p, p, p, p, 4, 256, 128, 100, 29, None) == -1
+    assert b'capacity' in lib.qv_error()
+    assert lib.qv_kv_pack(p, None, None, p, 4, 256, 128, 0, 1, None) == -1
+    assert lib.qv_attention_fused(*([p] * 8), 9, 0, 128, 1e-6, p, ws, None) == -1
+    assert lib.qv_error() == b'batch must be between 1 and 8'
