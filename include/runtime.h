@@ -107,14 +107,14 @@ int qv_attention_workspace(uint64_t *bytes, int q_heads, int kv_heads, int head_
  * q_heads/kv_heads/head_dim/scale: out[t][h] = softmax_p(q[t][h] . k[p][h/G] *
  * scale, p <= position+t) . v[p][h/G], G = q_heads/kv_heads.
  * q, out: [tokens][q_heads][head_dim] of `dtype`; fp32 softmax and
- * accumulation. head_dim 128 or 256; G <= 16; 1 <= tokens;
+ * accumulation. head_dim 128 or 256; G <= 48; 1 <= tokens;
  * position+tokens <= capacity. Split-K over all CUs plus a log-sum-exp
  * combine; work = qv_attention_split then qv_attention_combine. */
 int qv_attention(void *out, const void *q, const void *k_pages, const void *v_pages,
                  int dtype, int q_heads, int kv_heads, int head_dim,
                  int tokens, int position, int capacity, float scale,
                  void *workspace, uint64_t workspace_bytes, void *stream);
-/* The two phases of qv_attention for one token chunk (G*tokens <= 16), for
+/* The two phases of qv_attention for one token chunk (G*tokens <= 48), for
  * callers that time or schedule them separately. */
 int qv_attention_split(const void *q, const void *k_pages, const void *v_pages,
                        int dtype, int q_heads, int kv_heads, int head_dim,

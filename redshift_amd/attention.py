@@ -11,7 +11,7 @@ from .runtime import QV_BF16, QV_F16, check, library
 
 PAGE_TOKENS = 32
 # Query rows (group * tokens) per KV head that one split/combine pair serves.
-MAX_CHUNK_ROWS = 16
+MAX_CHUNK_ROWS = 48
 
 
 def dtype_code(dtype):

@@ -84,7 +84,7 @@ rs::Shape attention_shape(int q_heads, int kv_heads, int head_dim, int tokens,
                           int position, int capacity) {
     require(kv_heads >= 1 && q_heads >= kv_heads && q_heads % kv_heads == 0,
             "q_heads must be a positive multiple of kv_heads");
-    require(q_heads / kv_heads <= rs::kMaxRows, "at most 16 query heads per KV head");
+    require(q_heads / kv_heads <= rs::kMaxRows, "at most 48 query heads per KV head");
     require(head_dim == 128 || head_dim == 256, "head_dim must be 128 or 256");
     require(tokens >= 1, "tokens must be positive");
     require(position >= 0, "position must be non-negative");
@@ -97,9 +97,10 @@ void fits_cache(const rs::Shape &s) {
 }
 
 // Run split + combine over token chunks of at most kMaxRows query rows per
-// KV head; every chunk reuses the workspace in stream order.
+// KV head; every chunk reuses the workspace in stream order.  q (and q_lo,
+// the lo part of a precise query) are 16-bit [tokens][q_heads][D].
 void run_attention(const rs::Shape &s, rs::Dtype dtype, bool precise, float scale,
-                   const void *q, size_t q_elem, const void *k_pages, const void *v_pages,
+                   const void *q, const void *q_lo, const void *k_pages, const void *v_pages,
                    void *workspace, void *out, size_t out_elem, const float *gate,
                    hipStream_t stream) {
     const int ct = rs::chunk_tokens(s);
@@ -108,10 +109,11 @@ void run_attention(const rs::Shape &s, rs::Dtype dtype, bool precise, float scal
         rs::Shape c = s;
         c.position = s.position + t0;
         c.tokens = std::min(ct, s.tokens - t0);
-        const rs::SplitPlan plan = rs::plan_split(c, c.tokens, precise);
-        rs::launch_split(c, plan, dtype, precise, scale,
-                         static_cast<const char *>(q) + t0 * row * q_elem, k_pages, v_pages,
-                         workspace, stream);
+        const rs::SplitPlan plan = rs::plan_split(c, c.tokens, dtype, precise);
+        const size_t q_offset = t0 * row * sizeof(uint16_t);
+        rs::launch_split(c, plan, dtype, precise, scale, static_cast<const char *>(q) + q_offset,
+                         q_lo ? static_cast<const char *>(q_lo) + q_offset : nullptr,
+                         k_pages, v_pages, workspace, stream);
         rs::launch_combine(c, plan, dtype, workspace,
                            static_cast<char *>(out) + t0 * row * out_elem,
                            gate ? gate + (size_t)t0 * 2 * row : nullptr, stream);
@@ -168,8 +170,8 @@ extern "C" int qv_test_attention(float *out, void *key_cache, void *value_cache,
         DeviceBuffer k_rows((size_t)n * row_bytes), v_rows((size_t)n * row_bytes);
         DeviceBuffer qg(2 * out_bytes), k(kv_bytes), v(kv_bytes);
         DeviceBuffer qn(D * sizeof(float)), kn(D * sizeof(float));
-        DeviceBuffer q(out_bytes), output(out_bytes);
-        DeviceBuffer workspace(rs::attention_workspace_bytes(shape, true));
+        DeviceBuffer q(out_bytes), output(out_bytes);   // q: hi and lo fp16 parts
+        DeviceBuffer workspace(rs::attention_workspace_bytes(shape, rs::Dtype::F16, true));
         hipStream_t stream = nullptr;
         // Host -> device: only the prefix [0, position) of each cache.
         upload(k_rows.data(), key_cache, (size_t)position * row_bytes);
@@ -181,10 +183,11 @@ extern "C" int qv_test_attention(float *out, void *key_cache, void *value_cache,
         upload(kn.data(), k_norm, D * sizeof(float));
         rs::launch_pack(k_pages.data(), v_pages.data(), k_rows.data(), v_rows.data(), HKV, D,
                         capacity, 0, position, stream);
-        rs::launch_prepare(q.floats(), k_pages.data(), v_pages.data(), qg.floats(), k.floats(),
+        rs::launch_prepare(q.data(), k_pages.data(), v_pages.data(), qg.floats(), k.floats(),
                            v.floats(), qn.floats(), kn.floats(), batch, position, capacity,
                            epsilon, stream);
-        run_attention(shape, rs::Dtype::F16, true, 1.0f / 16.0f, q.data(), sizeof(float),
+        run_attention(shape, rs::Dtype::F16, true, 1.0f / 16.0f, q.data(),
+                      static_cast<uint16_t *>(q.data()) + (size_t)batch * H * D,
                       k_pages.data(), v_pages.data(), workspace.data(), output.data(),
                       sizeof(float), qg.floats(), stream);
         rs::launch_unpack(k_rows.data(), v_rows.data(), k_pages.data(), v_pages.data(), HKV, D,
@@ -274,7 +277,9 @@ extern "C" int qv_attention_workspace(uint64_t *bytes, int q_heads, int kv_heads
     return call([&] {
         require(bytes != nullptr, "null bytes output");
         const rs::Shape s = attention_shape(q_heads, kv_heads, head_dim, tokens, position, 0);
-        *bytes = rs::attention_workspace_bytes(s, false);
+        // The bf16 kernels use the same partial layout and the same split count.
+        *bytes = std::max(rs::attention_workspace_bytes(s, rs::Dtype::F16, false),
+                          rs::attention_workspace_bytes(s, rs::Dtype::BF16, false));
     });
 }
 
@@ -295,8 +300,8 @@ extern "C" int qv_attention(void *out, const void *q, const void *k_pages, const
         fits_cache(s);
         require(std::isfinite(scale), "scale must be finite");
         raw_buffers(out, q, k_pages, v_pages, workspace);
-        require(workspace_bytes >= rs::attention_workspace_bytes(s, false), "workspace too small");
-        run_attention(s, dt, false, scale, q, 2, k_pages, v_pages, workspace, out, 2, nullptr,
+        require(workspace_bytes >= rs::attention_workspace_bytes(s, dt, false), "workspace too small");
+        run_attention(s, dt, false, scale, q, nullptr, k_pages, v_pages, workspace, out, 2, nullptr,
                       static_cast<hipStream_t>(stream));
     });
 }
@@ -309,12 +314,12 @@ extern "C" int qv_attention_split(const void *q, const void *k_pages, const void
         const rs::Dtype dt = dtype_of(dtype);
         const rs::Shape s = attention_shape(q_heads, kv_heads, head_dim, tokens, position, capacity);
         fits_cache(s);
-        require(tokens <= rs::chunk_tokens(s), "qv_attention_split takes one chunk: group*tokens <= 16");
+        require(tokens <= rs::chunk_tokens(s), "qv_attention_split takes one chunk: group*tokens <= 48");
         require(std::isfinite(scale), "scale must be finite");
         raw_buffers(workspace, q, k_pages, v_pages, workspace);
-        const rs::SplitPlan plan = rs::plan_split(s, tokens, false);
+        const rs::SplitPlan plan = rs::plan_split(s, tokens, dt, false);
         require(workspace_bytes >= rs::plan_bytes(s, plan), "workspace too small");
-        rs::launch_split(s, plan, dt, false, scale, q, k_pages, v_pages, workspace,
+        rs::launch_split(s, plan, dt, false, scale, q, nullptr, k_pages, v_pages, workspace,
                          static_cast<hipStream_t>(stream));
     });
 }
@@ -325,10 +330,10 @@ extern "C" int qv_attention_combine(void *out, int dtype, int q_heads, int kv_he
     return call([&] {
         const rs::Dtype dt = dtype_of(dtype);
         const rs::Shape s = attention_shape(q_heads, kv_heads, head_dim, tokens, position, 0);
-        require(tokens <= rs::chunk_tokens(s), "qv_attention_combine takes one chunk: group*tokens <= 16");
+        require(tokens <= rs::chunk_tokens(s), "qv_attention_combine takes one chunk: group*tokens <= 48");
         require(out && workspace, "null attention buffer");
         require(aligned16(out) && aligned16(workspace), "attention buffers must be 16-byte aligned");
-        const rs::SplitPlan plan = rs::plan_split(s, tokens, false);
+        const rs::SplitPlan plan = rs::plan_split(s, tokens, dt, false);
         require(workspace_bytes >= rs::plan_bytes(s, plan), "workspace too small");
         rs::launch_combine(s, plan, dt, workspace, out, nullptr, static_cast<hipStream_t>(stream));
     });
@@ -337,7 +342,7 @@ extern "C" int qv_attention_combine(void *out, int dtype, int q_heads, int kv_he
 static size_t fused_workspace(int batch, int position) {
     constexpr int H = rs::kModelQHeads, HKV = rs::kModelKvHeads, D = rs::kModelHeadDim;
     const rs::Shape s{H, HKV, D, batch, position, 0};
-    return align256((size_t)batch * H * D * sizeof(float)) + rs::attention_workspace_bytes(s, true);
+    return align256((size_t)batch * H * D * sizeof(float)) + rs::attention_workspace_bytes(s, rs::Dtype::F16, true);
 }
 
 extern "C" int qv_attention_fused_workspace(uint64_t *bytes, int batch, int position) {
@@ -369,11 +374,11 @@ extern "C" int qv_attention_fused(float *out, void *k_pages, void *v_pages,
                 "attention buffers must be 16-byte aligned");
         require(workspace_bytes >= fused_workspace(batch, position), "workspace too small");
         hipStream_t st = static_cast<hipStream_t>(stream);
-        float *q = static_cast<float *>(workspace);
+        uint16_t *q = static_cast<uint16_t *>(workspace);   // hi then lo fp16 parts
         void *partials = static_cast<char *>(workspace) + align256((size_t)batch * H * D * sizeof(float));
         rs::launch_prepare(q, k_pages, v_pages, q_gate, key, value, q_norm, k_norm, batch, position,
                            capacity, epsilon, st);
-        run_attention(s, rs::Dtype::F16, true, 1.0f / 16.0f, q, sizeof(float), k_pages, v_pages,
-                      partials, out, sizeof(float), q_gate, st);
+        run_attention(s, rs::Dtype::F16, true, 1.0f / 16.0f, q, q + (size_t)batch * H * D, k_pages,
+                      v_pages, partials, out, sizeof(float), q_gate, st);
     });
 }

@@ -1,4 +1,4 @@
-// GQA attention over the paged KV cache: split-K partial kernel (decode and
+// GQA attention over the paged KV cache: split-K partial kernels (decode and
 // speculative verification) and the log-sum-exp combine.
 //
 // Reference counterparts: attention / attention_tiled (src/kernels.cu:435-456,
@@ -12,12 +12,25 @@
 //   O^T[dim][row] += V^T[dim][key] P^T[key][row]
 // Online softmax (base-2, fp32) runs on the S^T accumulators in registers: the
 // C layout of S^T is already the B-operand layout of P^T for the next MFMA
-// (see the V page layout in common.hpp), so P never leaves the lane.
+// (see the V page layout in common.hpp).
+//
+// Two partial kernels share that arithmetic:
+//   attention_stream  one query tile (<= 16 rows, decode).  Every wave streams
+//                     its own run of pages with a private softmax state; the
+//                     four waves merge through LDS once at the end.
+//   attention_coop    up to four query tiles (<= 64 rows, verification).  The
+//                     four waves split each 64-key block by keys for Q.K^T and
+//                     by head dims for P.V, exchanging the block max and the P
+//                     fragments through LDS, so the 48-row accumulators are
+//                     spread over the waves instead of replicated.
 #include "kernels.hpp"
 
 #include <algorithm>
 #include <cmath>
+#include <cstdlib>
+#include <cstring>
 #include <mutex>
+#include <type_traits>
 #include <vector>
 
 namespace rs {
@@ -27,6 +40,12 @@ template <typename T> struct Vec8;
 template <> struct Vec8<_Float16> { using type = f16x8; };
 template <> struct Vec8<__bf16> { using type = bf16x8; };
 
+typedef _Float16 f16x4 __attribute__((ext_vector_type(4)));
+typedef __bf16 bf16x4 __attribute__((ext_vector_type(4)));
+template <typename T> struct Vec4;
+template <> struct Vec4<_Float16> { using type = f16x4; };
+template <> struct Vec4<__bf16> { using type = bf16x4; };
+
 __device__ __forceinline__ f32x4 mfma(f16x8 a, f16x8 b, f32x4 c) {
     return __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, c, 0, 0, 0);
 }
@@ -34,186 +53,185 @@ __device__ __forceinline__ f32x4 mfma(bf16x8 a, bf16x8 b, f32x4 c) {
     return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, 0, 0, 0);
 }
 
-constexpr int kWaves = 4;          // waves per workgroup of the split kernel
+constexpr int kWaves = 4;          // waves per workgroup of the partial kernels
 constexpr int kMaxSplits = 1024;   // bound on workgroups per KV head
+constexpr int kCoopWaves = 8;      // waves per workgroup of attention_coop
 
 struct SplitArgs {
-    const void *q;
+    const void *q;        // [tokens][q_heads][D] 16-bit (hi part when QSPLIT)
+    const void *q_lo;     // QSPLIT: lo part, same layout
     const void *k_pages;
     const void *v_pages;
     float *part_o;    // [kv_heads][splits][rows][D]   unnormalised, base-2 max m
     float *part_ml;   // [kv_heads][splits][2][rows]   m (log2 domain), then l
     size_t head_stride;
-    int q_heads, group, rows, position, n_keys, n_blocks, splits;
+    int q_heads, group, rows, position, n_keys, n_pages, splits;
     float scale_log2;
 };
 
-// One workgroup = kWaves waves = one (split, KV head).  The split's 32-key
-// blocks are shared out evenly over the waves; every wave keeps its own
-// online-softmax state for all rows and the waves merge through LDS at the end.
-// Keys past n_keys in the last page are masked (scores) and zeroed (values),
-// so stale page contents never reach the result.
-template <int D, int NQT, bool PRECISE, typename KV>
-__global__ __launch_bounds__(kWaves * kWave)
-void attention_split(SplitArgs a) {
+// Query fragments (B operand of S^T): fragment (i, qt, ks) of lane l holds
+// row 16*qt + l%16, dims 32*ks + 8*(l/16) .. +7 of the hi (i = 0) or lo (i = 1,
+// QSPLIT) part.  A fp32 query arrives split into hi + lo 16-bit parts; the two
+// MFMAs carry ~22 significant bits, which keeps the fused path at fp32
+// accuracy.  Rows past `rows` repeat the last row; their results are never
+// stored.
+//
+// Every workgroup needs every fragment, and all of them start at once, so the
+// loads are shared: wave w fetches fragments w, w+4, ... (issue), the kernel
+// then issues its first KV loads, and only afterwards waits for the query
+// (publish: vector-memory counters retire in issue order, so that wait does
+// not drain the KV loads) and hands the fragments over through LDS.
+template <int D, int NQT, bool QSPLIT, typename KV>
+struct QueryStage {
     using V8 = typename Vec8<KV>::type;
-    constexpr int KS = D / 32, DT = D / 16, NQ = PRECISE ? 2 : 1;
-    constexpr int QBYTES = NQ * NQT * KS * kWave * 16;
-    constexpr int OBYTES = NQT * DT * kWave * 16;
-    constexpr int SBYTES = QBYTES > OBYTES ? QBYTES : OBYTES;
-    __shared__ __attribute__((aligned(16))) unsigned char smem[SBYTES];
-    __shared__ float sml[kWaves][2][16 * NQT];
-    V8 *sq = reinterpret_cast<V8 *>(smem);          // [NQ][NQT][KS][64] query fragments
-    f32x4 *so = reinterpret_cast<f32x4 *>(smem);    // [NQT][DT][64] merge buffer (after loop)
+    static constexpr int KS = D / 32, NQ = QSPLIT ? 2 : 1, N = NQ * NQT * KS, PER = N / kWaves;
+    static_assert(N % kWaves == 0, "fragments divide evenly over the waves");
+    V8 part[PER];
+
+    __device__ __forceinline__ void issue(const SplitArgs &a, int h, int lane, int w) {
+#pragma unroll
+        for (int i = 0; i < PER; ++i) {
+            const int e = w + kWaves * i;
+            const int ks = e % KS, qt = (e / KS) % NQT, lo = e / (KS * NQT);
+            const int row = min(16 * qt + (lane & 15), a.rows - 1);
+            const int t = row / a.group, gg = row - t * a.group;
+            const KV *src = static_cast<const KV *>(lo ? a.q_lo : a.q) +
+                            ((size_t)t * a.q_heads + (size_t)h * a.group + gg) * D + 32 * ks + 8 * (lane >> 4);
+            part[i] = *reinterpret_cast<const V8 *>(src);
+        }
+    }
+    __device__ __forceinline__ void publish(V8 *sq, int lane, int w) const {
+#pragma unroll
+        for (int i = 0; i < PER; ++i) sq[(w + kWaves * i) * kWave + lane] = part[i];
+    }
+    // After an LDS barrier: all fragments into registers.
+    static __device__ __forceinline__ void gather(const V8 *sq, int lane, V8 (&qf)[NQ][NQT][KS]) {
+#pragma unroll
+        for (int i = 0; i < NQ; ++i)
+#pragma unroll
+            for (int qt = 0; qt < NQT; ++qt)
+#pragma unroll
+                for (int ks = 0; ks < KS; ++ks) qf[i][qt][ks] = sq[((i * NQT + qt) * KS + ks) * kWave + lane];
+    }
+};
+
+// Token held in slot j of a V^T operand by lane group g (see common.hpp).
+__device__ __forceinline__ int v_slot_token(int g, int j) {
+    return j < 4 ? 4 * g + j : 16 + 4 * g + j - 4;
+}
+
+// ---------------------------------------------------------------------------
+// attention_stream: one query tile; wave-private online softmax over a run of
+// pages, merged across the four waves through LDS at the end.  Keys past
+// n_keys in the last page are masked (scores) and zeroed (values), so stale
+// page contents never reach the result.
+// ---------------------------------------------------------------------------
+template <int D, bool QSPLIT, bool PSPLIT, typename KV>
+__global__ __launch_bounds__(kWaves * kWave)
+void attention_stream(SplitArgs a) {
+    using V8 = typename Vec8<KV>::type;
+    using QS = QueryStage<D, 1, QSPLIT, KV>;
+    constexpr int KS = D / 32, DT = D / 16, NQ = QSPLIT ? 2 : 1;
+    __shared__ f32x4 so[DT * kWave];       // merge buffer
+    __shared__ V8 sq[QS::N * kWave];       // query fragments
+    __shared__ float sml[kWaves][2][16];
 
     const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
     const int split = blockIdx.x, h = blockIdx.y;
+    QS qs;
+    qs.issue(a, h, lane, w);
 
-    // Query fragments in B-operand order: lane l of (qt, ks) holds row
-    // 16*qt + l%16, dims 32*ks + 8*(l/16) .. +7.  Rows past `rows` are zero.
-    for (int e = threadIdx.x; e < NQT * KS * kWave; e += kWaves * kWave) {
-        const int l = e & 63, ks = (e >> 6) % KS, qt = e / (KS * kWave);
-        const int row = 16 * qt + (l & 15), d0 = 32 * ks + 8 * (l >> 4);
-        V8 hi = {}, lo = {};
-        if (row < a.rows) {
-            const int t = row / a.group, g = row - t * a.group;
-            const size_t base = ((size_t)t * a.q_heads + (size_t)h * a.group + g) * D + d0;
-            if constexpr (PRECISE) {
-                // fp32 query as hi + lo 16-bit parts: the two MFMAs carry ~22
-                // significant bits, which keeps the fused path at fp32 accuracy.
-                const float4 *src = reinterpret_cast<const float4 *>(static_cast<const float *>(a.q) + base);
-                const float4 x0 = src[0], x1 = src[1];
-                const float x[8] = {x0.x, x0.y, x0.z, x0.w, x1.x, x1.y, x1.z, x1.w};
-#pragma unroll
-                for (int i = 0; i < 8; ++i) {
-                    hi[i] = (KV)x[i];
-                    lo[i] = (KV)(x[i] - (float)hi[i]);
-                }
-            } else {
-                hi = *reinterpret_cast<const V8 *>(static_cast<const KV *>(a.q) + base);
-            }
-        }
-        sq[e] = hi;
-        if constexpr (PRECISE) sq[NQT * KS * kWave + e] = lo;
-    }
-    __syncthreads();
-
-    const long long waves_total = (long long)a.splits * kWaves;
-    const long long wi = (long long)split * kWaves + w;
-    const int b0 = (int)(wi * a.n_blocks / waves_total);
-    const int b1 = (int)((wi + 1) * a.n_blocks / waves_total);
+    // Pages are dealt out round-robin over the waves of all splits of this
+    // head: step j of wave wi is page j*waves_total + wi, so waves running in
+    // step stream one contiguous stretch of the head.
+    const int waves_total = a.splits * kWaves;
+    const int wi = split * kWaves + w;
+    const int n_steps = wi < a.n_pages ? (a.n_pages - 1 - wi) / waves_total + 1 : 0;
     const KV *kh = static_cast<const KV *>(a.k_pages) + (size_t)h * a.head_stride + lane * 8;
     const KV *vh = static_cast<const KV *>(a.v_pages) + (size_t)h * a.head_stride + lane * 8;
+    const int limit = a.position + min(lane & 15, a.rows - 1) / a.group;   // last visible key
 
-    // Last visible key of each row this lane holds (row 16*qt + lane%16).
-    int limit[NQT];
+    f32x4 acc[DT];
 #pragma unroll
-    for (int qt = 0; qt < NQT; ++qt) {
-        const int row = min(16 * qt + (lane & 15), a.rows - 1);
-        limit[qt] = a.position + row / a.group;
-    }
+    for (int dt = 0; dt < DT; ++dt) acc[dt] = f32x4{0.f, 0.f, 0.f, 0.f};
+    float m = -INFINITY, l = 0.f;
 
-    f32x4 acc[NQT][DT];
-    float m[NQT], l[NQT];
-#pragma unroll
-    for (int qt = 0; qt < NQT; ++qt) {
-        m[qt] = -INFINITY;
-        l[qt] = 0.f;
-#pragma unroll
-        for (int dt = 0; dt < DT; ++dt) acc[qt][dt] = f32x4{0.f, 0.f, 0.f, 0.f};
-    }
-
+    V8 qf1[NQ][1][KS];
     V8 kb[2][KS];
-    if (b0 < b1) {
-        const KV *kp = kh + (size_t)b0 * 32 * D;
+    auto load_k = [&](int b) {
+        const KV *kp = kh + (size_t)b * 32 * D;
 #pragma unroll
         for (int tile = 0; tile < 2; ++tile)
 #pragma unroll
             for (int ks = 0; ks < KS; ++ks)
                 kb[tile][ks] = *reinterpret_cast<const V8 *>(kp + tile * 16 * D + ks * 512);
-    }
-
-    for (int b = b0; b < b1; ++b) {
-        // V of this block is in flight while the scores are computed.
+    };
+    // One page; with PREFETCH the next page's K is loaded into kb once the
+    // scores no longer need it.  The last page runs without it, so every
+    // path issues the same loads.
+    auto page = [&](int b, auto prefetch) {
+        // V of this page is in flight while the scores are computed.
         V8 vb[DT];
         const KV *vp = vh + (size_t)b * 32 * D;
 #pragma unroll
         for (int dt = 0; dt < DT; ++dt) vb[dt] = *reinterpret_cast<const V8 *>(vp + dt * 512);
 
-        f32x4 s[NQT][2];
-#pragma unroll
-        for (int qt = 0; qt < NQT; ++qt) s[qt][0] = s[qt][1] = f32x4{0.f, 0.f, 0.f, 0.f};
+        f32x4 s0 = {0.f, 0.f, 0.f, 0.f}, s1 = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
         for (int ks = 0; ks < KS; ++ks) {
-#pragma unroll
-            for (int qt = 0; qt < NQT; ++qt) {
-                const V8 qf = sq[(qt * KS + ks) * kWave + lane];
-                s[qt][0] = mfma(kb[0][ks], qf, s[qt][0]);
-                s[qt][1] = mfma(kb[1][ks], qf, s[qt][1]);
-                if constexpr (PRECISE) {
-                    const V8 ql = sq[((NQT + qt) * KS + ks) * kWave + lane];
-                    s[qt][0] = mfma(kb[0][ks], ql, s[qt][0]);
-                    s[qt][1] = mfma(kb[1][ks], ql, s[qt][1]);
-                }
+            s0 = mfma(kb[0][ks], qf1[0][0][ks], s0);
+            s1 = mfma(kb[1][ks], qf1[0][0][ks], s1);
+            if constexpr (QSPLIT) {
+                s0 = mfma(kb[0][ks], qf1[NQ - 1][0][ks], s0);
+                s1 = mfma(kb[1][ks], qf1[NQ - 1][0][ks], s1);
             }
         }
-        // K of the next block is in flight during the softmax and P.V.
-        if (b + 1 < b1) {
-            const KV *kp = kh + (size_t)(b + 1) * 32 * D;
-#pragma unroll
-            for (int tile = 0; tile < 2; ++tile)
-#pragma unroll
-                for (int ks = 0; ks < KS; ++ks)
-                    kb[tile][ks] = *reinterpret_cast<const V8 *>(kp + tile * 16 * D + ks * 512);
-        }
+        if constexpr (decltype(prefetch)::value) load_k(b + waves_total);
 
-        // Lane l holds keys b*32 + 16*tile + 4*(l/16) + r for r < 4.
+        // Lane l holds keys b*32 + 16*tile + 4*(l/16) + r, r < 4.
         const int key0 = b * 32 + 4 * (lane >> 4);
-        const bool edge = b * 32 + 31 > a.position;
-        V8 ph[NQT], pl[NQT];
+        float x[8];
 #pragma unroll
-        for (int qt = 0; qt < NQT; ++qt) {
-            float x[8];
-#pragma unroll
-            for (int j = 0; j < 8; ++j) x[j] = s[qt][j >> 2][j & 3] * a.scale_log2;
-            if (edge) {
-#pragma unroll
-                for (int j = 0; j < 8; ++j)
-                    if (key0 + 16 * (j >> 2) + (j & 3) > limit[qt]) x[j] = -INFINITY;
-            }
-            float bm = x[0];
-#pragma unroll
-            for (int j = 1; j < 8; ++j) bm = fmaxf(bm, x[j]);
-            bm = fmaxf(bm, __shfl_xor(bm, 16, kWave));
-            bm = fmaxf(bm, __shfl_xor(bm, 32, kWave));
-            const float mn = fmaxf(m[qt], bm);
-            const float mu = mn == -INFINITY ? 0.f : mn;   // fully masked so far
-            const float alpha = exp2f(m[qt] - mu);
-            m[qt] = mn;
-            float ps = 0.f;
-#pragma unroll
-            for (int j = 0; j < 8; ++j) {
-                const float e = exp2f(x[j] - mu);
-                const KV eh = (KV)e;
-                ph[qt][j] = eh;
-                if constexpr (PRECISE) {
-                    pl[qt][j] = (KV)(e - (float)eh);
-                    ps += e;
-                } else {
-                    ps += (float)eh;   // normalise by the weights actually applied
-                }
-            }
-            l[qt] = l[qt] * alpha + ps;
-#pragma unroll
-            for (int dt = 0; dt < DT; ++dt) acc[qt][dt] *= alpha;
+        for (int r = 0; r < 4; ++r) {
+            x[r] = s0[r] * a.scale_log2;
+            x[4 + r] = s1[r] * a.scale_log2;
         }
+        if (b * 32 + 31 > a.position) {
+#pragma unroll
+            for (int j = 0; j < 8; ++j)
+                if (key0 + 16 * (j >> 2) + (j & 3) > limit) x[j] = -INFINITY;
+        }
+        float bm = x[0];
+#pragma unroll
+        for (int j = 1; j < 8; ++j) bm = fmaxf(bm, x[j]);
+        bm = fmaxf(bm, __shfl_xor(bm, 16, kWave));
+        bm = fmaxf(bm, __shfl_xor(bm, 32, kWave));
+        const float mn = fmaxf(m, bm);
+        const float mu = mn == -INFINITY ? 0.f : mn;   // fully masked so far
+        const float alpha = exp2f(m - mu);
+        m = mn;
+        V8 ph, pl;
+        float ps = 0.f;
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+            const float e = exp2f(x[j] - mu);
+            const KV eh = (KV)e;
+            ph[j] = eh;
+            if constexpr (PSPLIT) {
+                pl[j] = (KV)(e - (float)eh);
+                ps += e;
+            } else {
+                ps += (float)eh;   // normalise by the weights actually applied
+            }
+        }
+        l = l * alpha + ps;
+#pragma unroll
+        for (int dt = 0; dt < DT; ++dt) acc[dt] *= alpha;
         if (b * 32 + 32 > a.n_keys) {
             // Zero V slots past the last key: 0 * (stale NaN) would poison O.
-            const int g = lane >> 4;
 #pragma unroll
             for (int j = 0; j < 8; ++j) {
-                const int token = b * 32 + (j < 4 ? 4 * g + j : 16 + 4 * g + j - 4);
-                if (token >= a.n_keys) {
+                if (b * 32 + v_slot_token(lane >> 4, j) >= a.n_keys) {
 #pragma unroll
                     for (int dt = 0; dt < DT; ++dt) vb[dt][j] = (KV)0.f;
                 }
@@ -221,65 +239,318 @@ void attention_split(SplitArgs a) {
         }
 #pragma unroll
         for (int dt = 0; dt < DT; ++dt) {
-#pragma unroll
-            for (int qt = 0; qt < NQT; ++qt) {
-                acc[qt][dt] = mfma(vb[dt], ph[qt], acc[qt][dt]);
-                if constexpr (PRECISE) acc[qt][dt] = mfma(vb[dt], pl[qt], acc[qt][dt]);
-            }
+            acc[dt] = mfma(vb[dt], ph, acc[dt]);
+            if constexpr (PSPLIT) acc[dt] = mfma(vb[dt], pl, acc[dt]);
         }
+    };
+
+    // The first K load is unconditional (a wave without pages re-reads the
+    // head's last page), so every wave issues it before waiting on the query.
+    load_k(min(wi, a.n_pages - 1));
+    qs.publish(sq, lane, w);
+    lds_barrier();
+    QS::gather(sq, lane, qf1);
+    if (n_steps > 0) {
+        for (int j = 0; j + 1 < n_steps; ++j) page(j * waves_total + wi, std::true_type{});
+        page((n_steps - 1) * waves_total + wi, std::false_type{});
     }
 
     // ---- merge the waves of this workgroup -------------------------------
-#pragma unroll
-    for (int qt = 0; qt < NQT; ++qt) {
-        l[qt] += __shfl_xor(l[qt], 16, kWave);
-        l[qt] += __shfl_xor(l[qt], 32, kWave);
-    }
+    l += __shfl_xor(l, 16, kWave);
+    l += __shfl_xor(l, 32, kWave);
     if (lane < 16) {
-#pragma unroll
-        for (int qt = 0; qt < NQT; ++qt) {
-            sml[w][0][16 * qt + lane] = m[qt];
-            sml[w][1][16 * qt + lane] = l[qt];
-        }
+        sml[w][0][lane] = m;
+        sml[w][1][lane] = l;
     }
-    __syncthreads();   // every wave is past the loop: smem may now hold `so`
+    lds_barrier();   // every wave is past the loop: smem may now hold `so`
     float *pml = a.part_ml + ((size_t)h * a.splits + split) * 2 * a.rows;
+    const int row = lane & 15;
+    float M = -INFINITY;
 #pragma unroll
-    for (int qt = 0; qt < NQT; ++qt) {
-        const int row = 16 * qt + (lane & 15);
-        float M = -INFINITY;
+    for (int ww = 0; ww < kWaves; ++ww) M = fmaxf(M, sml[ww][0][row]);
+    const float mu = M == -INFINITY ? 0.f : M;
+    const float f = exp2f(m - mu);
 #pragma unroll
-        for (int ww = 0; ww < kWaves; ++ww) M = fmaxf(M, sml[ww][0][row]);
-        const float mu = M == -INFINITY ? 0.f : M;
-        const float f = exp2f(m[qt] - mu);
+    for (int dt = 0; dt < DT; ++dt) acc[dt] *= f;
+    if (w == 0 && lane < 16 && row < a.rows) {
+        float L = 0.f;
 #pragma unroll
-        for (int dt = 0; dt < DT; ++dt) acc[qt][dt] *= f;
-        if (w == 0 && lane < 16 && row < a.rows) {
-            float L = 0.f;
-#pragma unroll
-            for (int ww = 0; ww < kWaves; ++ww) L += sml[ww][1][row] * exp2f(sml[ww][0][row] - mu);
-            pml[row] = M;
-            pml[a.rows + row] = L;
-        }
+        for (int ww = 0; ww < kWaves; ++ww) L += sml[ww][1][row] * exp2f(sml[ww][0][row] - mu);
+        pml[row] = M;
+        pml[a.rows + row] = L;
     }
     for (int step = 0; step < kWaves; ++step) {
         if (w == step) {
 #pragma unroll
-            for (int qt = 0; qt < NQT; ++qt)
-#pragma unroll
-                for (int dt = 0; dt < DT; ++dt) {
-                    f32x4 &dst = so[(qt * DT + dt) * kWave + lane];
-                    dst = step ? dst + acc[qt][dt] : acc[qt][dt];
-                }
+            for (int dt = 0; dt < DT; ++dt) {
+                f32x4 &dst = so[dt * kWave + lane];
+                dst = step ? dst + acc[dt] : acc[dt];
+            }
         }
-        __syncthreads();
+        lds_barrier();
     }
     // Row-major store of the merged partial: element (row, 4*d4 .. +3) is the
-    // f32x4 of lane (row%16) + 16*(d4%4) in fragment (row/16, d4/4).
+    // f32x4 of lane (row%16) + 16*(d4%4) in fragment d4/4.
     f32x4 *po = reinterpret_cast<f32x4 *>(a.part_o + ((size_t)h * a.splits + split) * a.rows * D);
     for (int e = threadIdx.x; e < a.rows * (D / 4); e += kWaves * kWave) {
-        const int row = e / (D / 4), d4 = e - row * (D / 4);
-        po[e] = so[((row >> 4) * DT + (d4 >> 2)) * kWave + (row & 15) + 16 * (d4 & 3)];
+        const int r = e / (D / 4), d4 = e - r * (D / 4);
+        po[e] = so[(d4 >> 2) * kWave + r + 16 * (d4 & 3)];
+    }
+}
+
+// ---------------------------------------------------------------------------
+// attention_coop: NQT query tiles (up to 48 rows), WAVES waves per workgroup.
+// A split owns a contiguous run of pages, walked WAVES/2 pages (a block of
+// 16*WAVES keys) per step:
+//   * wave w computes S^T for the 16 keys of tile w of the block, all rows;
+//   * the block max per row is exchanged through LDS; every wave derives the
+//     same running max, so all waves scale their P values alike;
+//   * wave w writes its P values into the shared P^T operands (LDS) and then
+//     computes O^T for head dims w*D/WAVES .. +D/WAVES-1, all rows.
+// Row sums add across waves without rescaling; no O merge is needed.
+//
+// Register budget (two waves per SIMD): the query fragments live in LDS and
+// are read per use; each wave holds its own accumulators (NQT * D/WAVES dims)
+// and two register sets of KV operands, so the next block's loads stay in
+// flight across both barriers of the current block.  All loads are issued
+// unconditionally (pages past the split are clamped and masked), so every path
+// through the loop issues the same loads.
+//
+// The running max moves lazily: only when a block max exceeds it by more than
+// kLazy (log2 units).  P = exp2(s - m) then stays below 2^kLazy, exact in fp16
+// and bf16, and the accumulator rescale is skipped (wave-uniform branch) for
+// most blocks.
+// ---------------------------------------------------------------------------
+constexpr float kLazy = 8.f;
+
+template <int D, int NQT, bool QSPLIT, bool PSPLIT, typename KV, int WAVES>
+__global__ __launch_bounds__(WAVES * kWave, 2)
+void attention_coop(SplitArgs a) {
+    using V8 = typename Vec8<KV>::type;
+    using V4 = typename Vec4<KV>::type;
+    constexpr int KS = D / 32, NQ = QSPLIT ? 2 : 1, NP = PSPLIT ? 2 : 1;
+    constexpr int PAGES = WAVES / 2;              // pages per block
+    constexpr int DTW = D / (16 * WAVES);         // head-dim tiles per wave in P.V
+    constexpr int NQF = NQ * NQT * KS;            // query fragments
+    constexpr int QPW = (NQF + WAVES - 1) / WAVES;   // query fragments per wave
+    static_assert(DTW >= 1, "each wave owns at least one 16-dim tile");
+    __shared__ V8 sq[NQF * kWave];                // query fragments
+    __shared__ V8 sp[NP][PAGES][NQT][kWave];      // P^T operands of the block's pages
+    __shared__ float smax[WAVES][16 * NQT];       // per-wave block max per row
+    __shared__ float sl[WAVES][16 * NQT];         // row sums, exchanged once at the end
+
+    const int lane = threadIdx.x & 63, w = threadIdx.x >> 6, g = lane >> 4;
+    const int split = blockIdx.x, h = blockIdx.y;
+
+    // Query fragments: wave w fetches fragments w, w+WAVES, ... and the
+    // workgroup shares them through LDS.  This happens before any KV load:
+    // once the KV loads of every workgroup are queued in the memory system, a
+    // query line requested behind them waits for the whole flood.
+#pragma unroll
+    for (int i = 0; i < QPW; ++i) {
+        const int e = min(w + WAVES * i, NQF - 1);
+        const int ks = e % KS, qt = (e / KS) % NQT, lo = e / (KS * NQT);
+        const int row = min(16 * qt + (lane & 15), a.rows - 1);   // padded rows repeat the last
+        const int t = row / a.group, gg = row - t * a.group;
+        const V8 frag = *reinterpret_cast<const V8 *>(static_cast<const KV *>(lo ? a.q_lo : a.q) +
+                                                      ((size_t)t * a.q_heads + (size_t)h * a.group + gg) * D +
+                                                      32 * ks + 8 * g);
+        if (w + WAVES * i < NQF) sq[(w + WAVES * i) * kWave + lane] = frag;
+    }
+
+    const int p0 = (int)((long long)split * a.n_pages / a.splits);
+    const int p1 = (int)((long long)(split + 1) * a.n_pages / a.splits);
+    const int n_steps = (p1 - p0 + PAGES - 1) / PAGES;
+    const KV *kh = static_cast<const KV *>(a.k_pages) + (size_t)h * a.head_stride + lane * 8;
+    const KV *vh = static_cast<const KV *>(a.v_pages) + (size_t)h * a.head_stride + lane * 8;
+
+    int limit[NQT];   // last visible key of row 16*qt + lane%16
+#pragma unroll
+    for (int qt = 0; qt < NQT; ++qt)
+        limit[qt] = a.position + min(16 * qt + (lane & 15), a.rows - 1) / a.group;
+
+    f32x4 acc[NQT][DTW];
+    float m[NQT], l[NQT];
+#pragma unroll
+    for (int qt = 0; qt < NQT; ++qt) {
+        m[qt] = -INFINITY;
+        l[qt] = 0.f;
+#pragma unroll
+        for (int d = 0; d < DTW; ++d) acc[qt][d] = f32x4{0.f, 0.f, 0.f, 0.f};
+    }
+
+    struct Block {
+        V8 k[KS];             // this wave's 16-key tile (A operand of S^T)
+        V8 v[PAGES][DTW];     // this wave's head dims of every page (A operand of O^T)
+    };
+    auto load_block = [&](int step, Block &B) {
+        step = min(step, n_steps - 1);
+        const int page = min(p0 + step * PAGES + (w >> 1), p1 - 1);
+        const KV *kp = kh + (size_t)page * 32 * D + (w & 1) * 16 * D;
+#pragma unroll
+        for (int ks = 0; ks < KS; ++ks) B.k[ks] = *reinterpret_cast<const V8 *>(kp + ks * 512);
+#pragma unroll
+        for (int kk = 0; kk < PAGES; ++kk) {
+            const int pg = min(p0 + step * PAGES + kk, p1 - 1);
+            const KV *vp = vh + (size_t)pg * 32 * D + w * DTW * 512;
+#pragma unroll
+            for (int d = 0; d < DTW; ++d) B.v[kk][d] = *reinterpret_cast<const V8 *>(vp + d * 512);
+        }
+    };
+
+    auto process = [&](int step, Block &cur) {
+        const int pb = p0 + step * PAGES;                         // first page of the block
+        // ---- S^T for this wave's 16 keys, all rows ----
+        f32x4 s[NQT];
+#pragma unroll
+        for (int qt = 0; qt < NQT; ++qt) s[qt] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int ks = 0; ks < KS; ++ks) {
+#pragma unroll
+            for (int qt = 0; qt < NQT; ++qt) {
+                s[qt] = mfma(cur.k[ks], sq[(qt * KS + ks) * kWave + lane], s[qt]);
+                if constexpr (QSPLIT) s[qt] = mfma(cur.k[ks], sq[((NQT + qt) * KS + ks) * kWave + lane], s[qt]);
+            }
+        }
+        // Keys of register r: key0 + r.  Edge blocks (past the split, or
+        // holding keys past some row's limit) are masked; others only scaled.
+        const int page = pb + (w >> 1);
+        const int key0 = page * 32 + 16 * (w & 1) + 4 * g;
+        const bool edge = pb + PAGES > p1 || (pb + PAGES) * 32 - 1 > a.position;
+        float x[NQT][4];
+#pragma unroll
+        for (int qt = 0; qt < NQT; ++qt) {
+#pragma unroll
+            for (int r = 0; r < 4; ++r) x[qt][r] = s[qt][r] * a.scale_log2;
+            if (edge) {
+#pragma unroll
+                for (int r = 0; r < 4; ++r)
+                    if (page >= p1 || key0 + r > limit[qt]) x[qt][r] = -INFINITY;
+            }
+            float wm = fmaxf(fmaxf(x[qt][0], x[qt][1]), fmaxf(x[qt][2], x[qt][3]));
+            wm = fmaxf(wm, __shfl_xor(wm, 16, kWave));
+            wm = fmaxf(wm, __shfl_xor(wm, 32, kWave));
+            if (lane < 16) smax[w][16 * qt + lane] = wm;
+        }
+        lds_barrier();   // (1) block maxima visible
+
+        float alpha[NQT];
+        bool rescale = false;
+#pragma unroll
+        for (int qt = 0; qt < NQT; ++qt) {
+            const int row = 16 * qt + (lane & 15);
+            float bm = smax[0][row];
+#pragma unroll
+            for (int ww = 1; ww < WAVES; ++ww) bm = fmaxf(bm, smax[ww][row]);
+            alpha[qt] = 1.f;
+            if (bm > m[qt] + kLazy) {   // also the first finite block max of a row
+                alpha[qt] = __builtin_amdgcn_exp2f(m[qt] - bm);
+                m[qt] = bm;
+                rescale = true;
+            }
+            const float mu = m[qt] == -INFINITY ? 0.f : m[qt];   // fully masked so far
+            V4 ph, pl;
+            float ps = 0.f;
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                const float e = __builtin_amdgcn_exp2f(x[qt][r] - mu);
+                const KV eh = (KV)e;
+                ph[r] = eh;
+                if constexpr (PSPLIT) {
+                    pl[r] = (KV)(e - (float)eh);
+                    ps += e;
+                } else {
+                    ps += (float)eh;   // normalise by the weights actually applied
+                }
+            }
+            l[qt] = l[qt] * alpha[qt] + ps;
+            // Slots 4*(w%2) .. +3 of the P^T operand of page w/2 hold these keys.
+            *reinterpret_cast<V4 *>(reinterpret_cast<KV *>(&sp[0][w >> 1][qt][lane]) + 4 * (w & 1)) = ph;
+            if constexpr (PSPLIT)
+                *reinterpret_cast<V4 *>(reinterpret_cast<KV *>(&sp[NP - 1][w >> 1][qt][lane]) + 4 * (w & 1)) = pl;
+        }
+        lds_barrier();   // (2) P^T operands visible
+
+        // ---- O^T for this wave's head dims, all rows ----
+        if (__any(rescale)) {
+#pragma unroll
+            for (int qt = 0; qt < NQT; ++qt)
+#pragma unroll
+                for (int d = 0; d < DTW; ++d) acc[qt][d] *= alpha[qt];
+        }
+        if ((pb + PAGES) * 32 > a.n_keys || pb + PAGES > p1) {
+            // Zero V slots of keys past the last key or pages past the split
+            // (stale or re-read data): 0 * (stale NaN) would poison O.
+#pragma unroll
+            for (int kk = 0; kk < PAGES; ++kk)
+#pragma unroll
+                for (int j = 0; j < 8; ++j)
+                    if (pb + kk >= p1 || (pb + kk) * 32 + v_slot_token(g, j) >= a.n_keys) {
+#pragma unroll
+                        for (int d = 0; d < DTW; ++d) cur.v[kk][d][j] = (KV)0.f;
+                    }
+        }
+#pragma unroll
+        for (int kk = 0; kk < PAGES; ++kk) {
+#pragma unroll
+            for (int qt = 0; qt < NQT; ++qt) {
+                const V8 pf = sp[0][kk][qt][lane];
+#pragma unroll
+                for (int d = 0; d < DTW; ++d) acc[qt][d] = mfma(cur.v[kk][d], pf, acc[qt][d]);
+                if constexpr (PSPLIT) {
+                    const V8 pfl = sp[NP - 1][kk][qt][lane];
+#pragma unroll
+                    for (int d = 0; d < DTW; ++d) acc[qt][d] = mfma(cur.v[kk][d], pfl, acc[qt][d]);
+                }
+            }
+        }
+    };
+
+    // The first two blocks are requested together; afterwards a register set
+    // is refilled as soon as its block has been consumed, so the memory system
+    // always holds the next block of every workgroup.  The step count is the
+    // same for every wave of the workgroup, so the (uniform) breaks keep all
+    // waves at the same barriers.
+    lds_barrier();   // query fragments visible
+    if (n_steps > 0) {
+        Block S0, S1;
+        load_block(0, S0);
+        load_block(1, S1);
+        for (int j = 0;; j += 2) {
+            process(j, S0);
+            if (j + 1 >= n_steps) break;
+            load_block(j + 2, S0);
+            process(j + 1, S1);
+            if (j + 2 >= n_steps) break;
+            load_block(j + 3, S1);
+        }
+    }
+
+    // ---- partial results: O rows (this wave's dims), m and l ----
+#pragma unroll
+    for (int qt = 0; qt < NQT; ++qt) {
+        l[qt] += __shfl_xor(l[qt], 16, kWave);
+        l[qt] += __shfl_xor(l[qt], 32, kWave);
+        if (lane < 16) sl[w][16 * qt + lane] = l[qt];
+    }
+    lds_barrier();
+    float *pml = a.part_ml + ((size_t)h * a.splits + split) * 2 * a.rows;
+    float *po = a.part_o + ((size_t)h * a.splits + split) * a.rows * D;
+#pragma unroll
+    for (int qt = 0; qt < NQT; ++qt) {
+        const int row = 16 * qt + (lane & 15);
+        if (row < a.rows) {
+            if (w == 0 && lane < 16) {
+                float L = 0.f;
+#pragma unroll
+                for (int ww = 0; ww < WAVES; ++ww) L += sl[ww][row];
+                pml[row] = m[qt];
+                pml[a.rows + row] = L;
+            }
+#pragma unroll
+            for (int d = 0; d < DTW; ++d)
+                *reinterpret_cast<f32x4 *>(po + (size_t)row * D + (w * DTW + d) * 16 + 4 * g) = acc[qt][d];
+        }
     }
 }
 
@@ -290,29 +561,31 @@ struct CombineArgs {
     int q_heads, group, rows, splits;
 };
 
-// One workgroup per (row, KV head), one thread per head dim.
+// One workgroup (4 waves) per (row, KV head).  Lane l owns head dims
+// DV*l .. DV*l+DV-1 (DV = D/64); wave w sums splits w, w+4, w+8, ... with eight
+// independent loads in flight per batch; the waves reduce through LDS.
 template <int D, typename KV, bool FUSED>
-__global__ __launch_bounds__(D)
+__global__ __launch_bounds__(kWaves * kWave)
 void attention_combine(CombineArgs c) {
-    constexpr int NW = D / kWave;
+    constexpr int DV = D / kWave;
+    constexpr int kBatch = 8;
     __shared__ float wts[kMaxSplits];
-    __shared__ float red[NW];
+    __shared__ float red[kWaves];
+    __shared__ float part[kWaves - 1][D];
     const int row = blockIdx.x, h = blockIdx.y, tid = threadIdx.x;
     const int lane = tid & 63, w = tid >> 6;
     const float *ml = c.part_ml + (size_t)h * c.splits * 2 * c.rows;
 
     float M = -INFINITY;
-    for (int s = tid; s < c.splits; s += D) M = fmaxf(M, ml[(size_t)s * 2 * c.rows + row]);
+    for (int s = tid; s < c.splits; s += kWaves * kWave) M = fmaxf(M, ml[(size_t)s * 2 * c.rows + row]);
     M = wave_max(M);
     if (lane == 0) red[w] = M;
     __syncthreads();
-    M = red[0];
-#pragma unroll
-    for (int i = 1; i < NW; ++i) M = fmaxf(M, red[i]);
+    M = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
     __syncthreads();
     const float mu = M == -INFINITY ? 0.f : M;
     float L = 0.f;
-    for (int s = tid; s < c.splits; s += D) {
+    for (int s = tid; s < c.splits; s += kWaves * kWave) {
         const float wgt = exp2f(ml[(size_t)s * 2 * c.rows + row] - mu);
         wts[s] = wgt;
         L += wgt * ml[(size_t)s * 2 * c.rows + c.rows + row];
@@ -320,48 +593,89 @@ void attention_combine(CombineArgs c) {
     L = wave_sum(L);
     if (lane == 0) red[w] = L;
     __syncthreads();
-    L = 0.f;
-#pragma unroll
-    for (int i = 0; i < NW; ++i) L += red[i];
+    L = red[0] + red[1] + red[2] + red[3];
 
-    const float *po = c.part_o + ((size_t)h * c.splits * c.rows + row) * D + tid;
+    const float *po = c.part_o + ((size_t)h * c.splits * c.rows + row) * D + lane * DV;
     const size_t stride = (size_t)c.rows * D;
-    float acc = 0.f;
-    int s = 0;
-    for (; s + 4 <= c.splits; s += 4) {
-        const float v0 = po[(size_t)s * stride], v1 = po[(size_t)(s + 1) * stride];
-        const float v2 = po[(size_t)(s + 2) * stride], v3 = po[(size_t)(s + 3) * stride];
-        acc += wts[s] * v0 + wts[s + 1] * v1 + wts[s + 2] * v2 + wts[s + 3] * v3;
+    float acc[DV] = {};
+    for (int s0 = w; s0 < c.splits; s0 += kWaves * kBatch) {
+        float v[kBatch][DV];
+#pragma unroll
+        for (int i = 0; i < kBatch; ++i) {
+            const int s = s0 + i * kWaves;
+#pragma unroll
+            for (int d = 0; d < DV; ++d) v[i][d] = s < c.splits ? po[(size_t)s * stride + d] : 0.f;
+        }
+#pragma unroll
+        for (int i = 0; i < kBatch; ++i) {
+            const int s = s0 + i * kWaves;
+            const float wgt = s < c.splits ? wts[s] : 0.f;
+#pragma unroll
+            for (int d = 0; d < DV; ++d) acc[d] += wgt * v[i][d];
+        }
     }
-    for (; s < c.splits; ++s) acc += wts[s] * po[(size_t)s * stride];
-    const float o = acc / L;
-    const int t = row / c.group, hq = h * c.group + (row - t * c.group);
-    const size_t idx = ((size_t)t * c.q_heads + hq) * D + tid;
-    if constexpr (FUSED) {
-        const float g = c.gate[((size_t)t * c.q_heads + hq) * 2 * D + D + tid];
-        static_cast<float *>(c.out)[idx] = o * (1.f / (1.f + expf(-g)));
-    } else {
-        static_cast<KV *>(c.out)[idx] = (KV)o;
+    if (w > 0) {
+#pragma unroll
+        for (int d = 0; d < DV; ++d) part[w - 1][lane * DV + d] = acc[d];
+    }
+    __syncthreads();
+    if (w == 0) {
+        const int t = row / c.group, hq = h * c.group + (row - t * c.group);
+        const size_t idx = ((size_t)t * c.q_heads + hq) * D + lane * DV;
+#pragma unroll
+        for (int d = 0; d < DV; ++d) {
+            const float o = (acc[d] + part[0][lane * DV + d] + part[1][lane * DV + d] +
+                             part[2][lane * DV + d]) / L;
+            if constexpr (FUSED) {
+                const float gv = c.gate[((size_t)t * c.q_heads + hq) * 2 * D + D + lane * DV + d];
+                static_cast<float *>(c.out)[idx + d] = o * (1.f / (1.f + expf(-gv)));
+            } else {
+                static_cast<KV *>(c.out)[idx + d] = (KV)o;
+            }
+        }
     }
 }
 
-template <int D, int NQT, bool PRECISE, typename KV>
-const void *split_symbol() {
-    return reinterpret_cast<const void *>(&attention_split<D, NQT, PRECISE, KV>);
+// Kernel instance for a plan.  Raw fp16: 16-bit P; raw bf16: hi+lo P (bf16's
+// 8-bit significand would otherwise dominate the error); fused (fp32 q):
+// hi+lo q and hi+lo P.
+template <int D, int NQT>
+const void *pick(bool stream, Dtype dtype, bool precise) {
+    if (stream) {
+        if (precise) return (const void *)&attention_stream<D, true, true, _Float16>;
+        if (dtype == Dtype::BF16) return (const void *)&attention_stream<D, false, true, __bf16>;
+        return (const void *)&attention_stream<D, false, false, _Float16>;
+    }
+    if (precise) return (const void *)&attention_coop<D, NQT, true, true, _Float16, kCoopWaves>;
+    if (dtype == Dtype::BF16) return (const void *)&attention_coop<D, NQT, false, true, __bf16, kCoopWaves>;
+    return (const void *)&attention_coop<D, NQT, false, false, _Float16, kCoopWaves>;
 }
 
-// Resolve the kernel instance for (D, nqt, precise, dtype).
-const void *split_kernel(int D, int nqt, bool precise, Dtype dtype) {
-#define RS_SPLIT_CASE(DD, Q)                                                        \
-    if (D == DD && nqt == Q) {                                                      \
-        if (precise) return split_symbol<DD, Q, true, _Float16>();                  \
-        return dtype == Dtype::BF16 ? split_symbol<DD, Q, false, __bf16>()          \
-                                    : split_symbol<DD, Q, false, _Float16>();       \
+const void *split_kernel(const SplitPlan &p, int D, Dtype dtype, bool precise) {
+    const bool stream = p.kind == SplitKind::Stream;
+    if (D == 256) {
+        switch (p.nqt) {
+            case 1: return pick<256, 1>(stream, dtype, precise);
+            case 2: return pick<256, 2>(false, dtype, precise);
+            case 3: return pick<256, 3>(false, dtype, precise);
+        }
+    } else if (D == 128) {
+        switch (p.nqt) {
+            case 1: return pick<128, 1>(stream, dtype, precise);
+            case 2: return pick<128, 2>(false, dtype, precise);
+            case 3: return pick<128, 3>(false, dtype, precise);
+        }
     }
-    RS_SPLIT_CASE(128, 1)
-    RS_SPLIT_CASE(256, 1)
-#undef RS_SPLIT_CASE
     throw std::invalid_argument("unsupported head_dim / query rows for the split kernel");
+}
+
+// Decode kernel choice: the streaming kernel unless RS_DECODE_KERNEL=coop.
+bool decode_uses_coop() {
+    static const bool coop = [] {
+        const char *v = std::getenv("RS_DECODE_KERNEL");
+        return v && std::strcmp(v, "coop") == 0;
+    }();
+    return coop;
 }
 
 }  // namespace
@@ -383,18 +697,47 @@ int device_cu_count() {
 
 int chunk_tokens(const Shape &s) { return std::max(1, kMaxRows / s.group()); }
 
-SplitPlan plan_split(const Shape &s, int tokens, bool precise) {
-    (void)precise;
+int block_threads(const SplitPlan &p) {
+    return (p.kind == SplitKind::Coop ? kCoopWaves : kWaves) * kWave;
+}
+
+// Resident workgroups per CU of a kernel instance (cached per device).
+int blocks_per_cu(const void *kernel, int threads) {
+    static std::mutex mutex;
+    static std::vector<std::pair<std::pair<int, const void *>, int>> cache;
+    int device = 0;
+    check(hipGetDevice(&device));
+    std::lock_guard<std::mutex> lock(mutex);
+    for (const auto &e : cache)
+        if (e.first.first == device && e.first.second == kernel) return e.second;
+    int n = 0;
+    check(hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, kernel, threads, 0));
+    n = std::max(1, n);
+    cache.push_back({{device, kernel}, n});
+    return n;
+}
+
+SplitPlan plan_split(const Shape &s, int tokens, Dtype dtype, bool precise) {
     SplitPlan p;
     p.rows = s.group() * tokens;
     p.nqt = (p.rows + 15) / 16;
+    p.kind = (p.nqt == 1 && !decode_uses_coop()) ? SplitKind::Stream : SplitKind::Coop;
     const long long n_keys = (long long)s.position + tokens;
-    p.n_blocks = (int)((n_keys + kPageTokens - 1) / kPageTokens);
-    // One workgroup per CU keeps every CU streaming; never give a wave less
-    // than one block on average.
-    const int per_head = (device_cu_count() + s.kv_heads - 1) / s.kv_heads;
-    const int by_blocks = (p.n_blocks + kWaves - 1) / kWaves;
-    p.splits = std::max(1, std::min({per_head, by_blocks, kMaxSplits}));
+    p.n_pages = (int)((n_keys + kPageTokens - 1) / kPageTokens);
+    p.splits = 1;
+    // Fill every CU with as many workgroups as stay resident.
+    const int resident = device_cu_count() *
+                         blocks_per_cu(split_kernel(p, s.head_dim, dtype, precise), block_threads(p));
+    const int per_head = std::max(1, std::min(resident / s.kv_heads, kMaxSplits));
+    if (p.kind == SplitKind::Stream) {
+        // Every wave gets at least one page on average.
+        p.splits = std::max(1, std::min(per_head, (p.n_pages + kWaves - 1) / kWaves));
+    } else {
+        // Contiguous page runs: the longest run sets the time, so use as few
+        // splits as give that same longest run (fewer partials to combine).
+        const int longest = (p.n_pages + per_head - 1) / per_head;
+        p.splits = (p.n_pages + longest - 1) / longest;
+    }
     return p;
 }
 
@@ -402,22 +745,23 @@ size_t plan_bytes(const Shape &s, const SplitPlan &p) {
     return (size_t)s.kv_heads * p.splits * p.rows * ((size_t)s.head_dim + 2) * sizeof(float);
 }
 
-size_t attention_workspace_bytes(const Shape &s, bool precise) {
+size_t attention_workspace_bytes(const Shape &s, Dtype dtype, bool precise) {
     const int ct = chunk_tokens(s);
     size_t best = 0;
     for (int t0 = 0; t0 < s.tokens; t0 += ct) {
         Shape c = s;
         c.position = s.position + t0;
-        best = std::max(best, plan_bytes(c, plan_split(c, std::min(ct, s.tokens - t0), precise)));
+        best = std::max(best, plan_bytes(c, plan_split(c, std::min(ct, s.tokens - t0), dtype, precise)));
     }
     return best;
 }
 
 void launch_split(const Shape &s, const SplitPlan &plan, Dtype dtype, bool precise,
-                  float scale, const void *q, const void *k_pages, const void *v_pages,
-                  void *workspace, hipStream_t stream) {
+                  float scale, const void *q, const void *q_lo, const void *k_pages,
+                  const void *v_pages, void *workspace, hipStream_t stream) {
     SplitArgs a;
     a.q = q;
+    a.q_lo = q_lo;
     a.k_pages = k_pages;
     a.v_pages = v_pages;
     a.part_o = static_cast<float *>(workspace);
@@ -428,12 +772,12 @@ void launch_split(const Shape &s, const SplitPlan &plan, Dtype dtype, bool preci
     a.rows = plan.rows;
     a.position = s.position;
     a.n_keys = s.position + plan.rows / s.group();
-    a.n_blocks = plan.n_blocks;
+    a.n_pages = plan.n_pages;
     a.splits = plan.splits;
     a.scale_log2 = scale * 1.4426950408889634f;
-    const void *kernel = split_kernel(s.head_dim, plan.nqt, precise, dtype);
+    const void *kernel = split_kernel(plan, s.head_dim, dtype, precise);
     void *args[] = {&a};
-    check(hipLaunchKernel(kernel, dim3(plan.splits, s.kv_heads), dim3(kWaves * kWave),
+    check(hipLaunchKernel(kernel, dim3(plan.splits, s.kv_heads), dim3(block_threads(plan)),
                           args, 0, stream));
 }
 
@@ -463,7 +807,7 @@ void launch_combine(const Shape &s, const SplitPlan &plan, Dtype dtype,
         throw std::invalid_argument("unsupported head_dim for the combine kernel");
     }
     void *args[] = {&c};
-    check(hipLaunchKernel(kernel, grid, dim3(s.head_dim), args, 0, stream));
+    check(hipLaunchKernel(kernel, grid, dim3(kWaves * kWave), args, 0, stream));
 }
 
 }  // namespace rs

@@ -68,6 +68,16 @@ inline void check(hipError_t result) {
 }
 
 // Device wave helpers ---------------------------------------------------------
+
+// Workgroup barrier that orders LDS only.  __syncthreads() is a workgroup
+// release/acquire fence over all address spaces, which makes every wave wait
+// for its outstanding global loads (vmcnt 0) at each barrier and so drains any
+// prefetch in flight; this one waits for LDS traffic (lgkmcnt 0) alone.
+__device__ __forceinline__ void lds_barrier() {
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
+    __builtin_amdgcn_s_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
+}
 __device__ __forceinline__ float wave_max(float x) {
     for (int d = 32; d; d >>= 1) x = fmaxf(x, __shfl_xor(x, d, kWave));
     return x;

@@ -15,33 +15,37 @@ struct Shape {
     int n_keys() const { return position + tokens; }
 };
 
+enum class SplitKind { Stream, Coop };
+
 // The split-K decomposition chosen for one launch of the partial kernel.
 struct SplitPlan {
-    int nqt;        // 16-row query tiles per KV head (rows = group * tokens)
-    int rows;       // valid query rows per KV head
-    int n_blocks;   // 32-key blocks per KV head
-    int splits;     // workgroups per KV head
+    SplitKind kind;  // attention_stream (one query tile) or attention_coop
+    int nqt;         // 16-row query tiles per KV head (rows = group * tokens)
+    int rows;        // valid query rows per KV head
+    int n_pages;     // 32-key pages per KV head holding keys 0..n_keys-1
+    int splits;      // workgroups per KV head
 };
 
 // Largest number of query rows (group * tokens) per KV head that one launch of
 // the split kernel holds; longer token runs are processed in chunks.
-constexpr int kMaxRows = 16;
+constexpr int kMaxRows = 48;
 
 int device_cu_count();
-SplitPlan plan_split(const Shape &s, int chunk_tokens, bool precise);
+SplitPlan plan_split(const Shape &s, int chunk_tokens, Dtype dtype, bool precise);
 // Tokens per chunk for a shape (chunk_tokens * group <= kMaxRows).
 int chunk_tokens(const Shape &s);
 // Workspace bytes for qv_attention on this shape (largest chunk).
-size_t attention_workspace_bytes(const Shape &s, bool precise);
+size_t attention_workspace_bytes(const Shape &s, Dtype dtype, bool precise);
 
 // Split-K partial kernel over the pages of every KV head.  q is 16-bit of
-// `dtype` ([tokens][q_heads][D]) or, when `precise`, float32.
+// `dtype`, [tokens][q_heads][D]; when `precise` (fp16 only) q and q_lo are
+// the hi and lo parts of an fp32 query.
 // Partial buffers of one plan: o [kv_heads][splits][rows][D], then m and l
 // [kv_heads][splits][2][rows], all float32.
 size_t plan_bytes(const Shape &s, const SplitPlan &p);
 void launch_split(const Shape &s, const SplitPlan &plan, Dtype dtype, bool precise,
-                  float scale, const void *q, const void *k_pages, const void *v_pages,
-                  void *workspace, hipStream_t stream);
+                  float scale, const void *q, const void *q_lo, const void *k_pages,
+                  const void *v_pages, void *workspace, hipStream_t stream);
 // Log-sum-exp combine of the partials into out.  Raw mode writes `dtype`
 // [tokens][q_heads][D]; fused mode (gate != nullptr) writes float32 and
 // multiplies by sigmoid(gate), gate being q_gate[t][h][D + d] (row stride 2D).
@@ -59,8 +63,9 @@ void launch_unpack(void *k_rows, void *v_rows, const void *k_pages, const void *
 
 // RMSNorm + RoPE of q and k, fp16 append of k and v into the pages at
 // position..position+batch-1 (the reference's attn_prepare semantics for the
-// fixed 24/4/256 model).  Writes the prepared q as float32 [batch][24][256].
-void launch_prepare(float *q, void *k_pages, void *v_pages, const float *q_gate,
+// fixed 24/4/256 model).  Writes the prepared fp32 q as two fp16 arrays
+// [2][batch][24][256]: hi = fp16(q), lo = fp16(q - hi).
+void launch_prepare(void *q_hilo, void *k_pages, void *v_pages, const float *q_gate,
                     const float *key, const float *value, const float *q_norm,
                     const float *k_norm, int batch, int position, int capacity,
                     float epsilon, hipStream_t stream);

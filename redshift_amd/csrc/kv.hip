@@ -57,7 +57,7 @@ void convert(void *k_pages, void *v_pages, const void *k_rows, const void *v_row
 // double precision (the reference rounds the angle to fp32, which at position
 // 139,263 is off by up to 2^-7 rad); the rotation itself is fp32.
 __global__ __launch_bounds__(256)
-void prepare_kernel(float *q, _Float16 *k_pages, _Float16 *v_pages, const float *q_gate,
+void prepare_kernel(_Float16 *q_hilo, _Float16 *k_pages, _Float16 *v_pages, const float *q_gate,
                     const float *key, const float *value, const float *q_norm,
                     const float *k_norm, int position, size_t head_stride, float epsilon) {
     constexpr int D = kModelHeadDim, H = kModelQHeads, HKV = kModelKvHeads;
@@ -89,7 +89,10 @@ void prepare_kernel(float *q, _Float16 *k_pages, _Float16 *v_pages, const float 
     }
     __syncthreads();
     if (is_q) {
-        q[((size_t)t * H + h) * D + i] = row[i];
+        const size_t idx = ((size_t)t * H + h) * D + i;
+        const _Float16 hi = (_Float16)row[i];
+        q_hilo[idx] = hi;
+        q_hilo[(size_t)gridDim.y * H * D + idx] = (_Float16)(row[i] - (float)hi);
     } else {
         const int token = position + t;
         k_pages[(size_t)kh * head_stride + k_page_offset(token, i, D)] = (_Float16)row[i];
@@ -113,12 +116,13 @@ void launch_unpack(void *k_rows, void *v_rows, const void *k_pages, const void *
                    kv_heads, head_dim, capacity, first, count, stream);
 }
 
-void launch_prepare(float *q, void *k_pages, void *v_pages, const float *q_gate,
+void launch_prepare(void *q_hilo, void *k_pages, void *v_pages, const float *q_gate,
                     const float *key, const float *value, const float *q_norm,
                     const float *k_norm, int batch, int position, int capacity,
                     float epsilon, hipStream_t stream) {
     hipLaunchKernelGGL(prepare_kernel, dim3(kModelQHeads + kModelKvHeads, batch),
-                       dim3(kModelHeadDim), 0, stream, q, static_cast<_Float16 *>(k_pages),
+                       dim3(kModelHeadDim), 0, stream, static_cast<_Float16 *>(q_hilo),
+                       static_cast<_Float16 *>(k_pages),
                        static_cast<_Float16 *>(v_pages), q_gate, key, value, q_norm, k_norm,
                        position, (size_t)capacity * kModelHeadDim, epsilon);
     check(hipGetLastError());

@@ -139,7 +139,7 @@ def test_device_entry_points_validate_before_touching_the_device(lib):
     assert call(scale=math.inf) == -1 and b'scale' in lib.qv_error()
     assert call(out=None) == -1 and lib.qv_error() == b'null attention buffer'
     assert call(out=ct.c_void_p(4098)) == -1 and b'aligned' in lib.qv_error()
-    assert call(dtype=QV_BF16, q_heads=24 * 17, kv_heads=1) == -1 and b'16 query heads' in lib.qv_error()
+    assert call(dtype=QV_BF16, q_heads=24 * 17, kv_heads=1) == -1 and b'48 query heads' in lib.qv_error()
     assert lib.qv_kv_pack(p, p, p, p, 4, 256, 128, 100, 29, None) == -1
     assert b'capacity' in lib.qv_error()
     assert lib.qv_kv_pack(p, None, None, p, 4, 256, 128, 0, 1, None) == -1
