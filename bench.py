@@ -24,6 +24,7 @@ sys.path.insert(0, str(ROOT))
 
 METRIC = 'µs/layer + achieved HBM GB/s, GQA decode/verify-8 @16K and 139,264 ctx'
 HBM_PEAK_GBS = 8000.0
+MFMA_BF16_PEAK = 2.5e15   # dense bf16 FLOP/s
 LAYERS = 16
 
 
@@ -38,6 +39,7 @@ def make_layers(torch, A, w, layers, seed):
     gen.manual_seed(seed)
     caches, queries = [], []
     capacity = A.round_capacity(w.keys)
+    dtype = torch.bfloat16 if w.dtype == 'bf16' else torch.float16
     for _ in range(layers):
         k = torch.randn((w.keys, w.kv_heads, w.head_dim), generator=gen, device='cuda',
                         dtype=torch.float32) * w.kv_std
@@ -46,10 +48,10 @@ def make_layers(torch, A, w, layers, seed):
         if w.outliers:
             idx = torch.randperm(w.keys, generator=gen, device='cuda')[:w.outliers]
             k[idx] *= w.outlier_gain
-        cache = A.PagedKV(w.kv_heads, w.head_dim, capacity, torch.float16)
-        cache.pack(k.half(), v.half())
+        cache = A.PagedKV(w.kv_heads, w.head_dim, capacity, dtype)
+        cache.pack(k.to(dtype), v.to(dtype))
         del k, v
-        q = (torch.randn((w.tokens, w.q_heads, w.head_dim), generator=gen, device='cuda') * w.q_std).half()
+        q = (torch.randn((w.tokens, w.q_heads, w.head_dim), generator=gen, device='cuda') * w.q_std).to(dtype)
         caches.append(cache)
         queries.append(q)
     torch.cuda.synchronize()
@@ -57,11 +59,15 @@ def make_layers(torch, A, w, layers, seed):
 
 
 def time_workload(torch, A, w, layers, steps, warmup, seed):
-    """Returns dict(ms_per_step, split_us) for `steps` steps of `layers` calls."""
+    """Times `steps` steps of `layers` attention calls.
+
+    Returns dict(ms_per_step: one step replayed as a captured HIP graph,
+    eager_ms_per_step: the same launches issued one by one, split_us: average
+    duration of the split-K kernel from events recorded around each of its
+    launches in the eager loop, on the stream it runs on)."""
     caches, queries = make_layers(torch, A, w, layers, seed)
     ws = A.workspace(A.attention_workspace_bytes(w.q_heads, w.kv_heads, w.head_dim, w.tokens, w.position))
     outs = [torch.empty_like(q) for q in queries]
-
     one_chunk = w.tokens * w.group <= A.MAX_CHUNK_ROWS
 
     def step(events=None):
@@ -77,24 +83,40 @@ def time_workload(torch, A, w, layers, steps, warmup, seed):
             if one_chunk:
                 A.attention_combine(outs[i], caches[i], w.position, ws)
 
+    def timed(fn, n):
+        torch.cuda.synchronize()
+        start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        start.record()
+        for s in range(n):
+            fn(s)
+        end.record()
+        torch.cuda.synchronize()
+        return start.elapsed_time(end) / n
+
     for _ in range(warmup):
         step()
-    torch.cuda.synchronize()
     ev = [[[torch.cuda.Event(enable_timing=True) for _ in range(2)] for _ in range(layers)]
           for _ in range(steps)]
-    start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-    torch.cuda.synchronize()
-    start.record()
-    for s in range(steps):
-        step(ev[s])
-    end.record()
-    torch.cuda.synchronize()
-    total_ms = start.elapsed_time(end)
+    eager_ms = timed(lambda s: step(ev[s]), steps)
     split_ms = [e[0].elapsed_time(e[1]) for st in ev for e in st]
-    del caches
+
+    # The same step captured once and replayed (no per-launch host overhead).
+    graph = torch.cuda.CUDAGraph()
+    capture_stream = torch.cuda.Stream()
+    capture_stream.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(capture_stream):
+        step()                      # plans resolved before capture
+        torch.cuda.synchronize()
+        with torch.cuda.graph(graph, stream=capture_stream):
+            step()
+    torch.cuda.current_stream().wait_stream(capture_stream)
+    for _ in range(warmup):
+        graph.replay()
+    graph_ms = timed(lambda s: graph.replay(), steps)
+    del graph, caches
     torch.cuda.empty_cache()
-    return dict(ms_per_step=total_ms / steps, split_us=1000.0 * sum(split_ms) / len(split_ms),
-                outs=None)
+    return dict(ms_per_step=graph_ms, eager_ms_per_step=eager_ms,
+                split_us=1000.0 * sum(split_ms) / len(split_ms))
 
 
 def cpu_baseline(w, target_s=10.0):
@@ -163,6 +185,9 @@ def main():
                    'head_dim': w.head_dim, 'keys': w.keys, 'tokens': w.tokens,
                    'layers': args.layers, 'kv_dtype': 'f16', 'outlier_keys': w.outliers},
         'us_per_layer': round(1000 * r['ms_per_step'] / args.layers, 2),
+        'eager_us_per_layer': round(1000 * r['eager_ms_per_step'] / args.layers, 2),
+        'timing': 'step = 16 layers x (split-K kernel + combine) replayed as one HIP graph; '
+                  'roofline kernel_us = split-K kernel alone, HIP events in an eager loop',
         'roofline': {'bound': 'hbm', 'kernel': 'attention_split (decode)',
                      'achieved': round(split_gbs, 1), 'peak': HBM_PEAK_GBS, 'unit': 'GB/s',
                      'frac': round(split_gbs / HBM_PEAK_GBS, 4), 'traffic': None,
@@ -177,8 +202,19 @@ def main():
             us = 1000 * rx['ms_per_step'] / args.layers
             extra[name] = {'us_per_layer': round(us, 2),
                            'GB/s': round(wx.kv_bytes() / (us * 1e-6) / 1e9, 1),
+                           'eager_us_per_layer': round(1000 * rx['eager_ms_per_step'] / args.layers, 2),
                            'split_kernel_us': round(rx['split_us'], 2),
+                           'split_kernel_GB/s': round(wx.kv_bytes() / (rx['split_us'] * 1e-6) / 1e9, 1),
                            'frac_hbm': round(wx.kv_bytes() / (us * 1e-6) / 1e9 / HBM_PEAK_GBS, 4)}
+        wp = WORKLOADS['prefill_2k']
+        log(f'prefill_2k: 4 layers')
+        rp = time_workload(torch, A, wp, 4, max(3, args.steps // 4), 2, seed=2)
+        kernel_s = rp['split_us'] * 1e-6
+        extra['prefill_2k'] = {'us_per_layer': round(1000 * rp['ms_per_step'] / 4, 1),
+                               'kernel_us': round(rp['split_us'], 1),
+                               'TFLOP/s': round(wp.flops() / kernel_s / 1e12, 1),
+                               'frac_mfma_peak': round(wp.flops() / kernel_s / MFMA_BF16_PEAK, 4),
+                               'flops_per_layer': wp.flops()}
         result['extra'] = extra
     if not args.no_cpu:
         log('cpu baseline (numpy fp32, 1 thread, one layer)')

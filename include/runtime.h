@@ -85,6 +85,7 @@ void qv_destroy(void *handle);
  * ---------------------------------------------------------------------- */
 #define QV_F16 1
 #define QV_BF16 2
+#define QV_F32 3 /* output type only */
 
 /* Bytes of one K (or V) cache: kv_heads * capacity * head_dim * 2. */
 int qv_kv_bytes(uint64_t *bytes, int kv_heads, int head_dim, int capacity);
@@ -106,12 +107,16 @@ int qv_attention_workspace(uint64_t *bytes, int q_heads, int kv_heads, int head_
  * (src/kernels.cu:435-456,466-503) without prepare and gate, generalised to
  * q_heads/kv_heads/head_dim/scale: out[t][h] = softmax_p(q[t][h] . k[p][h/G] *
  * scale, p <= position+t) . v[p][h/G], G = q_heads/kv_heads.
- * q, out: [tokens][q_heads][head_dim] of `dtype`; fp32 softmax and
- * accumulation. head_dim 128 or 256; G <= 48; 1 <= tokens;
- * position+tokens <= capacity. Split-K over all CUs plus a log-sum-exp
- * combine; work = qv_attention_split then qv_attention_combine. */
+ * q: [tokens][q_heads][head_dim] of `dtype` (QV_F16 or QV_BF16), like the
+ * pages; out: same shape, of `out_dtype` (`dtype`, or QV_F32 as the
+ * reference's float output); fp32 softmax and accumulation. head_dim 128 or
+ * 256; G <= 48; 1 <= tokens; position+tokens <= capacity. Up to 48 query
+ * rows per KV head (G*tokens): split-K over all CUs plus a log-sum-exp
+ * combine (qv_attention_split then qv_attention_combine). More rows (chunked
+ * prefill): one workgroup per 128 rows streams the visible pages through LDS;
+ * the workspace is then 0 bytes and may be NULL. */
 int qv_attention(void *out, const void *q, const void *k_pages, const void *v_pages,
-                 int dtype, int q_heads, int kv_heads, int head_dim,
+                 int dtype, int out_dtype, int q_heads, int kv_heads, int head_dim,
                  int tokens, int position, int capacity, float scale,
                  void *workspace, uint64_t workspace_bytes, void *stream);
 /* The two phases of qv_attention for one token chunk (G*tokens <= 48), for
@@ -120,7 +125,7 @@ int qv_attention_split(const void *q, const void *k_pages, const void *v_pages,
                        int dtype, int q_heads, int kv_heads, int head_dim,
                        int tokens, int position, int capacity, float scale,
                        void *workspace, uint64_t workspace_bytes, void *stream);
-int qv_attention_combine(void *out, int dtype, int q_heads, int kv_heads, int head_dim,
+int qv_attention_combine(void *out, int dtype, int out_dtype, int q_heads, int kv_heads, int head_dim,
                          int tokens, int position, const void *workspace,
                          uint64_t workspace_bytes, void *stream);
 

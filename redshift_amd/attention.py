@@ -7,7 +7,7 @@ import ctypes as ct
 
 import torch
 
-from .runtime import QV_BF16, QV_F16, check, library
+from .runtime import QV_BF16, QV_F16, QV_F32, check, library
 
 PAGE_TOKENS = 32
 # Query rows (group * tokens) per KV head that one split/combine pair serves.
@@ -20,6 +20,11 @@ def dtype_code(dtype):
     if dtype == torch.bfloat16:
         return QV_BF16
     raise ValueError(f'unsupported KV dtype {dtype}: use float16 or bfloat16')
+
+
+def out_code(dtype):
+    """Output type code: the input's 16-bit type or float32."""
+    return QV_F32 if dtype == torch.float32 else dtype_code(dtype)
 
 
 def round_capacity(tokens):
@@ -80,19 +85,21 @@ def workspace(nbytes, device='cuda'):
     return torch.empty(max(int(nbytes), 256), dtype=torch.uint8, device=device)
 
 
-def attention(q, cache, position, scale, out=None, ws=None):
+def attention(q, cache, position, scale, out=None, ws=None, out_dtype=None):
     """Raw causal GQA attention: q [tokens][q_heads][head_dim] (cache dtype),
-    row t sees keys 0..position+t of `cache` (a PagedKV)."""
+    row t sees keys 0..position+t of `cache` (a PagedKV).  The output has
+    q's dtype, or float32 when out_dtype (or out's dtype) says so."""
     lib = library()
     q = q.contiguous()
     tokens, q_heads, head_dim = q.shape
     if out is None:
-        out = torch.empty_like(q)
+        out = torch.empty(q.shape, dtype=out_dtype or q.dtype, device=q.device)
     if ws is None:
         ws = workspace(attention_workspace_bytes(q_heads, cache.kv_heads, head_dim, tokens, position), q.device)
     check(lib, lib.qv_attention(_ptr(out), _ptr(q), _ptr(cache.k), _ptr(cache.v), dtype_code(q.dtype),
-                                q_heads, cache.kv_heads, head_dim, tokens, position, cache.capacity,
-                                float(scale), _ptr(ws), ws.numel(), _stream()))
+                                out_code(out.dtype), q_heads, cache.kv_heads, head_dim, tokens,
+                                position, cache.capacity, float(scale), _ptr(ws), ws.numel(),
+                                _stream()))
     return out
 
 
@@ -109,8 +116,9 @@ def attention_combine(out, cache, position, ws):
     """Phase 2 of `attention` for one chunk (log-sum-exp combine into out)."""
     lib = library()
     tokens, q_heads, head_dim = out.shape
-    check(lib, lib.qv_attention_combine(_ptr(out), dtype_code(out.dtype), q_heads, cache.kv_heads,
-                                        head_dim, tokens, position, _ptr(ws), ws.numel(), _stream()))
+    check(lib, lib.qv_attention_combine(_ptr(out), dtype_code(cache.dtype), out_code(out.dtype), q_heads,
+                                        cache.kv_heads, head_dim, tokens, position, _ptr(ws),
+                                        ws.numel(), _stream()))
 
 
 def fused_workspace_bytes(batch, position):

@@ -73,6 +73,12 @@ rs::Dtype dtype_of(int dtype) {
     return dtype == QV_BF16 ? rs::Dtype::BF16 : rs::Dtype::F16;
 }
 
+// True for fp32 output; otherwise the output type must equal the input's.
+bool out_f32_of(int dtype, int out_dtype) {
+    require(out_dtype == dtype || out_dtype == QV_F32, "out_dtype must be dtype or QV_F32");
+    return out_dtype == QV_F32;
+}
+
 void geometry(int kv_heads, int head_dim, int capacity) {
     require(kv_heads >= 1 && kv_heads <= 256, "kv_heads must be in 1..256");
     require(head_dim == 128 || head_dim == 256, "head_dim must be 128 or 256");
@@ -101,8 +107,14 @@ void fits_cache(const rs::Shape &s) {
 // the lo part of a precise query) are 16-bit [tokens][q_heads][D].
 void run_attention(const rs::Shape &s, rs::Dtype dtype, bool precise, float scale,
                    const void *q, const void *q_lo, const void *k_pages, const void *v_pages,
-                   void *workspace, void *out, size_t out_elem, const float *gate,
+                   void *workspace, void *out, bool out_f32, const float *gate,
                    hipStream_t stream) {
+    if (!precise && s.group() * s.tokens > rs::kMaxRows) {
+        // Long token runs (chunked prefill): one launch, no workspace.
+        rs::launch_prefill(s, dtype, scale, q, k_pages, v_pages, out, out_f32, stream);
+        return;
+    }
+    const size_t out_elem = out_f32 ? sizeof(float) : sizeof(uint16_t);
     const int ct = rs::chunk_tokens(s);
     const size_t row = (size_t)s.q_heads * s.head_dim;
     for (int t0 = 0; t0 < s.tokens; t0 += ct) {
@@ -115,7 +127,7 @@ void run_attention(const rs::Shape &s, rs::Dtype dtype, bool precise, float scal
                          q_lo ? static_cast<const char *>(q_lo) + q_offset : nullptr,
                          k_pages, v_pages, workspace, stream);
         rs::launch_combine(c, plan, dtype, workspace,
-                           static_cast<char *>(out) + t0 * row * out_elem,
+                           static_cast<char *>(out) + t0 * row * out_elem, out_f32,
                            gate ? gate + (size_t)t0 * 2 * row : nullptr, stream);
     }
 }
@@ -189,7 +201,7 @@ extern "C" int qv_test_attention(float *out, void *key_cache, void *value_cache,
         run_attention(shape, rs::Dtype::F16, true, 1.0f / 16.0f, q.data(),
                       static_cast<uint16_t *>(q.data()) + (size_t)batch * H * D,
                       k_pages.data(), v_pages.data(), workspace.data(), output.data(),
-                      sizeof(float), qg.floats(), stream);
+                      true, qg.floats(), stream);
         rs::launch_unpack(k_rows.data(), v_rows.data(), k_pages.data(), v_pages.data(), HKV, D,
                           capacity, 0, n, stream);
         check(hipGetLastError());
@@ -285,24 +297,31 @@ extern "C" int qv_attention_workspace(uint64_t *bytes, int q_heads, int kv_heads
 
 static void raw_buffers(const void *out, const void *q, const void *k_pages, const void *v_pages,
                         const void *workspace) {
-    require(q && k_pages && v_pages && workspace && out, "null attention buffer");
+    require(q && k_pages && v_pages && out, "null attention buffer");
     require(aligned16(q) && aligned16(k_pages) && aligned16(v_pages) && aligned16(workspace) &&
             aligned16(out), "attention buffers must be 16-byte aligned");
 }
 
+// The workspace may be NULL only where the shape needs none.
+static void workspace_fits(const void *workspace, uint64_t bytes, size_t needed) {
+    require(workspace || !needed, "null attention buffer");
+    require(bytes >= needed, "workspace too small");
+}
+
 extern "C" int qv_attention(void *out, const void *q, const void *k_pages, const void *v_pages,
-                            int dtype, int q_heads, int kv_heads, int head_dim,
+                            int dtype, int out_dtype, int q_heads, int kv_heads, int head_dim,
                             int tokens, int position, int capacity, float scale,
                             void *workspace, uint64_t workspace_bytes, void *stream) {
     return call([&] {
         const rs::Dtype dt = dtype_of(dtype);
+        const bool out_f32 = out_f32_of(dtype, out_dtype);
         const rs::Shape s = attention_shape(q_heads, kv_heads, head_dim, tokens, position, capacity);
         fits_cache(s);
         require(std::isfinite(scale), "scale must be finite");
         raw_buffers(out, q, k_pages, v_pages, workspace);
-        require(workspace_bytes >= rs::attention_workspace_bytes(s, dt, false), "workspace too small");
-        run_attention(s, dt, false, scale, q, nullptr, k_pages, v_pages, workspace, out, 2, nullptr,
-                      static_cast<hipStream_t>(stream));
+        workspace_fits(workspace, workspace_bytes, rs::attention_workspace_bytes(s, dt, false));
+        run_attention(s, dt, false, scale, q, nullptr, k_pages, v_pages, workspace, out, out_f32,
+                      nullptr, static_cast<hipStream_t>(stream));
     });
 }
 
@@ -324,18 +343,19 @@ extern "C" int qv_attention_split(const void *q, const void *k_pages, const void
     });
 }
 
-extern "C" int qv_attention_combine(void *out, int dtype, int q_heads, int kv_heads, int head_dim,
-                                    int tokens, int position, const void *workspace,
+extern "C" int qv_attention_combine(void *out, int dtype, int out_dtype, int q_heads, int kv_heads,
+                                    int head_dim, int tokens, int position, const void *workspace,
                                     uint64_t workspace_bytes, void *stream) {
     return call([&] {
         const rs::Dtype dt = dtype_of(dtype);
+        const bool out_f32 = out_f32_of(dtype, out_dtype);
         const rs::Shape s = attention_shape(q_heads, kv_heads, head_dim, tokens, position, 0);
         require(tokens <= rs::chunk_tokens(s), "qv_attention_combine takes one chunk: group*tokens <= 48");
         require(out && workspace, "null attention buffer");
         require(aligned16(out) && aligned16(workspace), "attention buffers must be 16-byte aligned");
         const rs::SplitPlan plan = rs::plan_split(s, tokens, dt, false);
         require(workspace_bytes >= rs::plan_bytes(s, plan), "workspace too small");
-        rs::launch_combine(s, plan, dt, workspace, out, nullptr, static_cast<hipStream_t>(stream));
+        rs::launch_combine(s, plan, dt, workspace, out, out_f32, nullptr, static_cast<hipStream_t>(stream));
     });
 }
 
@@ -379,6 +399,6 @@ extern "C" int qv_attention_fused(float *out, void *k_pages, void *v_pages,
         rs::launch_prepare(q, k_pages, v_pages, q_gate, key, value, q_norm, k_norm, batch, position,
                            capacity, epsilon, st);
         run_attention(s, rs::Dtype::F16, true, 1.0f / 16.0f, q, q + (size_t)batch * H * D, k_pages,
-                      v_pages, partials, out, sizeof(float), q_gate, st);
+                      v_pages, partials, out, true, q_gate, st);
     });
 }

@@ -562,73 +562,81 @@ struct CombineArgs {
 };
 
 // One workgroup (4 waves) per (row, KV head).  Lane l owns head dims
-// DV*l .. DV*l+DV-1 (DV = D/64); wave w sums splits w, w+4, w+8, ... with eight
-// independent loads in flight per batch; the waves reduce through LDS.
-template <int D, typename KV, bool FUSED>
+// DV*l .. DV*l+DV-1 (DV = D/64); wave w takes splits w, w+4, w+8, ... and
+// issues the loads of up to kBatch of them (their m, l and partial row) at
+// once, so a combine over up to 4*kBatch splits costs one memory round trip.
+// The waves then agree on the row max and reduce through LDS.
+// OUT: kOutSame writes the KV type, kOutF32 fp32, kOutGated fp32 times
+// sigmoid(gate).
+enum { kOutSame = 0, kOutF32 = 1, kOutGated = 2 };
+
+template <int D, typename KV, int OUT>
 __global__ __launch_bounds__(kWaves * kWave)
 void attention_combine(CombineArgs c) {
     constexpr int DV = D / kWave;
-    constexpr int kBatch = 8;
-    __shared__ float wts[kMaxSplits];
-    __shared__ float red[kWaves];
-    __shared__ float part[kWaves - 1][D];
+    constexpr int kBatch = 16;
+    __shared__ float wmax[kWaves];
+    __shared__ float part[kWaves][D + 1];
     const int row = blockIdx.x, h = blockIdx.y, tid = threadIdx.x;
     const int lane = tid & 63, w = tid >> 6;
-    const float *ml = c.part_ml + (size_t)h * c.splits * 2 * c.rows;
-
-    float M = -INFINITY;
-    for (int s = tid; s < c.splits; s += kWaves * kWave) M = fmaxf(M, ml[(size_t)s * 2 * c.rows + row]);
-    M = wave_max(M);
-    if (lane == 0) red[w] = M;
-    __syncthreads();
-    M = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
-    __syncthreads();
-    const float mu = M == -INFINITY ? 0.f : M;
-    float L = 0.f;
-    for (int s = tid; s < c.splits; s += kWaves * kWave) {
-        const float wgt = exp2f(ml[(size_t)s * 2 * c.rows + row] - mu);
-        wts[s] = wgt;
-        L += wgt * ml[(size_t)s * 2 * c.rows + c.rows + row];
-    }
-    L = wave_sum(L);
-    if (lane == 0) red[w] = L;
-    __syncthreads();
-    L = red[0] + red[1] + red[2] + red[3];
-
+    const float *ml = c.part_ml + (size_t)h * c.splits * 2 * c.rows + row;
     const float *po = c.part_o + ((size_t)h * c.splits * c.rows + row) * D + lane * DV;
     const size_t stride = (size_t)c.rows * D;
-    float acc[DV] = {};
-    for (int s0 = w; s0 < c.splits; s0 += kWaves * kBatch) {
-        float v[kBatch][DV];
+
+    float M = -INFINITY, L = 0.f, acc[DV] = {};
+    // Rounds of 4*kBatch splits (one round for up to 64 splits).
+    for (int s0 = 0; s0 < c.splits; s0 += kWaves * kBatch) {
+        float mv[kBatch], lv[kBatch], ov[kBatch][DV];
 #pragma unroll
         for (int i = 0; i < kBatch; ++i) {
-            const int s = s0 + i * kWaves;
+            const int s = s0 + w + kWaves * i;
+            const bool ok = s < c.splits;
+            const int sc = ok ? s : 0;
+            mv[i] = ok ? ml[(size_t)sc * 2 * c.rows] : -INFINITY;
+            lv[i] = ok ? ml[(size_t)sc * 2 * c.rows + c.rows] : 0.f;
 #pragma unroll
-            for (int d = 0; d < DV; ++d) v[i][d] = s < c.splits ? po[(size_t)s * stride + d] : 0.f;
+            for (int d = 0; d < DV; ++d) ov[i][d] = ok ? po[(size_t)sc * stride + d] : 0.f;
         }
+        // Fold this round into the running (M, L, acc) of the wave.
+        float rm = M;
+#pragma unroll
+        for (int i = 0; i < kBatch; ++i) rm = fmaxf(rm, mv[i]);
+        const float mu = rm == -INFINITY ? 0.f : rm;
+        const float f = __builtin_amdgcn_exp2f(M - mu);
+        L *= f;
+#pragma unroll
+        for (int d = 0; d < DV; ++d) acc[d] *= f;
 #pragma unroll
         for (int i = 0; i < kBatch; ++i) {
-            const int s = s0 + i * kWaves;
-            const float wgt = s < c.splits ? wts[s] : 0.f;
+            const float wgt = __builtin_amdgcn_exp2f(mv[i] - mu);
+            L += wgt * lv[i];
 #pragma unroll
-            for (int d = 0; d < DV; ++d) acc[d] += wgt * v[i][d];
+            for (int d = 0; d < DV; ++d) acc[d] += wgt * ov[i][d];
         }
+        M = rm;
     }
-    if (w > 0) {
+    if (lane == 0) wmax[w] = M;
+    __syncthreads();
+    const float G = fmaxf(fmaxf(wmax[0], wmax[1]), fmaxf(wmax[2], wmax[3]));
+    const float gu = G == -INFINITY ? 0.f : G;
+    const float f = __builtin_amdgcn_exp2f(M - gu);
 #pragma unroll
-        for (int d = 0; d < DV; ++d) part[w - 1][lane * DV + d] = acc[d];
-    }
+    for (int d = 0; d < DV; ++d) part[w][lane * DV + d] = acc[d] * f;
+    if (lane == 0) part[w][D] = L * f;
     __syncthreads();
     if (w == 0) {
+        const float Lt = part[0][D] + part[1][D] + part[2][D] + part[3][D];
         const int t = row / c.group, hq = h * c.group + (row - t * c.group);
         const size_t idx = ((size_t)t * c.q_heads + hq) * D + lane * DV;
 #pragma unroll
         for (int d = 0; d < DV; ++d) {
-            const float o = (acc[d] + part[0][lane * DV + d] + part[1][lane * DV + d] +
-                             part[2][lane * DV + d]) / L;
-            if constexpr (FUSED) {
-                const float gv = c.gate[((size_t)t * c.q_heads + hq) * 2 * D + D + lane * DV + d];
+            const int j = lane * DV + d;
+            const float o = (part[0][j] + part[1][j] + part[2][j] + part[3][j]) / Lt;
+            if constexpr (OUT == kOutGated) {
+                const float gv = c.gate[((size_t)t * c.q_heads + hq) * 2 * D + D + j];
                 static_cast<float *>(c.out)[idx + d] = o * (1.f / (1.f + expf(-gv)));
+            } else if constexpr (OUT == kOutF32) {
+                static_cast<float *>(c.out)[idx + d] = o;
             } else {
                 static_cast<KV *>(c.out)[idx + d] = (KV)o;
             }
@@ -649,6 +657,14 @@ const void *pick(bool stream, Dtype dtype, bool precise) {
     if (precise) return (const void *)&attention_coop<D, NQT, true, true, _Float16, kCoopWaves>;
     if (dtype == Dtype::BF16) return (const void *)&attention_coop<D, NQT, false, true, __bf16, kCoopWaves>;
     return (const void *)&attention_coop<D, NQT, false, false, _Float16, kCoopWaves>;
+}
+
+template <int D>
+const void *combine_kernel(Dtype dtype, bool out_f32, bool gated) {
+    if (gated) return (const void *)&attention_combine<D, _Float16, kOutGated>;
+    if (out_f32) return (const void *)&attention_combine<D, _Float16, kOutF32>;
+    return dtype == Dtype::BF16 ? (const void *)&attention_combine<D, __bf16, kOutSame>
+                                : (const void *)&attention_combine<D, _Float16, kOutSame>;
 }
 
 const void *split_kernel(const SplitPlan &p, int D, Dtype dtype, bool precise) {
@@ -746,6 +762,7 @@ size_t plan_bytes(const Shape &s, const SplitPlan &p) {
 }
 
 size_t attention_workspace_bytes(const Shape &s, Dtype dtype, bool precise) {
+    if (!precise && s.group() * s.tokens > kMaxRows) return 0;   // prefill kernel
     const int ct = chunk_tokens(s);
     size_t best = 0;
     for (int t0 = 0; t0 < s.tokens; t0 += ct) {
@@ -782,7 +799,7 @@ void launch_split(const Shape &s, const SplitPlan &plan, Dtype dtype, bool preci
 }
 
 void launch_combine(const Shape &s, const SplitPlan &plan, Dtype dtype,
-                    const void *workspace, void *out, const float *gate,
+                    const void *workspace, void *out, bool out_f32, const float *gate,
                     hipStream_t stream) {
     CombineArgs c;
     c.part_o = static_cast<const float *>(workspace);
@@ -794,18 +811,10 @@ void launch_combine(const Shape &s, const SplitPlan &plan, Dtype dtype,
     c.rows = plan.rows;
     c.splits = plan.splits;
     const dim3 grid(plan.rows, s.kv_heads);
-    const void *kernel = nullptr;
-    if (s.head_dim == 256) {
-        kernel = gate ? (const void *)&attention_combine<256, _Float16, true>
-               : dtype == Dtype::BF16 ? (const void *)&attention_combine<256, __bf16, false>
-                                      : (const void *)&attention_combine<256, _Float16, false>;
-    } else if (s.head_dim == 128) {
-        kernel = gate ? (const void *)&attention_combine<128, _Float16, true>
-               : dtype == Dtype::BF16 ? (const void *)&attention_combine<128, __bf16, false>
-                                      : (const void *)&attention_combine<128, _Float16, false>;
-    } else {
-        throw std::invalid_argument("unsupported head_dim for the combine kernel");
-    }
+    const void *kernel = s.head_dim == 256 ? combine_kernel<256>(dtype, out_f32, gate != nullptr)
+                       : s.head_dim == 128 ? combine_kernel<128>(dtype, out_f32, gate != nullptr)
+                                           : nullptr;
+    require(kernel != nullptr, "unsupported head_dim for the combine kernel");
     void *args[] = {&c};
     check(hipLaunchKernel(kernel, grid, dim3(kWaves * kWave), args, 0, stream));
 }

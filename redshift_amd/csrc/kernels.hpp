@@ -50,8 +50,13 @@ void launch_split(const Shape &s, const SplitPlan &plan, Dtype dtype, bool preci
 // [tokens][q_heads][D]; fused mode (gate != nullptr) writes float32 and
 // multiplies by sigmoid(gate), gate being q_gate[t][h][D + d] (row stride 2D).
 void launch_combine(const Shape &s, const SplitPlan &plan, Dtype dtype,
-                    const void *workspace, void *out, const float *gate,
+                    const void *workspace, void *out, bool out_f32, const float *gate,
                     hipStream_t stream);
+
+// Chunked prefill: all group*tokens query rows against the pages in one
+// launch (no workspace); `dtype` q and out, [tokens][q_heads][D].
+void launch_prefill(const Shape &s, Dtype dtype, float scale, const void *q, const void *k_pages,
+                    const void *v_pages, void *out, bool out_f32, hipStream_t stream);
 
 // Token-major rows [count][kv_heads][D] <-> pages, for tokens first..first+count.
 void launch_pack(void *k_pages, void *v_pages, const void *k_rows, const void *v_rows,

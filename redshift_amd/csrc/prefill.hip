@@ -1,0 +1,278 @@
+// Chunked prefill: many query tokens against the paged cache, on the matrix
+// cores.  The reference has no prefill kernel (its server prefills 8 tokens
+// at a time through attention/attention_tiled, src/kernels.cu:435-503 and
+// qvelox/server.py:187-191); this is the same causal GQA formula for long
+// token runs: row t sees keys 0..position+t.
+//
+// One workgroup (4 waves) owns 128 query rows of one KV head (row = token *
+// group + query head within the group); wave w owns rows 32w..32w+31 as two
+// 16-row tiles whose fragments stay in registers.  The workgroup walks the
+// pages that its last row can see.  Each page (K then V, 32 keys, 32*D
+// elements each) is copied verbatim into LDS with direct global->LDS loads,
+// double buffered: since pages are stored in MFMA operand order, every wave
+// then reads its A operands as conflict-free 16-byte LDS fragments.
+//   S^T[key][row] = K[key][:] . Q[row][:]     (A = K tile from LDS, B = Q)
+//   O^T[dim][row] += V^T[dim][key] P^T[key][row]  (A = V^T from LDS, B = P^T,
+//                                                  straight from S^T's C layout)
+// Online softmax in base 2 with a lazily moved row max (see attention.hip).
+// bf16 caches multiply by P split into hi + lo bf16 parts, fp16 caches by a
+// single fp16 P.
+//
+// Scheduling: workgroup i serves KV head i % kv_heads (with 4 KV heads the
+// round-robin dispatch over the 8 XCDs keeps every head on the same two XCDs,
+// whose L2s then hold that head's pages for all of its workgroups), and row
+// tiles go heaviest (latest rows, most keys) first.
+#include "kernels.hpp"
+
+#include <algorithm>
+#include <cmath>
+
+namespace rs {
+namespace {
+
+template <typename T> struct Vec8;
+template <> struct Vec8<_Float16> { using type = f16x8; };
+template <> struct Vec8<__bf16> { using type = bf16x8; };
+
+__device__ __forceinline__ f32x4 mfma(f16x8 a, f16x8 b, f32x4 c) {
+    return __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, c, 0, 0, 0);
+}
+__device__ __forceinline__ f32x4 mfma(bf16x8 a, bf16x8 b, f32x4 c) {
+    return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, 0, 0, 0);
+}
+
+constexpr int kPWaves = 4;                 // waves per prefill workgroup
+constexpr int kRowsPerWave = 32;           // two 16-row tiles
+constexpr int kRowsPerGroup = kPWaves * kRowsPerWave;
+constexpr float kLazy = 8.f;
+
+struct PrefillArgs {
+    const void *q;
+    const void *k_pages;
+    const void *v_pages;
+    void *out;
+    size_t head_stride;
+    int q_heads, kv_heads, group, rows, position, n_tiles;
+    float scale_log2;
+};
+
+__device__ __forceinline__ int v_slot_token(int g, int j) {
+    return j < 4 ? 4 * g + j : 16 + 4 * g + j - 4;
+}
+
+template <int D, typename KV, bool PSPLIT, typename OUT>
+__global__ __launch_bounds__(kPWaves * kWave, 1)
+void attention_prefill(PrefillArgs a) {
+    using V8 = typename Vec8<KV>::type;
+    constexpr int KS = D / 32, DT = D / 16, RT = kRowsPerWave / 16;
+    constexpr int PAGE = 32 * D;                       // elements of one K (or V) page
+    constexpr int CHUNKS = 2 * PAGE * 2 / 1024;        // 1 KiB chunks of K + V page
+    constexpr int CPW = CHUNKS / kPWaves;              // chunks per wave
+    static_assert(CHUNKS % kPWaves == 0, "chunks divide over the waves");
+    // Two page buffers [K page | V page], declared apart so the compiler can
+    // tell the buffer being filled from the one being read.
+    __shared__ __attribute__((aligned(16))) KV stage0[2 * PAGE];
+    __shared__ __attribute__((aligned(16))) KV stage1[2 * PAGE];
+
+    const int lane = threadIdx.x & 63, w = threadIdx.x >> 6, g = lane >> 4;
+    const int h = blockIdx.x % a.kv_heads;
+    const int tile = a.n_tiles - 1 - blockIdx.x / a.kv_heads;        // heaviest first
+    const int row0 = tile * kRowsPerGroup + w * kRowsPerWave;
+
+    // Query fragments (B operand): tile rt, k-step ks of lane l holds row
+    // row0 + 16*rt + l%16, dims 32*ks + 8*(l/16) .. +7.  Padded rows repeat
+    // the last row; their results are not stored.
+    V8 qf[RT][KS];
+    int limit[RT];
+#pragma unroll
+    for (int rt = 0; rt < RT; ++rt) {
+        const int row = min(row0 + 16 * rt + (lane & 15), a.rows - 1);
+        const int t = row / a.group, gg = row - t * a.group;
+        limit[rt] = a.position + t;
+        const KV *src = static_cast<const KV *>(a.q) +
+                        ((size_t)t * a.q_heads + (size_t)h * a.group + gg) * D + 8 * g;
+#pragma unroll
+        for (int ks = 0; ks < KS; ++ks) qf[rt][ks] = *reinterpret_cast<const V8 *>(src + 32 * ks);
+    }
+    // Keys this workgroup can see: 0 .. position + (token of its last row).
+    const int last_row = min(tile * kRowsPerGroup + kRowsPerGroup - 1, a.rows - 1);
+    const int n_keys = a.position + last_row / a.group + 1;
+    const int n_pages = (n_keys + 31) / 32;
+    // First page that any row of this wave masks (all rows see keys <= position).
+    const int wave_first_limit = a.position + min(row0, a.rows - 1) / a.group;
+
+    const KV *kh = static_cast<const KV *>(a.k_pages) + (size_t)h * a.head_stride;
+    const KV *vh = static_cast<const KV *>(a.v_pages) + (size_t)h * a.head_stride;
+    // Wave w copies chunks w*CPW .. of the [K | V] page p into `dst`.
+    auto stage_page = [&](int p, KV *dst) {
+#pragma unroll
+        for (int c = 0; c < CPW; ++c) {
+            const int chunk = w * CPW + c;
+            const int half = chunk / (CHUNKS / 2), off = (chunk % (CHUNKS / 2)) * 512;
+            const KV *src = (half ? vh : kh) + (size_t)p * PAGE + off + lane * 8;
+            __builtin_amdgcn_global_load_lds(reinterpret_cast<const void *>(src),
+                                             (__attribute__((address_space(3))) void *)(dst + half * PAGE + off),
+                                             16, 0, 0);
+        }
+    };
+
+    f32x4 acc[RT][DT];
+    float m[RT], l[RT];
+#pragma unroll
+    for (int rt = 0; rt < RT; ++rt) {
+        m[rt] = -INFINITY;
+        l[rt] = 0.f;
+#pragma unroll
+        for (int dt = 0; dt < DT; ++dt) acc[rt][dt] = f32x4{0.f, 0.f, 0.f, 0.f};
+    }
+
+    auto page = [&](int p, const KV *cur, KV *next) {
+        if (p + 1 < n_pages) stage_page(p + 1, next);   // uniform over the workgroup
+        const KV *ks_lds = cur;
+        const KV *vs_lds = cur + PAGE;
+        // ---- S^T for both 16-key tiles of the page ----
+        f32x4 s[RT][2];
+#pragma unroll
+        for (int rt = 0; rt < RT; ++rt) s[rt][0] = s[rt][1] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int ks = 0; ks < KS; ++ks) {
+#pragma unroll
+            for (int kt = 0; kt < 2; ++kt) {
+                const V8 kf = *reinterpret_cast<const V8 *>(ks_lds + kt * 16 * D + ks * 512 + lane * 8);
+#pragma unroll
+                for (int rt = 0; rt < RT; ++rt) s[rt][kt] = mfma(kf, qf[rt][ks], s[rt][kt]);
+            }
+        }
+        // ---- online softmax; keys past a row's limit are masked ----
+        const bool edge = p * 32 + 31 > wave_first_limit;
+        V8 ph[RT], pl[RT];
+        float alpha[RT];
+        bool rescale = false;
+#pragma unroll
+        for (int rt = 0; rt < RT; ++rt) {
+            float x[8];
+#pragma unroll
+            for (int j = 0; j < 8; ++j) x[j] = s[rt][j >> 2][j & 3] * a.scale_log2;
+            if (edge) {
+#pragma unroll
+                for (int j = 0; j < 8; ++j)
+                    if (p * 32 + 16 * (j >> 2) + 4 * g + (j & 3) > limit[rt]) x[j] = -INFINITY;
+            }
+            float bm = fmaxf(fmaxf(fmaxf(x[0], x[1]), fmaxf(x[2], x[3])),
+                             fmaxf(fmaxf(x[4], x[5]), fmaxf(x[6], x[7])));
+            bm = fmaxf(bm, __shfl_xor(bm, 16, kWave));
+            bm = fmaxf(bm, __shfl_xor(bm, 32, kWave));
+            alpha[rt] = 1.f;
+            if (bm > m[rt] + kLazy) {
+                alpha[rt] = __builtin_amdgcn_exp2f(m[rt] - bm);
+                m[rt] = bm;
+                rescale = true;
+            }
+            const float mu = m[rt] == -INFINITY ? 0.f : m[rt];
+            float ps = 0.f;
+#pragma unroll
+            for (int j = 0; j < 8; ++j) {
+                const float e = __builtin_amdgcn_exp2f(x[j] - mu);
+                const KV eh = (KV)e;
+                ph[rt][j] = eh;
+                if constexpr (PSPLIT) {
+                    pl[rt][j] = (KV)(e - (float)eh);
+                    ps += e;
+                } else {
+                    ps += (float)eh;
+                }
+            }
+            l[rt] = l[rt] * alpha[rt] + ps;
+        }
+        if (__any(rescale)) {
+#pragma unroll
+            for (int rt = 0; rt < RT; ++rt)
+#pragma unroll
+                for (int dt = 0; dt < DT; ++dt) acc[rt][dt] *= alpha[rt];
+        }
+        // ---- O^T += V^T P^T; V slots past the last key are zeroed ----
+        const bool tail = p * 32 + 32 > n_keys;
+#pragma unroll
+        for (int dt = 0; dt < DT; ++dt) {
+            V8 vf = *reinterpret_cast<const V8 *>(vs_lds + dt * 512 + lane * 8);
+            if (tail) {
+#pragma unroll
+                for (int j = 0; j < 8; ++j)
+                    if (p * 32 + v_slot_token(g, j) >= n_keys) vf[j] = (KV)0.f;
+            }
+#pragma unroll
+            for (int rt = 0; rt < RT; ++rt) {
+                acc[rt][dt] = mfma(vf, ph[rt], acc[rt][dt]);
+                if constexpr (PSPLIT) acc[rt][dt] = mfma(vf, pl[rt], acc[rt][dt]);
+            }
+        }
+        // The next page has landed in LDS for every wave, and every wave is
+        // done reading this one before it is overwritten.
+        __builtin_amdgcn_s_waitcnt(0);
+        __syncthreads();
+    };
+
+    stage_page(0, stage0);
+    __builtin_amdgcn_s_waitcnt(0);
+    __syncthreads();
+    for (int p = 0; p < n_pages; p += 2) {
+        page(p, stage0, stage1);
+        if (p + 1 < n_pages) page(p + 1, stage1, stage0);
+    }
+
+    // ---- normalise and store rows ----
+#pragma unroll
+    for (int rt = 0; rt < RT; ++rt) {
+        l[rt] += __shfl_xor(l[rt], 16, kWave);
+        l[rt] += __shfl_xor(l[rt], 32, kWave);
+        const int row = row0 + 16 * rt + (lane & 15);
+        if (row < a.rows) {
+            const int t = row / a.group, gg = row - t * a.group;
+            OUT *dst = static_cast<OUT *>(a.out) + ((size_t)t * a.q_heads + (size_t)h * a.group + gg) * D + 4 * g;
+            const float inv = 1.f / l[rt];
+#pragma unroll
+            for (int dt = 0; dt < DT; ++dt) {
+                typedef OUT OUT4 __attribute__((ext_vector_type(4)));
+                OUT4 o;
+#pragma unroll
+                for (int r = 0; r < 4; ++r) o[r] = (OUT)(acc[rt][dt][r] * inv);
+                *reinterpret_cast<OUT4 *>(dst + dt * 16) = o;
+            }
+        }
+    }
+}
+
+template <int D>
+const void *prefill_kernel(Dtype dtype, bool out_f32) {
+    if (dtype == Dtype::BF16)
+        return out_f32 ? (const void *)&attention_prefill<D, __bf16, true, float>
+                       : (const void *)&attention_prefill<D, __bf16, true, __bf16>;
+    return out_f32 ? (const void *)&attention_prefill<D, _Float16, false, float>
+                   : (const void *)&attention_prefill<D, _Float16, false, _Float16>;
+}
+
+}  // namespace
+
+void launch_prefill(const Shape &s, Dtype dtype, float scale, const void *q, const void *k_pages,
+                    const void *v_pages, void *out, bool out_f32, hipStream_t stream) {
+    PrefillArgs a;
+    a.q = q;
+    a.k_pages = k_pages;
+    a.v_pages = v_pages;
+    a.out = out;
+    a.head_stride = (size_t)s.capacity * s.head_dim;
+    a.q_heads = s.q_heads;
+    a.kv_heads = s.kv_heads;
+    a.group = s.group();
+    a.rows = s.group() * s.tokens;
+    a.position = s.position;
+    a.n_tiles = (a.rows + kRowsPerGroup - 1) / kRowsPerGroup;
+    a.scale_log2 = scale * 1.4426950408889634f;
+    const void *kernel = s.head_dim == 256 ? prefill_kernel<256>(dtype, out_f32)
+                       : s.head_dim == 128 ? prefill_kernel<128>(dtype, out_f32) : nullptr;
+    require(kernel != nullptr, "unsupported head_dim for the prefill kernel");
+    void *args[] = {&a};
+    check(hipLaunchKernel(kernel, dim3(a.n_tiles * s.kv_heads), dim3(kPWaves * kWave), args, 0, stream));
+}
+
+}  // namespace rs

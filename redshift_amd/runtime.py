@@ -13,6 +13,7 @@ DEFAULT_LIBRARY = Path(__file__).resolve().parent / 'lib' / 'libredshift_hip.so'
 
 QV_F16 = 1
 QV_BF16 = 2
+QV_F32 = 3
 
 # The reference's validation ABI (qvelox/runtime.py:13-17).
 TEST_SIGNATURES = {
@@ -41,9 +42,9 @@ DEVICE_SIGNATURES = {
     'qv_kv_pack': [_P] * 4 + [_I] * 5 + [_P],
     'qv_kv_unpack': [_P] * 4 + [_I] * 5 + [_P],
     'qv_attention_workspace': [ct.POINTER(_U64)] + [_I] * 5,
-    'qv_attention': [_P] * 4 + [_I] * 7 + [_F, _P, _U64, _P],
+    'qv_attention': [_P] * 4 + [_I] * 8 + [_F, _P, _U64, _P],
     'qv_attention_split': [_P] * 3 + [_I] * 7 + [_F, _P, _U64, _P],
-    'qv_attention_combine': [_P] + [_I] * 6 + [_P, _U64, _P],
+    'qv_attention_combine': [_P] + [_I] * 7 + [_P, _U64, _P],
     'qv_attention_fused_workspace': [ct.POINTER(_U64), _I, _I],
     'qv_attention_fused': [_P] * 8 + [_I] * 3 + [_F, _P, _U64, _P],
 }

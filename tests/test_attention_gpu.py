@@ -130,9 +130,9 @@ def make_cache(k, v, w, torch, capacity=None, fill_nan=False):
     return cache
 
 
-def gpu_attention(w, q, k, v, torch, **kw):
+def gpu_attention(w, q, k, v, torch, out_dtype=None, **kw):
     cache = make_cache(k, v, w, torch, **kw)
-    out = A.attention(to_torch(q, w.dtype, torch), cache, w.position, w.scale)
+    out = A.attention(to_torch(q, w.dtype, torch), cache, w.position, w.scale, out_dtype=out_dtype)
     torch.cuda.synchronize()
     return out.float().cpu().numpy().astype(np.float64)
 
@@ -237,3 +237,67 @@ def test_fused_device_path_matches_oracle(gpu):
     assert_close(out.cpu().numpy(), expected[0], 3e-4)
     assert_close(kc.float().cpu().numpy(), expected[1], 2e-3)
     assert_close(vc.float().cpu().numpy(), expected[2], 0)
+
+
+@pytest.mark.parametrize('T,position', [(1, 50000), (8, 2000)])
+def test_graph_replay_matches_eager(gpu, T, position):
+    """The device entry points enqueue kernels only (no allocation, no
+    synchronisation, no memset), so they can be captured in a HIP graph; every
+    replay, with eager work and synchronisations in between, reproduces the
+    eager result bit for bit."""
+    torch = gpu
+    w = Workload('graph', 24, 4, 256, T, position, 1 / 16, 'f16', 21, 1.0, 0.5)
+    q, k, v, _ = make_inputs(w)
+    cache = make_cache(k, v, w, torch)
+    qt = to_torch(q, 'f16', torch)
+    ws = A.workspace(A.attention_workspace_bytes(24, 4, 256, T, position))
+    eager = A.attention(qt, cache, position, w.scale, ws=ws).clone()
+    out = torch.empty_like(qt)
+    graph = torch.cuda.CUDAGraph()
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        A.attention(qt, cache, position, w.scale, out=out, ws=ws)
+        torch.cuda.synchronize()
+        with torch.cuda.graph(graph, stream=side):
+            A.attention(qt, cache, position, w.scale, out=out, ws=ws)
+    torch.cuda.current_stream().wait_stream(side)
+    for _ in range(3):
+        out.zero_()
+        A.attention(qt[:1], cache, position, w.scale, ws=ws)   # eager work reusing the workspace
+        torch.cuda.synchronize()
+        graph.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(out, eager)
+
+
+@pytest.mark.parametrize('q_heads,kv_heads,head_dim,T,position,dtype', [
+    (24, 4, 256, 9, 0, 'f16'),      # 54 rows: just past the split-K path
+    (24, 4, 256, 100, 37, 'bf16'),
+    (24, 4, 256, 300, 1000, 'f16'),
+    (8, 2, 128, 13, 5, 'bf16'),     # 52 rows, head_dim 128
+    (8, 2, 128, 200, 64, 'f16'),
+])
+def test_prefill_kernel_all_rows(gpu, q_heads, kv_heads, head_dim, T, position, dtype):
+    """Long token runs go through the prefill kernel; every row against the
+    oracle, pages past the last key filled with NaN.  The float32 output
+    (the reference's output type) is held to both bounds; the 16-bit output
+    must equal that value up to its own rounding (half an ulp)."""
+    w = Workload('prefill', q_heads, kv_heads, head_dim, T, position, 1 / head_dim ** .5, dtype, 300 + T, 1.0, 1.0)
+    q, k, v, _ = make_inputs(w)
+    want = ref.gqa_attention(to_float(q, dtype), to_float(k, dtype), to_float(v, dtype), position, w.scale)
+    got32 = gpu_attention(w, q, k, v, gpu, fill_nan=True, out_dtype=gpu.float32)
+    assert_parity(got32, want)
+    got16 = gpu_attention(w, q, k, v, gpu, fill_nan=True)
+    half_ulp = np.abs(want) * (2.0 ** -8 if dtype == 'bf16' else 2.0 ** -11)
+    assert np.all(np.abs(got16 - want) <= MAX_ABS + half_ulp)
+
+
+@pytest.mark.parametrize('dtype', ['f16', 'bf16'])
+def test_split_path_float32_output(gpu, dtype):
+    """Verify-shaped call (8 tokens, split-K + combine) with float32 output,
+    both input types, against the oracle to the full bounds."""
+    w = Workload('verify', 24, 4, 256, 8, 3000, 1 / 16, dtype, 77, 1.0, 0.5)
+    q, k, v, _ = make_inputs(w)
+    want = ref.gqa_attention(to_float(q, dtype), to_float(k, dtype), to_float(v, dtype), w.position, w.scale)
+    assert_parity(gpu_attention(w, q, k, v, gpu, fill_nan=True, out_dtype=gpu.float32), want)

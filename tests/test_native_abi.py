@@ -11,7 +11,7 @@ import subprocess
 
 import pytest
 
-from redshift_amd.runtime import DEFAULT_LIBRARY, QV_BF16, QV_F16
+from redshift_amd.runtime import DEFAULT_LIBRARY, QV_BF16, QV_F16, QV_F32
 
 from conftest import ROOT
 
@@ -36,9 +36,10 @@ int main(void) {
     int (*attention)(float *, void *, void *, const float *, const float *, const float *,
                      const float *, const float *, int, int, float) = qv_test_attention;
     int (*raw)(void *, const void *, const void *, const void *, int, int, int, int, int, int,
-               int, float, void *, uint64_t, void *) = qv_attention;
+               int, int, float, void *, uint64_t, void *) = qv_attention;
+    int out_types = QV_F16 + QV_BF16 + QV_F32;
     return error == 0 || mm == 0 || norm == 0 || verify == 0 || commit == 0 ||
-           attention == 0 || raw == 0;
+           attention == 0 || raw == 0 || out_types != 6;
 }
 '''
     path = tmp_path / 'abi.c'
@@ -125,12 +126,15 @@ def test_device_entry_points_validate_before_touching_the_device(lib):
     ws = ct.c_uint64(1 << 20)
     args = dict(q_heads=24, kv_heads=4, head_dim=256, tokens=1, position=4095, capacity=4096)
 
-    def call(dtype=QV_F16, scale=0.0625, out=p, **kw):
+    def call(dtype=QV_F16, out_dtype=None, scale=0.0625, out=p, **kw):
         a = {**args, **kw}
-        return lib.qv_attention(out, p, p, p, dtype, a['q_heads'], a['kv_heads'], a['head_dim'],
-                                a['tokens'], a['position'], a['capacity'], scale, p, ws, None)
+        return lib.qv_attention(out, p, p, p, dtype, dtype if out_dtype is None else out_dtype,
+                                a['q_heads'], a['kv_heads'], a['head_dim'], a['tokens'],
+                                a['position'], a['capacity'], scale, p, ws, None)
 
     assert call(dtype=7) == -1 and b'dtype' in lib.qv_error()
+    assert call(dtype=QV_F32) == -1 and b'dtype must be QV_F16 or QV_BF16' in lib.qv_error()
+    assert call(dtype=QV_F16, out_dtype=QV_BF16) == -1 and b'out_dtype' in lib.qv_error()
     assert call(q_heads=25) == -1 and b'multiple of kv_heads' in lib.qv_error()
     assert call(head_dim=64) == -1 and b'head_dim' in lib.qv_error()
     assert call(tokens=0) == -1 and b'tokens' in lib.qv_error()
