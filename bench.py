@@ -23,6 +23,9 @@ ROOT = Path(__file__).resolve().parent
 sys.path.insert(0, str(ROOT))
 
 METRIC = 'µs/layer + achieved HBM GB/s, GQA decode/verify-8 @16K and 139,264 ctx'
+# HBM bytes per launch of the decode kernel, from rocprofv3 FETCH_SIZE and
+# WRITE_SIZE passes scaled by a plain-copy calibration (see the file).
+TRAFFIC_FILE = ROOT / 'profiles' / 'attention_stream_decode_139k_traffic.txt'
 HBM_PEAK_GBS = 8000.0
 MFMA_BF16_PEAK = 2.5e15   # dense bf16 FLOP/s
 LAYERS = 16
@@ -119,30 +122,108 @@ def time_workload(torch, A, w, layers, steps, warmup, seed):
                 split_us=1000.0 * sum(split_ms) / len(split_ms))
 
 
-def cpu_baseline(w, target_s=10.0):
-    """Single-thread numpy fp32 restatement (oracle) on one layer's decode."""
+def measured_traffic():
+    """traffic_bytes_per_launch from the committed counter summary, or None."""
+    try:
+        for line in TRAFFIC_FILE.read_text().splitlines():
+            if line.startswith('traffic_bytes_per_launch'):
+                return int(line.split('=')[1])
+    except (OSError, ValueError, IndexError):
+        pass
+    return None
+
+
+def copy_probe(mib, repeats=5):
+    """A plain device copy of `mib` MiB, `repeats` times: the calibration
+    kernel for the FETCH_SIZE / WRITE_SIZE counters (bytes known exactly)."""
+    import torch
+    n = mib * (1 << 20) // 4
+    src = torch.ones(n, dtype=torch.float32, device='cuda')
+    dst = torch.empty_like(src)
+    for _ in range(repeats):
+        dst.copy_(src)
+    torch.cuda.synchronize()
+    log(f'copy probe: {repeats} x {mib} MiB device-to-device copies')
+
+
+def drop_in_rate(lib, cases=((1, 139263), (8, 16384), (1, 4095)), repeats=5):
+    """Times the host-buffer drop-in qv_test_attention (allocation, cache
+    upload and download, synchronisation included): the PCIe-inclusive rate,
+    reported beside the device-resident figures and never as `value`."""
+    import ctypes as ct
+
     import numpy as np
-    from threadpoolctl import threadpool_limits
+    H, HKV, D = 24, 4, 256
+    rows = []
+    for batch, position in cases:
+        rng = np.random.default_rng(0)
+        n = position + batch
+        kc = (rng.standard_normal((n, HKV, D)) * .5).astype(np.float16)
+        vc = (rng.standard_normal((n, HKV, D)) * .5).astype(np.float16)
+        qg = rng.standard_normal((batch, H, 2 * D)).astype(np.float32)
+        k = rng.standard_normal((batch, HKV, D)).astype(np.float32)
+        v = rng.standard_normal((batch, HKV, D)).astype(np.float32)
+        gamma = np.ones(D, np.float32)
+        out = np.empty((batch, H, D), np.float32)
+        ptrs = [a.ctypes.data_as(ct.c_void_p) for a in (out, kc, vc, qg, k, v, gamma, gamma)]
+        times = []
+        for i in range(repeats + 1):
+            t0 = time.perf_counter()
+            if lib.qv_test_attention(*ptrs, batch, position, ct.c_float(1e-6)) != 0:
+                raise RuntimeError(lib.qv_error().decode())
+            if i:
+                times.append(time.perf_counter() - t0)
+        sec = float(np.median(times))
+        cache = 2 * position * HKV * D * 2
+        rows.append({'batch': batch, 'position': position, 'ms': round(sec * 1e3, 2),
+                     'cache_GB/s': round(cache / sec / 1e9, 2)})
+    return rows
+
+
+def cpu_baseline(w, target_s=8.0):
+    """The numpy fp32 restatement of the reference's CPU attention (oracle),
+    one layer's decode, timed single-threaded and on all host cores (capped
+    at 16 threads): median of at least 5 calls, about target_s each."""
+    import numpy as np
+    from threadpoolctl import threadpool_info, threadpool_limits
 
     from oracle.attention_ref import gqa_attention_fp32
     from redshift_amd.workloads import make_inputs
 
     q, k, v, _ = make_inputs(w)
-    with threadpool_limits(limits=1):
-        gqa_attention_fp32(q, k, v, w.position, w.scale)  # warm-up
-        times = []
-        t_end = time.perf_counter() + target_s
-        while len(times) < 3 or time.perf_counter() < t_end:
-            t0 = time.perf_counter()
-            gqa_attention_fp32(q, k, v, w.position, w.scale)
-            times.append(time.perf_counter() - t0)
-    sec = float(np.median(times))
+    k32, v32 = k.astype(np.float32), v.astype(np.float32)
+
+    def run(threads):
+        with threadpool_limits(limits=threads):
+            gqa_attention_fp32(q, k32, v32, w.position, w.scale)   # warm-up
+            times = []
+            t_end = time.perf_counter() + target_s
+            while len(times) < 5 or time.perf_counter() < t_end:
+                t0 = time.perf_counter()
+                gqa_attention_fp32(q, k32, v32, w.position, w.scale)
+                times.append(time.perf_counter() - t0)
+        return float(np.median(times)), len(times)
+
+    host = len(os.sched_getaffinity(0))
+    threads = max(1, min(host, 16))
+    one, n_one = run(1)
+    many, n_many = run(threads)
+    model = 'unknown'
+    try:
+        model = next(line.split(':', 1)[1].strip() for line in open('/proc/cpuinfo')
+                     if line.startswith('model name'))
+    except (OSError, StopIteration):
+        pass
+    blas = next((f"{i['internal_api']} {i['version']}" for i in threadpool_info()
+                 if i.get('user_api') == 'blas'), 'unknown')
+    gbs = lambda sec: round(w.kv_bytes() / sec / 1e9, 3)
     return {
-        'value': round(w.kv_bytes() / sec / 1e9, 3), 'unit': 'GB/s', 'cores': 1, 'kind': 'port',
-        'us_per_layer': round(sec * 1e6, 1),
-        'sample': f'{len(times)} single-layer {w.name} calls ({w.keys} keys, 24/4/256, fp16 cache '
-                  f'widened to fp32, fp32 BLAS, 1 thread), median; host affinity '
-                  f'{len(os.sched_getaffinity(0))} cores',
+        'value': gbs(many), 'unit': 'GB/s', 'cores': threads, 'kind': 'port',
+        'us_per_layer': round(many * 1e6, 1),
+        'single_thread': {'value': gbs(one), 'unit': 'GB/s', 'cores': 1, 'us_per_layer': round(one * 1e6, 1)},
+        'sample': f'median of {n_many} ({threads} threads) and {n_one} (1 thread) single-layer {w.name} '
+                  f'calls: {w.keys} keys, 24/4/256, fp16 cache widened to fp32 before timing, fp32 BLAS '
+                  f'({blas}) per KV group; host {model}, {host} cores in affinity',
     }
 
 
@@ -154,6 +235,12 @@ def main():
     ap.add_argument('--layers', type=int, default=LAYERS)
     ap.add_argument('--no-cpu', action='store_true', help='skip the CPU baseline')
     ap.add_argument('--no-extra', action='store_true', help='skip the secondary workloads')
+    ap.add_argument('--extras', default='verify8_16k,decode_4k,prefill_2k',
+                    help='comma-separated secondary workloads to run')
+    ap.add_argument('--drop-in', action='store_true',
+                    help='only time the host-buffer qv_test_attention (PCIe-inclusive) and exit')
+    ap.add_argument('--copy-probe', type=int, metavar='MIB',
+                    help='only run a plain MIB-MiB device copy (counter calibration) and exit')
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get('WORLD_SIZE', '1')) != 1:
         print('bench.py measures one GPU only: the attention path runs on a single MI355X; '
@@ -166,9 +253,16 @@ def main():
     from redshift_amd.runtime import load_library
     from redshift_amd.workloads import WORKLOADS
 
-    load_library()
     assert torch.cuda.is_available(), 'bench.py needs a GPU'
     torch.cuda.set_device(0)
+    if args.copy_probe:
+        copy_probe(args.copy_probe)
+        return
+    lib = load_library()
+    if args.drop_in:
+        print(json.dumps({'drop_in': 'qv_test_attention, host buffers, median of 5 after 1 warm-up',
+                          'cases': drop_in_rate(lib)}), flush=True)
+        return
 
     w = WORKLOADS['decode_139k']
     log(f'decode_139k: {args.layers} layers x {w.keys} keys, steps={args.steps} warmup={args.warmup}')
@@ -190,15 +284,18 @@ def main():
                   'roofline kernel_us = split-K kernel alone, HIP events in an eager loop',
         'roofline': {'bound': 'hbm', 'kernel': 'attention_split (decode)',
                      'achieved': round(split_gbs, 1), 'peak': HBM_PEAK_GBS, 'unit': 'GB/s',
-                     'frac': round(split_gbs / HBM_PEAK_GBS, 4), 'traffic': None,
+                     'frac': round(split_gbs / HBM_PEAK_GBS, 4), 'traffic': measured_traffic(),
                      'kernel_us': round(r['split_us'], 2), 'bytes_per_launch': w.kv_bytes()},
     }
-    if not args.no_extra:
+    chosen = [] if args.no_extra else [x for x in args.extras.split(',') if x]
+    if chosen:
         extra = {}
-        for name, steps in (('verify8_16k', args.steps), ('decode_4k', args.steps)):
+        for name in ('verify8_16k', 'decode_4k'):
+            if name not in chosen:
+                continue
             wx = WORKLOADS[name]
             log(f'{name}: {args.layers} layers')
-            rx = time_workload(torch, A, wx, args.layers, steps, args.warmup, seed=1)
+            rx = time_workload(torch, A, wx, args.layers, args.steps, args.warmup, seed=1)
             us = 1000 * rx['ms_per_step'] / args.layers
             extra[name] = {'us_per_layer': round(us, 2),
                            'GB/s': round(wx.kv_bytes() / (us * 1e-6) / 1e9, 1),
@@ -206,15 +303,16 @@ def main():
                            'split_kernel_us': round(rx['split_us'], 2),
                            'split_kernel_GB/s': round(wx.kv_bytes() / (rx['split_us'] * 1e-6) / 1e9, 1),
                            'frac_hbm': round(wx.kv_bytes() / (us * 1e-6) / 1e9 / HBM_PEAK_GBS, 4)}
-        wp = WORKLOADS['prefill_2k']
-        log(f'prefill_2k: 4 layers')
-        rp = time_workload(torch, A, wp, 4, max(3, args.steps // 4), 2, seed=2)
-        kernel_s = rp['split_us'] * 1e-6
-        extra['prefill_2k'] = {'us_per_layer': round(1000 * rp['ms_per_step'] / 4, 1),
-                               'kernel_us': round(rp['split_us'], 1),
-                               'TFLOP/s': round(wp.flops() / kernel_s / 1e12, 1),
-                               'frac_mfma_peak': round(wp.flops() / kernel_s / MFMA_BF16_PEAK, 4),
-                               'flops_per_layer': wp.flops()}
+        if 'prefill_2k' in chosen:
+            wp = WORKLOADS['prefill_2k']
+            log('prefill_2k: 4 layers')
+            rp = time_workload(torch, A, wp, 4, max(3, args.steps // 4), 2, seed=2)
+            kernel_s = rp['split_us'] * 1e-6
+            extra['prefill_2k'] = {'us_per_layer': round(1000 * rp['ms_per_step'] / 4, 1),
+                                   'kernel_us': round(rp['split_us'], 1),
+                                   'TFLOP/s': round(wp.flops() / kernel_s / 1e12, 1),
+                                   'frac_mfma_peak': round(wp.flops() / kernel_s / MFMA_BF16_PEAK, 4),
+                                   'flops_per_layer': wp.flops()}
         result['extra'] = extra
     if not args.no_cpu:
         log('cpu baseline (numpy fp32, 1 thread, one layer)')

@@ -80,7 +80,11 @@ void qv_destroy(void *handle);
  * KV cache: per KV head a contiguous run of `capacity` tokens (a multiple of
  * 32) in 32-token pages laid out in matrix-core operand order; K and V are
  * separate allocations of qv_kv_bytes() bytes each. Element type is 16-bit
- * (fp16 or bf16, chosen by the caller per call).
+ * (fp16 or bf16, chosen by the caller per call). Element (token p, dim d)
+ * of KV head h sits at h*capacity*D plus
+ *   K: (p/32)*32*D + (p%32/16)*16*D + (d/8)*128 + (p%16)*8 + d%8
+ *   V: (p/32)*32*D + (d/16)*512 + ((p/4)%4)*128 + (d%16)*8 + (p%32/16)*4 + p%4
+ * (elements, not bytes); qv_kv_pack / qv_kv_unpack convert token-major rows.
  * Query row t (0-based) of a call at `position` sees keys 0..position+t.
  * ---------------------------------------------------------------------- */
 #define QV_F16 1

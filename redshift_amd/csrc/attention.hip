@@ -18,11 +18,12 @@
 //   attention_stream  one query tile (<= 16 rows, decode).  Every wave streams
 //                     its own run of pages with a private softmax state; the
 //                     four waves merge through LDS once at the end.
-//   attention_coop    up to four query tiles (<= 64 rows, verification).  The
-//                     four waves split each 64-key block by keys for Q.K^T and
-//                     by head dims for P.V, exchanging the block max and the P
-//                     fragments through LDS, so the 48-row accumulators are
-//                     spread over the waves instead of replicated.
+//   attention_coop    up to three query tiles (<= 48 rows, verification).
+//                     Eight waves split each 128-key block (four pages) by
+//                     keys for Q.K^T and by head dims for P.V, exchanging the
+//                     block max and the P fragments through LDS, so the 48-row
+//                     accumulators are spread over the waves instead of
+//                     replicated.
 #include "kernels.hpp"
 
 #include <algorithm>
