@@ -3,11 +3,12 @@
 A step is one token's attention over all 16 full-attention layers of the
 model (24 query heads, 4 KV heads, head_dim 256), each layer with its own
 fp16 KV cache of 139,264 tokens in HBM (64 keys per layer scaled x8): the
-decode at maximum context.  `value` is the achieved HBM bandwidth over the
-algorithmic K+V bytes (each key read once), whole step including the
-split-K combine; `roofline` is the split-K kernel alone, timed with HIP events
-on the stream it runs on.  Secondary workloads (speculative verify-8 on a
-16K prefix, decode at 4K) are reported under `extra`.
+decode at maximum context.  Each layer is two kernels: split-K over the
+pages, then the log-sum-exp combine.  `value` is the achieved HBM bandwidth
+over the algorithmic K+V bytes (each key read once) of the whole step
+replayed as a HIP graph; `roofline` is the split-K kernel alone, timed with
+HIP events on the stream it runs on.  Secondary workloads (speculative
+verify-8 on a 16K prefix, decode at 4K, chunked prefill) are under `extra`.
 
 The CPU baseline is the numpy fp32 restatement of the reference's CPU
 attention (oracle/attention_ref.py), run on this host on one layer's decode.
@@ -66,13 +67,16 @@ def time_workload(torch, A, w, layers, steps, warmup, seed):
 
     Returns dict(ms_per_step: one step replayed as a captured HIP graph,
     eager_ms_per_step: the same launches issued one by one, split_us: average
-    duration of the split-K kernel from events recorded around each of its
-    launches in the eager loop, on the stream it runs on)."""
+    duration of the split-K (or prefill) kernel from events recorded around
+    each of its launches in the eager loop, on the stream it runs on)."""
     caches, queries = make_layers(torch, A, w, layers, seed)
     ws = A.workspace(A.attention_workspace_bytes(w.q_heads, w.kv_heads, w.head_dim, w.tokens, w.position))
     outs = [torch.empty_like(q) for q in queries]
     one_chunk = w.tokens * w.group <= A.MAX_CHUNK_ROWS
 
+    # One layer: the split-K kernel then the combine kernel (the two launches
+    # qv_attention makes, issued through its two phases so that events can
+    # bracket the split kernel alone), or the prefill kernel.
     def step(events=None):
         for i in range(layers):
             if events is not None:
@@ -280,9 +284,9 @@ def main():
                    'layers': args.layers, 'kv_dtype': 'f16', 'outlier_keys': w.outliers},
         'us_per_layer': round(1000 * r['ms_per_step'] / args.layers, 2),
         'eager_us_per_layer': round(1000 * r['eager_ms_per_step'] / args.layers, 2),
-        'timing': 'step = 16 layers x (split-K kernel + combine) replayed as one HIP graph; '
+        'timing': 'step = 16 layers x (split-K kernel + combine kernel) replayed as one HIP graph; '
                   'roofline kernel_us = split-K kernel alone, HIP events in an eager loop',
-        'roofline': {'bound': 'hbm', 'kernel': 'attention_split (decode)',
+        'roofline': {'bound': 'hbm', 'kernel': 'attention_stream (decode split-K)',
                      'achieved': round(split_gbs, 1), 'peak': HBM_PEAK_GBS, 'unit': 'GB/s',
                      'frac': round(split_gbs / HBM_PEAK_GBS, 4), 'traffic': measured_traffic(),
                      'kernel_us': round(r['split_us'], 2), 'bytes_per_launch': w.kv_bytes()},

@@ -13,7 +13,7 @@ from pathlib import Path
 
 PACKAGE = Path(__file__).resolve().parent
 ROOT = PACKAGE.parent
-SOURCES = ['abi.cpp', 'attention.hip', 'kv.hip', 'prefill.hip']
+SOURCES = ['abi.cpp', 'attention.hip', 'kv.hip', 'prefill.hip', 'ring.hip']
 LIBRARY = PACKAGE / 'lib' / 'libredshift_hip.so'
 ARCH = 'gfx950'
 
@@ -25,6 +25,12 @@ COMMON_FLAGS = [
     '-Wall', '-Wno-unused-result',
     f'-I{ROOT / "include"}', f'-I{PACKAGE / "csrc"}',
 ]
+
+
+# Per-source flags.  ring.hip keeps MFMA accumulators in architectural VGPRs:
+# with AGPR accumulators the compiler copies all of them out and back on
+# every page.
+SOURCE_FLAGS = {'ring.hip': ['-mllvm', '-amdgpu-mfma-vgpr-form']}
 
 
 def hipcc():
@@ -56,7 +62,7 @@ def build(verbose=False, jobs=None):
     def compile_one(name):
         src = PACKAGE / 'csrc' / name
         obj = objdir / (name + '.o')
-        cmd = [compiler, '-x', 'hip', *COMMON_FLAGS, '-c', str(src), '-o', str(obj)]
+        cmd = [compiler, '-x', 'hip', *COMMON_FLAGS, *SOURCE_FLAGS.get(name, []), '-c', str(src), '-o', str(obj)]
         return obj, _run(cmd)
 
     with ThreadPoolExecutor(jobs) as pool:

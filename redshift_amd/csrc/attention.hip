@@ -24,6 +24,7 @@
 //                     block max and the P fragments through LDS, so the 48-row
 //                     accumulators are spread over the waves instead of
 //                     replicated.
+#include "combine.hpp"
 #include "kernels.hpp"
 
 #include <algorithm>
@@ -57,18 +58,6 @@ __device__ __forceinline__ f32x4 mfma(bf16x8 a, bf16x8 b, f32x4 c) {
 constexpr int kWaves = 4;          // waves per workgroup of the partial kernels
 constexpr int kMaxSplits = 1024;   // bound on workgroups per KV head
 constexpr int kCoopWaves = 8;      // waves per workgroup of attention_coop
-
-struct SplitArgs {
-    const void *q;        // [tokens][q_heads][D] 16-bit (hi part when QSPLIT)
-    const void *q_lo;     // QSPLIT: lo part, same layout
-    const void *k_pages;
-    const void *v_pages;
-    float *part_o;    // [kv_heads][splits][rows][D]   unnormalised, base-2 max m
-    float *part_ml;   // [kv_heads][splits][2][rows]   m (log2 domain), then l
-    size_t head_stride;
-    int q_heads, group, rows, position, n_keys, n_pages, splits;
-    float scale_log2;
-};
 
 // Query fragments (B operand of S^T): fragment (i, qt, ks) of lane l holds
 // row 16*qt + l%16, dims 32*ks + 8*(l/16) .. +7 of the hi (i = 0) or lo (i = 1,
@@ -138,7 +127,7 @@ void attention_stream(SplitArgs a) {
     __shared__ float sml[kWaves][2][16];
 
     const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
-    const int split = blockIdx.x, h = blockIdx.y;
+    const int split = blockIdx.x % a.splits, h = blockIdx.x / a.splits;
     QS qs;
     qs.issue(a, h, lane, w);
 
@@ -341,7 +330,7 @@ void attention_coop(SplitArgs a) {
     __shared__ float sl[WAVES][16 * NQT];         // row sums, exchanged once at the end
 
     const int lane = threadIdx.x & 63, w = threadIdx.x >> 6, g = lane >> 4;
-    const int split = blockIdx.x, h = blockIdx.y;
+    const int split = blockIdx.x % a.splits, h = blockIdx.x / a.splits;
 
     // Query fragments: wave w fetches fragments w, w+WAVES, ... and the
     // workgroup shares them through LDS.  This happens before any KV load:
@@ -558,91 +547,17 @@ void attention_coop(SplitArgs a) {
 struct CombineArgs {
     const float *part_o, *part_ml;
     void *out;
-    const float *gate;   // fused mode: q_gate rows of 2*D floats, gate at +D
+    const float *gate;   // gated output: q_gate rows of 2*D floats, gate at +D
     int q_heads, group, rows, splits;
 };
 
-// One workgroup (4 waves) per (row, KV head).  Lane l owns head dims
-// DV*l .. DV*l+DV-1 (DV = D/64); wave w takes splits w, w+4, w+8, ... and
-// issues the loads of up to kBatch of them (their m, l and partial row) at
-// once, so a combine over up to 4*kBatch splits costs one memory round trip.
-// The waves then agree on the row max and reduce through LDS.
-// OUT: kOutSame writes the KV type, kOutF32 fp32, kOutGated fp32 times
-// sigmoid(gate).
-enum { kOutSame = 0, kOutF32 = 1, kOutGated = 2 };
-
+// Standalone combine: one workgroup (4 waves) per (row, KV head).
 template <int D, typename KV, int OUT>
 __global__ __launch_bounds__(kWaves * kWave)
 void attention_combine(CombineArgs c) {
-    constexpr int DV = D / kWave;
-    constexpr int kBatch = 16;
-    __shared__ float wmax[kWaves];
-    __shared__ float part[kWaves][D + 1];
-    const int row = blockIdx.x, h = blockIdx.y, tid = threadIdx.x;
-    const int lane = tid & 63, w = tid >> 6;
-    const float *ml = c.part_ml + (size_t)h * c.splits * 2 * c.rows + row;
-    const float *po = c.part_o + ((size_t)h * c.splits * c.rows + row) * D + lane * DV;
-    const size_t stride = (size_t)c.rows * D;
-
-    float M = -INFINITY, L = 0.f, acc[DV] = {};
-    // Rounds of 4*kBatch splits (one round for up to 64 splits).
-    for (int s0 = 0; s0 < c.splits; s0 += kWaves * kBatch) {
-        float mv[kBatch], lv[kBatch], ov[kBatch][DV];
-#pragma unroll
-        for (int i = 0; i < kBatch; ++i) {
-            const int s = s0 + w + kWaves * i;
-            const bool ok = s < c.splits;
-            const int sc = ok ? s : 0;
-            mv[i] = ok ? ml[(size_t)sc * 2 * c.rows] : -INFINITY;
-            lv[i] = ok ? ml[(size_t)sc * 2 * c.rows + c.rows] : 0.f;
-#pragma unroll
-            for (int d = 0; d < DV; ++d) ov[i][d] = ok ? po[(size_t)sc * stride + d] : 0.f;
-        }
-        // Fold this round into the running (M, L, acc) of the wave.
-        float rm = M;
-#pragma unroll
-        for (int i = 0; i < kBatch; ++i) rm = fmaxf(rm, mv[i]);
-        const float mu = rm == -INFINITY ? 0.f : rm;
-        const float f = __builtin_amdgcn_exp2f(M - mu);
-        L *= f;
-#pragma unroll
-        for (int d = 0; d < DV; ++d) acc[d] *= f;
-#pragma unroll
-        for (int i = 0; i < kBatch; ++i) {
-            const float wgt = __builtin_amdgcn_exp2f(mv[i] - mu);
-            L += wgt * lv[i];
-#pragma unroll
-            for (int d = 0; d < DV; ++d) acc[d] += wgt * ov[i][d];
-        }
-        M = rm;
-    }
-    if (lane == 0) wmax[w] = M;
-    __syncthreads();
-    const float G = fmaxf(fmaxf(wmax[0], wmax[1]), fmaxf(wmax[2], wmax[3]));
-    const float gu = G == -INFINITY ? 0.f : G;
-    const float f = __builtin_amdgcn_exp2f(M - gu);
-#pragma unroll
-    for (int d = 0; d < DV; ++d) part[w][lane * DV + d] = acc[d] * f;
-    if (lane == 0) part[w][D] = L * f;
-    __syncthreads();
-    if (w == 0) {
-        const float Lt = part[0][D] + part[1][D] + part[2][D] + part[3][D];
-        const int t = row / c.group, hq = h * c.group + (row - t * c.group);
-        const size_t idx = ((size_t)t * c.q_heads + hq) * D + lane * DV;
-#pragma unroll
-        for (int d = 0; d < DV; ++d) {
-            const int j = lane * DV + d;
-            const float o = (part[0][j] + part[1][j] + part[2][j] + part[3][j]) / Lt;
-            if constexpr (OUT == kOutGated) {
-                const float gv = c.gate[((size_t)t * c.q_heads + hq) * 2 * D + D + j];
-                static_cast<float *>(c.out)[idx + d] = o * (1.f / (1.f + expf(-gv)));
-            } else if constexpr (OUT == kOutF32) {
-                static_cast<float *>(c.out)[idx + d] = o;
-            } else {
-                static_cast<KV *>(c.out)[idx + d] = (KV)o;
-            }
-        }
-    }
+    __shared__ float scratch[4 * (D + 1) + 4];
+    combine_row<D, KV>(c.part_o, c.part_ml, c.splits, c.rows, c.group, c.q_heads, blockIdx.x, blockIdx.y,
+                       true, threadIdx.x >> 6, threadIdx.x & 63, scratch, c.out, c.gate, OUT);
 }
 
 // Kernel instance for a plan.  Raw fp16: 16-bit P; raw bf16: hi+lo P (bf16's
@@ -669,6 +584,11 @@ const void *combine_kernel(Dtype dtype, bool out_f32, bool gated) {
 }
 
 const void *split_kernel(const SplitPlan &p, int D, Dtype dtype, bool precise) {
+    if (p.kind == SplitKind::Ring) {
+        const void *k = ring_kernel(D, p.nqt, dtype, precise);
+        require(k != nullptr, "unsupported head_dim / query rows for the ring kernel");
+        return k;
+    }
     const bool stream = p.kind == SplitKind::Stream;
     if (D == 256) {
         switch (p.nqt) {
@@ -686,13 +606,28 @@ const void *split_kernel(const SplitPlan &p, int D, Dtype dtype, bool precise) {
     throw std::invalid_argument("unsupported head_dim / query rows for the split kernel");
 }
 
-// Decode kernel choice: the streaming kernel unless RS_DECODE_KERNEL=coop.
-bool decode_uses_coop() {
-    static const bool coop = [] {
-        const char *v = std::getenv("RS_DECODE_KERNEL");
-        return v && std::strcmp(v, "coop") == 0;
+// Kernel of a plan: one query tile (decode) runs attention_stream, more run
+// attention_ring (16-bit queries) or attention_coop (fp32 queries).
+// RS_DECODE_KERNEL=coop|ring and RS_VERIFY_KERNEL=coop pick the alternatives
+// (for measurement).
+SplitKind env_kind(const char *name, SplitKind fallback) {
+    const char *v = std::getenv(name);
+    if (v && std::strcmp(v, "coop") == 0) return SplitKind::Coop;
+    if (v && std::strcmp(v, "ring") == 0) return SplitKind::Ring;
+    if (v && std::strcmp(v, "stream") == 0) return SplitKind::Stream;
+    return fallback;
+}
+
+SplitKind kind_for(int nqt, bool precise) {
+    static const SplitKind decode = env_kind("RS_DECODE_KERNEL", SplitKind::Stream);
+    static const SplitKind verify = [] {
+        const SplitKind k = env_kind("RS_VERIFY_KERNEL", SplitKind::Ring);
+        return k == SplitKind::Stream ? SplitKind::Ring : k;
     }();
-    return coop;
+    const SplitKind k = nqt == 1 ? decode : verify;
+    // The ring kernel takes 16-bit queries only; fp32 (hi + lo) queries of
+    // several tiles use attention_coop.
+    return precise && k == SplitKind::Ring ? (nqt == 1 ? SplitKind::Stream : SplitKind::Coop) : k;
 }
 
 }  // namespace
@@ -715,7 +650,9 @@ int device_cu_count() {
 int chunk_tokens(const Shape &s) { return std::max(1, kMaxRows / s.group()); }
 
 int block_threads(const SplitPlan &p) {
-    return (p.kind == SplitKind::Coop ? kCoopWaves : kWaves) * kWave;
+    return p.kind == SplitKind::Stream ? kWaves * kWave
+         : p.kind == SplitKind::Coop   ? kCoopWaves * kWave
+                                       : kRingThreads;
 }
 
 // Resident workgroups per CU of a kernel instance (cached per device).
@@ -738,7 +675,7 @@ SplitPlan plan_split(const Shape &s, int tokens, Dtype dtype, bool precise) {
     SplitPlan p;
     p.rows = s.group() * tokens;
     p.nqt = (p.rows + 15) / 16;
-    p.kind = (p.nqt == 1 && !decode_uses_coop()) ? SplitKind::Stream : SplitKind::Coop;
+    p.kind = kind_for(p.nqt, precise);
     const long long n_keys = (long long)s.position + tokens;
     p.n_pages = (int)((n_keys + kPageTokens - 1) / kPageTokens);
     p.splits = 1;
@@ -786,6 +723,7 @@ void launch_split(const Shape &s, const SplitPlan &plan, Dtype dtype, bool preci
     a.part_ml = a.part_o + (size_t)s.kv_heads * plan.splits * plan.rows * s.head_dim;
     a.head_stride = (size_t)s.capacity * s.head_dim;
     a.q_heads = s.q_heads;
+    a.kv_heads = s.kv_heads;
     a.group = s.group();
     a.rows = plan.rows;
     a.position = s.position;
@@ -795,7 +733,8 @@ void launch_split(const Shape &s, const SplitPlan &plan, Dtype dtype, bool preci
     a.scale_log2 = scale * 1.4426950408889634f;
     const void *kernel = split_kernel(plan, s.head_dim, dtype, precise);
     void *args[] = {&a};
-    check(hipLaunchKernel(kernel, dim3(plan.splits, s.kv_heads), dim3(block_threads(plan)),
+    // One-dimensional grid: workgroup id = KV head * splits + split.
+    check(hipLaunchKernel(kernel, dim3(plan.splits * s.kv_heads), dim3(block_threads(plan)),
                           args, 0, stream));
 }
 

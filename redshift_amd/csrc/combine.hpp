@@ -1,0 +1,106 @@
+// Log-sum-exp combine of split-K partials (the per-row work of the combine
+// kernel).
+#pragma once
+#include "kernels.hpp"
+
+#include <cmath>
+
+namespace rs {
+
+// Output of a combine: kOutSame writes the KV type, kOutF32 fp32, kOutGated
+// fp32 times sigmoid(gate), gate being q_gate[t][h][D + d] (row stride 2D).
+enum { kOutSame = 0, kOutF32 = 1, kOutGated = 2 };
+
+// One row of one KV head, combined by the four waves w4 = 0..3 of a
+// workgroup (every wave must call it, `valid` or not: it holds two workgroup
+// barriers).  Lane l owns head dims DV*l .. DV*l+DV-1 (DV = D/64);
+// wave w4 takes splits w4, w4+4, ... and issues the loads of up to kBatch of
+// them (their m, l and partial row) at once, so a combine over up to
+// 4*kBatch splits costs one memory round trip.  The waves then agree on the
+// row max and reduce through `scratch` (4*(D+1) + 4 floats of LDS per group).
+template <int D, typename KV>
+__device__ __forceinline__ void combine_row(const float *part_o, const float *part_ml, int splits,
+                                            int rows, int group, int q_heads, int row, int h,
+                                            bool valid, int w4, int lane, float *scratch,
+                                            void *out, const float *gate, int out_mode) {
+    constexpr int DV = D / kWave;
+    constexpr int kBatch = 16;
+    float *part = scratch;                   // [4][D + 1]
+    float *wmax = scratch + 4 * (D + 1);     // [4]
+    const int rc = valid ? row : rows - 1;   // in-bounds reads for a padding group
+    const float *ml = part_ml + (size_t)h * splits * 2 * rows + rc;
+    const float *po = part_o + ((size_t)h * splits * rows + rc) * D + lane * DV;
+    const size_t stride = (size_t)rows * D;
+
+    float M = -INFINITY, L = 0.f, acc[DV] = {};
+    // Rounds of 4*kBatch splits (one round for up to 64 splits).
+    for (int s0 = 0; s0 < splits; s0 += 4 * kBatch) {
+        // Every load is issued unconditionally (splits past the end re-read
+        // the last one) so that all of them are in flight together; the
+        // surplus ones are discarded afterwards.
+        typedef float OV __attribute__((ext_vector_type(DV)));
+        float mv[kBatch], lv[kBatch];
+        OV ov[kBatch];
+#pragma unroll
+        for (int i = 0; i < kBatch; ++i) {
+            const int sc = min(s0 + w4 + 4 * i, splits - 1);
+            mv[i] = ml[(size_t)sc * 2 * rows];
+            lv[i] = ml[(size_t)sc * 2 * rows + rows];
+            ov[i] = *reinterpret_cast<const OV *>(po + (size_t)sc * stride);
+        }
+#pragma unroll
+        for (int i = 0; i < kBatch; ++i) {
+            if (s0 + w4 + 4 * i >= splits) {
+                mv[i] = -INFINITY;
+                lv[i] = 0.f;
+                ov[i] = OV{};
+            }
+        }
+        // Fold this round into the running (M, L, acc) of the wave.
+        float rm = M;
+#pragma unroll
+        for (int i = 0; i < kBatch; ++i) rm = fmaxf(rm, mv[i]);
+        const float mu = rm == -INFINITY ? 0.f : rm;
+        const float f = __builtin_amdgcn_exp2f(M - mu);
+        L *= f;
+#pragma unroll
+        for (int d = 0; d < DV; ++d) acc[d] *= f;
+#pragma unroll
+        for (int i = 0; i < kBatch; ++i) {
+            const float wgt = __builtin_amdgcn_exp2f(mv[i] - mu);
+            L += wgt * lv[i];
+#pragma unroll
+            for (int d = 0; d < DV; ++d) acc[d] += wgt * ov[i][d];
+        }
+        M = rm;
+    }
+    if (lane == 0) wmax[w4] = M;
+    __syncthreads();
+    const float G = fmaxf(fmaxf(wmax[0], wmax[1]), fmaxf(wmax[2], wmax[3]));
+    const float gu = G == -INFINITY ? 0.f : G;
+    const float f = __builtin_amdgcn_exp2f(M - gu);
+#pragma unroll
+    for (int d = 0; d < DV; ++d) part[w4 * (D + 1) + lane * DV + d] = acc[d] * f;
+    if (lane == 0) part[w4 * (D + 1) + D] = L * f;
+    __syncthreads();
+    if (w4 == 0 && valid) {
+        const float Lt = part[D] + part[(D + 1) + D] + part[2 * (D + 1) + D] + part[3 * (D + 1) + D];
+        const int t = row / group, hq = h * group + (row - t * group);
+        const size_t idx = ((size_t)t * q_heads + hq) * D + lane * DV;
+#pragma unroll
+        for (int d = 0; d < DV; ++d) {
+            const int j = lane * DV + d;
+            const float o = (part[j] + part[(D + 1) + j] + part[2 * (D + 1) + j] + part[3 * (D + 1) + j]) / Lt;
+            if (out_mode == kOutGated) {
+                const float gv = gate[((size_t)t * q_heads + hq) * 2 * D + D + j];
+                static_cast<float *>(out)[idx + d] = o * (1.f / (1.f + expf(-gv)));
+            } else if (out_mode == kOutF32) {
+                static_cast<float *>(out)[idx + d] = o;
+            } else {
+                static_cast<KV *>(out)[idx + d] = (KV)o;
+            }
+        }
+    }
+}
+
+}  // namespace rs

@@ -15,11 +15,30 @@ struct Shape {
     int n_keys() const { return position + tokens; }
 };
 
-enum class SplitKind { Stream, Coop };
+enum class SplitKind { Stream, Coop, Ring };
+
+// Arguments of every split-K partial kernel.
+struct SplitArgs {
+    const void *q;        // [tokens][q_heads][D] 16-bit (hi part when QSPLIT)
+    const void *q_lo;     // QSPLIT: lo part, same layout
+    const void *k_pages;
+    const void *v_pages;
+    float *part_o;    // [kv_heads][splits][rows][D]   unnormalised, base-2 max m
+    float *part_ml;   // [kv_heads][splits][2][rows]   m (log2 domain), then l
+    size_t head_stride;
+    int q_heads, kv_heads, group, rows, position, n_keys, n_pages, splits;
+    float scale_log2;
+};
+
+// attention_ring instance (ring.hip) for head_dim D and nqt query tiles
+// (1..4), or nullptr for fp32 (precise) queries.  It takes kRingThreads
+// threads and SplitArgs.
+constexpr int kRingThreads = 512;
+const void *ring_kernel(int D, int nqt, Dtype dtype, bool precise);
 
 // The split-K decomposition chosen for one launch of the partial kernel.
 struct SplitPlan {
-    SplitKind kind;  // attention_stream (one query tile) or attention_coop
+    SplitKind kind;  // attention_stream (one query tile), attention_coop or attention_ring
     int nqt;         // 16-row query tiles per KV head (rows = group * tokens)
     int rows;        // valid query rows per KV head
     int n_pages;     // 32-key pages per KV head holding keys 0..n_keys-1

@@ -301,3 +301,49 @@ def test_split_path_float32_output(gpu, dtype):
     q, k, v, _ = make_inputs(w)
     want = ref.gqa_attention(to_float(q, dtype), to_float(k, dtype), to_float(v, dtype), w.position, w.scale)
     assert_parity(gpu_attention(w, q, k, v, gpu, fill_nan=True, out_dtype=gpu.float32), want)
+
+
+@pytest.mark.parametrize('q_heads,kv_heads,head_dim,T,position,dtype', [
+    (24, 4, 256, 8, 0, 'f16'),       # one page, one split
+    (24, 4, 256, 3, 40, 'bf16'),     # 18 rows, two pages
+    (24, 4, 256, 8, 70, 'f16'),      # three pages
+    (24, 4, 256, 8, 16384, 'bf16'),  # the verify shape in bf16
+    (16, 4, 128, 8, 1000, 'f16'),    # head_dim 128, 32 rows
+    (16, 2, 128, 6, 777, 'bf16'),    # head_dim 128, 48 rows
+    (24, 1, 256, 1, 5000, 'f16'),    # 24 rows of one token
+])
+def test_multi_tile_split_kernel(gpu, q_heads, kv_heads, head_dim, T, position, dtype):
+    """17..48 query rows per KV head (several 16-row tiles) go through the
+    paged split kernel and the combine; pages past the last key hold NaN."""
+    w = Workload('tiles', q_heads, kv_heads, head_dim, T, position, 1 / head_dim ** .5, dtype, 500 + T, 1.0, 0.5)
+    q, k, v, _ = make_inputs(w)
+    want = ref.gqa_attention(to_float(q, dtype), to_float(k, dtype), to_float(v, dtype), position, w.scale)
+    assert_parity(gpu_attention(w, q, k, v, gpu, fill_nan=True, out_dtype=gpu.float32), want)
+
+
+def test_one_workspace_across_shapes_and_phases(gpu):
+    """One workspace serves calls of different shapes in a row (different
+    split counts, KV-head counts and head dims), repeatedly; the two-phase
+    entry points (split, then combine) give exactly qv_attention's result."""
+    cases = [Workload('a', 24, 4, 256, 1, 9000, 1 / 16, 'f16', 11, 1.0, 0.5),
+             Workload('b', 24, 4, 256, 8, 3000, 1 / 16, 'f16', 12, 1.0, 0.5),
+             Workload('c', 16, 2, 128, 3, 700, 1 / 128 ** .5, 'bf16', 13, 1.0, 0.5)]
+    ws = A.workspace(max(A.attention_workspace_bytes(w.q_heads, w.kv_heads, w.head_dim, w.tokens, w.position)
+                         for w in cases))
+    prepared = []
+    for w in cases:
+        q, k, v, _ = make_inputs(w)
+        want = ref.gqa_attention(to_float(q, w.dtype), to_float(k, w.dtype), to_float(v, w.dtype), w.position, w.scale)
+        prepared.append((w, to_torch(q, w.dtype, gpu), make_cache(k, v, w, gpu, fill_nan=True), want))
+    for _ in range(3):
+        for w, qt, cache, want in prepared:
+            out = A.attention(qt, cache, w.position, w.scale, ws=ws, out_dtype=gpu.float32)
+            gpu.cuda.synchronize()
+            assert_parity(out.cpu().numpy().astype(np.float64), want)
+    for w, qt, cache, want in prepared[:2]:
+        out = gpu.empty((w.tokens, w.q_heads, w.head_dim), dtype=gpu.float16, device='cuda')
+        A.attention_split(qt, cache, w.position, w.scale, ws)
+        A.attention_combine(out, cache, w.position, ws)
+        fused = A.attention(qt, cache, w.position, w.scale, ws=ws)
+        gpu.cuda.synchronize()
+        np.testing.assert_array_equal(out.cpu().numpy(), fused.cpu().numpy())
