@@ -103,6 +103,17 @@ int qv_kv_unpack(void *k_rows, void *v_rows, const void *k_pages, const void *v_
                  int kv_heads, int head_dim, int capacity, int first, int count,
                  void *stream);
 
+/* Checkpoint / restore of the valid prefix (the reference's copy_state for
+ * the full-attention layers, src/runtime.cu:455-485, which copies
+ * prefix*kv_heads*head_dim fp16 values of each cache): copies the pages that
+ * hold tokens 0..tokens-1 of every KV head, K and V, from caches of
+ * src_capacity tokens to caches of dst_capacity tokens (whole pages, so up to
+ * 31 tokens past the prefix come along; they are unreachable, as in the
+ * reference). A snapshot needs capacity tokens rounded up to 32 only. */
+int qv_kv_copy(void *dst_k, void *dst_v, const void *src_k, const void *src_v,
+               int kv_heads, int head_dim, int dst_capacity, int src_capacity, int tokens,
+               void *stream);
+
 /* Workspace bytes that qv_attention needs for this shape on the current
  * device (split-K partials). */
 int qv_attention_workspace(uint64_t *bytes, int q_heads, int kv_heads, int head_dim,

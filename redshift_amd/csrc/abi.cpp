@@ -284,6 +284,24 @@ extern "C" int qv_kv_unpack(void *k_rows, void *v_rows, const void *k_pages, con
     });
 }
 
+extern "C" int qv_kv_copy(void *dst_k, void *dst_v, const void *src_k, const void *src_v,
+                          int kv_heads, int head_dim, int dst_capacity, int src_capacity, int tokens,
+                          void *stream) {
+    return call([&] {
+        geometry(kv_heads, head_dim, dst_capacity);
+        geometry(kv_heads, head_dim, src_capacity);
+        require(tokens >= 0, "tokens must be non-negative");
+        const int pages = (tokens + rs::kPageTokens - 1) / rs::kPageTokens;
+        require((long long)pages * rs::kPageTokens <= std::min(dst_capacity, src_capacity),
+                "the pages of tokens exceed a cache capacity");
+        require(dst_k && dst_v && src_k && src_v, "null KV cache");
+        require(aligned16(dst_k) && aligned16(dst_v) && aligned16(src_k) && aligned16(src_v),
+                "KV caches must be 16-byte aligned");
+        rs::launch_copy(dst_k, dst_v, src_k, src_v, kv_heads, head_dim, dst_capacity, src_capacity, pages,
+                        static_cast<hipStream_t>(stream));
+    });
+}
+
 extern "C" int qv_attention_workspace(uint64_t *bytes, int q_heads, int kv_heads, int head_dim,
                                       int tokens, int position) {
     return call([&] {

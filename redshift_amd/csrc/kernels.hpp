@@ -77,6 +77,11 @@ void launch_combine(const Shape &s, const SplitPlan &plan, Dtype dtype,
 void launch_prefill(const Shape &s, Dtype dtype, float scale, const void *q, const void *k_pages,
                     const void *v_pages, void *out, bool out_f32, hipStream_t stream);
 
+// Whole pages 0 .. pages-1 of every KV head, K and V, from caches of
+// src_capacity tokens to caches of dst_capacity tokens (checkpoint/restore).
+void launch_copy(void *dst_k, void *dst_v, const void *src_k, const void *src_v, int kv_heads,
+                 int head_dim, int dst_capacity, int src_capacity, int pages, hipStream_t stream);
+
 // Token-major rows [count][kv_heads][D] <-> pages, for tokens first..first+count.
 void launch_pack(void *k_pages, void *v_pages, const void *k_rows, const void *v_rows,
                  int kv_heads, int head_dim, int capacity, int first, int count,

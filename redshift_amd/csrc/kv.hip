@@ -101,7 +101,37 @@ void prepare_kernel(_Float16 *q_hilo, _Float16 *k_pages, _Float16 *v_pages, cons
     }
 }
 
+// Copy of whole pages: for every KV head, elements [0, n) of its run (the
+// pages of tokens 0 .. n/D-1) from a cache of stride src_stride to one of
+// stride dst_stride, 16 bytes per lane.
+__global__ __launch_bounds__(256)
+void copy_pages(uint4 *dst, const uint4 *src, size_t dst_stride, size_t src_stride, size_t n,
+                int kv_heads) {
+    const size_t per_head = n / 8;   // uint4 per head
+    const size_t total = per_head * kv_heads;
+    for (size_t e = (size_t)blockIdx.x * blockDim.x + threadIdx.x; e < total;
+         e += (size_t)gridDim.x * blockDim.x) {
+        const size_t h = e / per_head, i = e - h * per_head;
+        dst[h * (dst_stride / 8) + i] = src[h * (src_stride / 8) + i];
+    }
+}
+
 }  // namespace
+
+void launch_copy(void *dst_k, void *dst_v, const void *src_k, const void *src_v, int kv_heads,
+                 int head_dim, int dst_capacity, int src_capacity, int pages, hipStream_t stream) {
+    const size_t n = (size_t)pages * kPageTokens * head_dim;   // 16-bit elements per head
+    if (!n) return;
+    const size_t total = n / 8 * kv_heads;
+    const unsigned blocks = (unsigned)std::min<size_t>((total + 255) / 256, 4096);
+    const size_t ds = (size_t)dst_capacity * head_dim, ss = (size_t)src_capacity * head_dim;
+    hipLaunchKernelGGL(copy_pages, dim3(blocks), dim3(256), 0, stream, static_cast<uint4 *>(dst_k),
+                       static_cast<const uint4 *>(src_k), ds, ss, n, kv_heads);
+    check(hipGetLastError());
+    hipLaunchKernelGGL(copy_pages, dim3(blocks), dim3(256), 0, stream, static_cast<uint4 *>(dst_v),
+                       static_cast<const uint4 *>(src_v), ds, ss, n, kv_heads);
+    check(hipGetLastError());
+}
 
 void launch_pack(void *k_pages, void *v_pages, const void *k_rows, const void *v_rows,
                  int kv_heads, int head_dim, int capacity, int first, int count,

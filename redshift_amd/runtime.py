@@ -41,6 +41,7 @@ DEVICE_SIGNATURES = {
     'qv_kv_bytes': [ct.POINTER(_U64), _I, _I, _I],
     'qv_kv_pack': [_P] * 4 + [_I] * 5 + [_P],
     'qv_kv_unpack': [_P] * 4 + [_I] * 5 + [_P],
+    'qv_kv_copy': [_P] * 4 + [_I] * 5 + [_P],
     'qv_attention_workspace': [ct.POINTER(_U64)] + [_I] * 5,
     'qv_attention': [_P] * 4 + [_I] * 8 + [_F, _P, _U64, _P],
     'qv_attention_split': [_P] * 3 + [_I] * 7 + [_F, _P, _U64, _P],

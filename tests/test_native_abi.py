@@ -147,5 +147,13 @@ def test_device_entry_points_validate_before_touching_the_device(lib):
     assert lib.qv_kv_pack(p, p, p, p, 4, 256, 128, 100, 29, None) == -1
     assert b'capacity' in lib.qv_error()
     assert lib.qv_kv_pack(p, None, None, p, 4, 256, 128, 0, 1, None) == -1
+    assert lib.qv_kv_copy(p, p, p, p, 4, 256, 64, 4096, 65, None) == -1
+    assert b'capacity' in lib.qv_error()
+    assert lib.qv_kv_copy(p, p, p, p, 4, 256, 100, 4096, 10, None) == -1
+    assert b'multiple of 32' in lib.qv_error()
+    assert lib.qv_kv_copy(p, None, p, p, 4, 256, 64, 4096, 10, None) == -1
+    assert lib.qv_error() == b'null KV cache'
+    assert lib.qv_kv_copy(p, p, p, p, 4, 256, 64, 4096, -1, None) == -1
+    assert b'non-negative' in lib.qv_error()
     assert lib.qv_attention_fused(*([p] * 8), 9, 0, 128, 1e-6, p, ws, None) == -1
     assert lib.qv_error() == b'batch must be between 1 and 8'
