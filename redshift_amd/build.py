@@ -27,10 +27,10 @@ COMMON_FLAGS = [
 ]
 
 
-# Per-source flags.  ring.hip keeps MFMA accumulators in architectural VGPRs:
-# with AGPR accumulators the compiler copies all of them out and back on
-# every page.
-SOURCE_FLAGS = {'ring.hip': ['-mllvm', '-amdgpu-mfma-vgpr-form']}
+# Per-source flags.  ring.hip and prefill.hip keep MFMA accumulators in
+# architectural VGPRs: with AGPR accumulators the compiler copies them out
+# and back on every page (for the rarely taken softmax rescale).
+SOURCE_FLAGS = {name: ['-mllvm', '-amdgpu-mfma-vgpr-form'] for name in ('ring.hip', 'prefill.hip')}
 
 
 def hipcc():

@@ -1,0 +1,86 @@
+// Device helpers of the kernels that stream KV pages through LDS with
+// direct global->LDS loads (ring.hip, prefill.hip).
+#pragma once
+#include "common.hpp"
+
+#include <cstdint>
+#include <type_traits>
+
+namespace rs {
+
+// s_waitcnt vmcnt(N) leaving the other counters alone (gfx9 encoding:
+// vmcnt bits 3:0 and 15:14, expcnt 6:4, lgkmcnt 11:8).
+template <int N>
+__device__ __forceinline__ void wait_vmcnt() {
+    static_assert(N >= 0 && N < 64, "vmcnt range");
+    __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | (7 << 4) | (15 << 8));
+}
+
+// LDS byte address of a __shared__ object.
+__device__ __forceinline__ uint32_t lds_addr(const void *p) {
+    return (uint32_t)(uintptr_t)(__attribute__((address_space(3))) const void *)p;
+}
+
+// Compile-time loop: f(std::integral_constant<int, I>) for I in [B, E).
+template <int B, int E, typename F>
+__device__ __forceinline__ void static_for(F &&f) {
+    if constexpr (B < E) {
+        f(std::integral_constant<int, B>{});
+        static_for<B + 1, E>(f);
+    }
+}
+
+// LDS reads of page fragments at addr + OFF, issued as written.  They bypass
+// the compiler's own wait insertion, which cannot tell the ring buffers'
+// direct loads apart for every buffer and would drain the whole ring before
+// some reads; their completion is awaited explicitly with lds_wait.
+template <int OFF, typename V>
+__device__ __forceinline__ void lds_read(V &v, uint32_t addr) {
+    static_assert(OFF >= 0 && OFF < 65536, "ds_read offset range");
+    if constexpr (sizeof(V) == 16)
+        asm volatile("ds_read_b128 %0, %1 offset:%2" : "=v"(v) : "v"(addr), "i"(OFF));
+    else
+        asm volatile("ds_read_b64 %0, %1 offset:%2" : "=v"(v) : "v"(addr), "i"(OFF));
+}
+// LDS reads in flight are counted by lgkmcnt, a 4-bit counter: a wave never
+// has more than 15 of them outstanding, so every wait count below is exact.
+constexpr int kMaxLdsInFlight = 15;
+
+// s_waitcnt lgkmcnt(N), after which v (read by lds_read) may be used.
+template <int N, typename V>
+__device__ __forceinline__ void lds_wait(V &v) {
+    static_assert(N >= 0 && N < 16, "lgkmcnt range");
+    asm volatile("s_waitcnt lgkmcnt(%1)" : "+v"(v) : "i"(N));
+}
+
+// Marks a rarely taken branch body as having side effects, so the compiler
+// keeps the branch instead of executing the body on every page as selects.
+__device__ __forceinline__ void keep_branch() { asm volatile(""); }
+
+// Workgroup barrier for the page ring.  A workgroup-scope fence would also
+// wait for every direct global->LDS load in flight (they count as LDS
+// writes), draining the ring; instead each wave waits explicitly for the
+// loads and LDS reads that the barrier hands over, and the empty asm
+// statements keep the compiler from moving memory accesses across it.
+__device__ __forceinline__ void ring_barrier() {
+    asm volatile("" ::: "memory");
+    __builtin_amdgcn_s_barrier();
+    asm volatile("" ::: "memory");
+}
+
+// Maximum (sum) over the four 16-lane rows of the wave: lanes l, l^16, l^32
+// and l^48, exchanged with the lane-swap instructions instead of LDS.
+__device__ __forceinline__ float row_group_max(float x) {
+    const auto a = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+    const float y = fmaxf(__uint_as_float(a[0]), __uint_as_float(a[1]));
+    const auto b = __builtin_amdgcn_permlane16_swap(__float_as_uint(y), __float_as_uint(y), false, false);
+    return fmaxf(__uint_as_float(b[0]), __uint_as_float(b[1]));
+}
+__device__ __forceinline__ float row_group_sum(float x) {
+    const auto a = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+    const float y = __uint_as_float(a[0]) + __uint_as_float(a[1]);
+    const auto b = __builtin_amdgcn_permlane16_swap(__float_as_uint(y), __float_as_uint(y), false, false);
+    return __uint_as_float(b[0]) + __uint_as_float(b[1]);
+}
+
+}  // namespace rs

@@ -6,23 +6,27 @@
 //
 // One workgroup (4 waves) owns 128 query rows of one KV head (row = token *
 // group + query head within the group); wave w owns rows 32w..32w+31 as two
-// 16-row tiles whose fragments stay in registers.  The workgroup walks the
-// pages that its last row can see.  Each page (K then V, 32 keys, 32*D
-// elements each) is copied verbatim into LDS with direct global->LDS loads,
-// double buffered: since pages are stored in MFMA operand order, every wave
-// then reads its A operands as conflict-free 16-byte LDS fragments.
+// 16-row tiles whose query fragments stay in registers.  The workgroup walks
+// the pages that its last row can see through a ring of four LDS buffers
+// ([K page | V page], 32 KiB at D=256) filled by direct global->LDS loads,
+// three pages ahead.  Since pages are stored in MFMA operand order, every
+// wave reads its A operands as conflict-free 16-byte LDS fragments, each one
+// feeding both of its tiles:
 //   S^T[key][row] = K[key][:] . Q[row][:]     (A = K tile from LDS, B = Q)
 //   O^T[dim][row] += V^T[dim][key] P^T[key][row]  (A = V^T from LDS, B = P^T,
 //                                                  straight from S^T's C layout)
-// Online softmax in base 2 with a lazily moved row max (see attention.hip).
-// bf16 caches multiply by P split into hi + lo bf16 parts, fp16 caches by a
-// single fp16 P.
+// A page's 16 K fragments are requested at once and consumed as they arrive
+// (four independent accumulation chains), and its V fragments are requested
+// while the softmax runs.  Online softmax in base 2 with a lazily moved row
+// max (see ring.hip).  bf16 caches multiply by P split into hi + lo bf16
+// parts, fp16 caches by a single fp16 P.
 //
 // Scheduling: workgroup i serves KV head i % kv_heads (with 4 KV heads the
 // round-robin dispatch over the 8 XCDs keeps every head on the same two XCDs,
 // whose L2s then hold that head's pages for all of its workgroups), and row
 // tiles go heaviest (latest rows, most keys) first.
 #include "kernels.hpp"
+#include "lds.hpp"
 
 #include <algorithm>
 #include <cmath>
@@ -67,12 +71,12 @@ void attention_prefill(PrefillArgs a) {
     constexpr int KS = D / 32, DT = D / 16, RT = kRowsPerWave / 16;
     constexpr int PAGE = 32 * D;                       // elements of one K (or V) page
     constexpr int CHUNKS = 2 * PAGE * 2 / 1024;        // 1 KiB chunks of K + V page
-    constexpr int CPW = CHUNKS / kPWaves;              // chunks per wave
+    constexpr int CPW = CHUNKS / kPWaves;              // chunks (loads) per wave per page
     static_assert(CHUNKS % kPWaves == 0, "chunks divide over the waves");
-    // Two page buffers [K page | V page], declared apart so the compiler can
-    // tell the buffer being filled from the one being read.
-    __shared__ __attribute__((aligned(16))) KV stage0[2 * PAGE];
-    __shared__ __attribute__((aligned(16))) KV stage1[2 * PAGE];
+    __shared__ __attribute__((aligned(16))) KV ring0[2 * PAGE];
+    __shared__ __attribute__((aligned(16))) KV ring1[2 * PAGE];
+    __shared__ __attribute__((aligned(16))) KV ring2[2 * PAGE];
+    __shared__ __attribute__((aligned(16))) KV ring3[2 * PAGE];
 
     const int lane = threadIdx.x & 63, w = threadIdx.x >> 6, g = lane >> 4;
     const int h = blockIdx.x % a.kv_heads;
@@ -81,7 +85,10 @@ void attention_prefill(PrefillArgs a) {
 
     // Query fragments (B operand): tile rt, k-step ks of lane l holds row
     // row0 + 16*rt + l%16, dims 32*ks + 8*(l/16) .. +7.  Padded rows repeat
-    // the last row; their results are not stored.
+    // the last row; their results are not stored.  They are in registers
+    // before the first page is requested (a workgroup runs for hundreds of
+    // pages, so this one round trip is negligible, and the page loop never
+    // waits on them).
     V8 qf[RT][KS];
     int limit[RT];
 #pragma unroll
@@ -94,17 +101,18 @@ void attention_prefill(PrefillArgs a) {
 #pragma unroll
         for (int ks = 0; ks < KS; ++ks) qf[rt][ks] = *reinterpret_cast<const V8 *>(src + 32 * ks);
     }
+    wait_vmcnt<0>();
     // Keys this workgroup can see: 0 .. position + (token of its last row).
     const int last_row = min(tile * kRowsPerGroup + kRowsPerGroup - 1, a.rows - 1);
     const int n_keys = a.position + last_row / a.group + 1;
-    const int n_pages = (n_keys + 31) / 32;
+    const int n = (n_keys + 31) / 32;
     // First page that any row of this wave masks (all rows see keys <= position).
     const int wave_first_limit = a.position + min(row0, a.rows - 1) / a.group;
 
     const KV *kh = static_cast<const KV *>(a.k_pages) + (size_t)h * a.head_stride;
     const KV *vh = static_cast<const KV *>(a.v_pages) + (size_t)h * a.head_stride;
-    // Wave w copies chunks w*CPW .. of the [K | V] page p into `dst`.
-    auto stage_page = [&](int p, KV *dst) {
+    // Wave w copies 1 KiB chunks w*CPW .. of the [K | V] page p into `dst`.
+    auto stage = [&](int p, KV *dst) __attribute__((always_inline)) {
 #pragma unroll
         for (int c = 0; c < CPW; ++c) {
             const int chunk = w * CPW + c;
@@ -126,42 +134,64 @@ void attention_prefill(PrefillArgs a) {
         for (int dt = 0; dt < DT; ++dt) acc[rt][dt] = f32x4{0.f, 0.f, 0.f, 0.f};
     }
 
-    auto page = [&](int p, const KV *cur, KV *next) {
-        if (p + 1 < n_pages) stage_page(p + 1, next);   // uniform over the workgroup
-        const KV *ks_lds = cur;
-        const KV *vs_lds = cur + PAGE;
-        // ---- S^T for both 16-key tiles of the page ----
+    auto compute = [&](int p, const KV *cur) __attribute__((always_inline)) {
+        const uint32_t kbase = lds_addr(cur) + lane * 16;
+        const uint32_t vbase = lds_addr(cur) + PAGE * 2 + lane * 16;
+        // ---- S^T for both 16-key tiles of the page and both row tiles ----
+        // The 16 K fragments are requested in two batches of 8 (at most 15
+        // LDS reads in flight) and consumed as they arrive: four independent
+        // accumulation chains (row tile x key tile).
+        static_assert(KS == 8 || KS == 4, "head_dim 256 or 128");
+        constexpr int KB = KS / 2;                     // k-steps per batch
+        V8 kf[KS][2];
+        auto read_k = [&](auto ks) __attribute__((always_inline)) {
+            static_for<0, 2>([&](auto kt) {
+                lds_read<(decltype(kt)::value * 16 * D + decltype(ks)::value * 512) * 2>(
+                    kf[decltype(ks)::value][decltype(kt)::value], kbase);
+            });
+        };
+        static_for<0, KB>(read_k);
         f32x4 s[RT][2];
 #pragma unroll
         for (int rt = 0; rt < RT; ++rt) s[rt][0] = s[rt][1] = f32x4{0.f, 0.f, 0.f, 0.f};
+        static_for<0, KS>([&](auto ks_) {
+            constexpr int ks = decltype(ks_)::value;
+            // Reads outstanding after the pair of k-step ks has landed.
+            constexpr int later = ks < KB ? 2 * (KB - 1 - ks) + (ks == 0 ? 0 : 2 * KB)
+                                          : 2 * (KS - 1 - ks);
+            lds_wait<later>(kf[ks][0]);
+            lds_wait<later>(kf[ks][1]);
+            if constexpr (ks == 0) static_for<KB, KS>(read_k);   // second batch
 #pragma unroll
-        for (int ks = 0; ks < KS; ++ks) {
+            for (int kt = 0; kt < 2; ++kt)
 #pragma unroll
-            for (int kt = 0; kt < 2; ++kt) {
-                const V8 kf = *reinterpret_cast<const V8 *>(ks_lds + kt * 16 * D + ks * 512 + lane * 8);
-#pragma unroll
-                for (int rt = 0; rt < RT; ++rt) s[rt][kt] = mfma(kf, qf[rt][ks], s[rt][kt]);
-            }
-        }
+                for (int rt = 0; rt < RT; ++rt) s[rt][kt] = mfma(kf[ks][kt], qf[rt][ks], s[rt][kt]);
+        });
+        // The first half of the V fragments is requested now and arrives
+        // during the softmax; the second half once the first has landed.
+        constexpr int VB = DT / 2;
+        V8 vf[DT];
+        auto read_v = [&](auto dt) __attribute__((always_inline)) {
+            lds_read<decltype(dt)::value * 1024>(vf[decltype(dt)::value], vbase);
+        };
+        static_for<0, VB>(read_v);
         // ---- online softmax; keys past a row's limit are masked ----
-        const bool edge = p * 32 + 31 > wave_first_limit;
         V8 ph[RT], pl[RT];
-        float alpha[RT];
         bool rescale = false;
+        float alpha[RT];
 #pragma unroll
         for (int rt = 0; rt < RT; ++rt) {
             float x[8];
 #pragma unroll
             for (int j = 0; j < 8; ++j) x[j] = s[rt][j >> 2][j & 3] * a.scale_log2;
-            if (edge) {
+            if (p * 32 + 31 > wave_first_limit) {
+                keep_branch();
 #pragma unroll
                 for (int j = 0; j < 8; ++j)
                     if (p * 32 + 16 * (j >> 2) + 4 * g + (j & 3) > limit[rt]) x[j] = -INFINITY;
             }
-            float bm = fmaxf(fmaxf(fmaxf(x[0], x[1]), fmaxf(x[2], x[3])),
-                             fmaxf(fmaxf(x[4], x[5]), fmaxf(x[6], x[7])));
-            bm = fmaxf(bm, __shfl_xor(bm, 16, kWave));
-            bm = fmaxf(bm, __shfl_xor(bm, 32, kWave));
+            const float bm = row_group_max(fmaxf(fmaxf(fmaxf(x[0], x[1]), fmaxf(x[2], x[3])),
+                                                 fmaxf(fmaxf(x[4], x[5]), fmaxf(x[6], x[7]))));
             alpha[rt] = 1.f;
             if (bm > m[rt] + kLazy) {
                 alpha[rt] = __builtin_amdgcn_exp2f(m[rt] - bm);
@@ -185,46 +215,68 @@ void attention_prefill(PrefillArgs a) {
             l[rt] = l[rt] * alpha[rt] + ps;
         }
         if (__any(rescale)) {
+            keep_branch();
 #pragma unroll
             for (int rt = 0; rt < RT; ++rt)
 #pragma unroll
                 for (int dt = 0; dt < DT; ++dt) acc[rt][dt] *= alpha[rt];
         }
-        // ---- O^T += V^T P^T; V slots past the last key are zeroed ----
-        const bool tail = p * 32 + 32 > n_keys;
-#pragma unroll
-        for (int dt = 0; dt < DT; ++dt) {
-            V8 vf = *reinterpret_cast<const V8 *>(vs_lds + dt * 512 + lane * 8);
-            if (tail) {
+        lds_wait<VB - 1>(vf[0]);
+        static_for<VB, DT>(read_v);                    // second half
+        if (p * 32 + 32 > n_keys) {
+            // Last page: V slots past the last key are zeroed (stale pages may
+            // hold anything, and 0 * NaN is NaN).
+            keep_branch();
+            static_for<0, DT>([&](auto dt_) {
+                constexpr int dt = decltype(dt_)::value;
+                lds_wait<0>(vf[dt]);
 #pragma unroll
                 for (int j = 0; j < 8; ++j)
-                    if (p * 32 + v_slot_token(g, j) >= n_keys) vf[j] = (KV)0.f;
-            }
+                    if (p * 32 + v_slot_token(g, j) >= n_keys) vf[dt][j] = (KV)0.f;
+            });
+        }
+        // ---- O^T += V^T P^T ----
+        static_for<0, DT>([&](auto dt_) {
+            constexpr int dt = decltype(dt_)::value;
+            lds_wait<DT - 1 - dt>(vf[dt]);
 #pragma unroll
             for (int rt = 0; rt < RT; ++rt) {
-                acc[rt][dt] = mfma(vf, ph[rt], acc[rt][dt]);
-                if constexpr (PSPLIT) acc[rt][dt] = mfma(vf, pl[rt], acc[rt][dt]);
+                acc[rt][dt] = mfma(vf[dt], ph[rt], acc[rt][dt]);
+                if constexpr (PSPLIT) acc[rt][dt] = mfma(vf[dt], pl[rt], acc[rt][dt]);
             }
-        }
-        // The next page has landed in LDS for every wave, and every wave is
-        // done reading this one before it is overwritten.
-        __builtin_amdgcn_s_waitcnt(0);
-        __syncthreads();
+        });
     };
 
-    stage_page(0, stage0);
-    __builtin_amdgcn_s_waitcnt(0);
-    __syncthreads();
-    for (int p = 0; p < n_pages; p += 2) {
-        page(p, stage0, stage1);
-        if (p + 1 < n_pages) page(p + 1, stage1, stage0);
+    auto wait_page = [&](int i) __attribute__((always_inline)) {
+        const int ahead = min(2, n - 1 - i);
+        if (ahead >= 2) wait_vmcnt<2 * CPW>();
+        else if (ahead == 1) wait_vmcnt<CPW>();
+        else wait_vmcnt<0>();
+    };
+    // Step i: this wave's share of page i has landed (pages i+1 and i+2 may
+    // stay in flight), the waves meet (page i complete, page i-1 consumed),
+    // the consumed buffer is refilled with page i+3, and page i is consumed.
+    auto step = [&](int i, const KV *cur, KV *fill) __attribute__((always_inline)) {
+        wait_page(i);
+        ring_barrier();
+        if (i + 3 < n) stage(i + 3, fill);
+        compute(i, cur);
+    };
+
+    stage(0, ring0);
+    if (n > 1) stage(1, ring1);
+    if (n > 2) stage(2, ring2);
+    for (int i = 0; i < n; i += 4) {
+        step(i, ring0, ring3);
+        if (i + 1 < n) step(i + 1, ring1, ring0);
+        if (i + 2 < n) step(i + 2, ring2, ring1);
+        if (i + 3 < n) step(i + 3, ring3, ring2);
     }
 
     // ---- normalise and store rows ----
 #pragma unroll
     for (int rt = 0; rt < RT; ++rt) {
-        l[rt] += __shfl_xor(l[rt], 16, kWave);
-        l[rt] += __shfl_xor(l[rt], 32, kWave);
+        l[rt] = row_group_sum(l[rt]);
         const int row = row0 + 16 * rt + (lane & 15);
         if (row < a.rows) {
             const int t = row / a.group, gg = row - t * a.group;

@@ -20,6 +20,7 @@
 // The partials (m, l, unnormalised O) use the layout of the other split
 // kernels, so attention_combine merges them.
 #include "kernels.hpp"
+#include "lds.hpp"
 
 #include <cmath>
 #include <cstdint>
@@ -54,77 +55,6 @@ __device__ __forceinline__ f32x4 mfma(bf16x4 a, bf16x4 b, f32x4 c) {
 
 constexpr int kRingWaves = 8;
 constexpr float kLazy = 8.f;   // lazy row-max threshold, log2 units
-
-// s_waitcnt vmcnt(N) leaving the other counters alone (gfx9 encoding:
-// vmcnt bits 3:0 and 15:14, expcnt 6:4, lgkmcnt 11:8).
-template <int N>
-__device__ __forceinline__ void wait_vmcnt() {
-    static_assert(N >= 0 && N < 64, "vmcnt range");
-    __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | (7 << 4) | (15 << 8));
-}
-
-// LDS byte address of a __shared__ object.
-__device__ __forceinline__ uint32_t lds_addr(const void *p) {
-    return (uint32_t)(uintptr_t)(__attribute__((address_space(3))) const void *)p;
-}
-
-// Compile-time loop: f(std::integral_constant<int, I>) for I in [B, E).
-template <int B, int E, typename F>
-__device__ __forceinline__ void static_for(F &&f) {
-    if constexpr (B < E) {
-        f(std::integral_constant<int, B>{});
-        static_for<B + 1, E>(f);
-    }
-}
-
-// LDS reads of page fragments at addr + OFF, issued as written.  They bypass
-// the compiler's own wait insertion, which cannot tell the ring buffers'
-// direct loads apart for every buffer and would drain the whole ring before
-// some reads; their completion is awaited explicitly with lds_wait.
-template <int OFF, typename V>
-__device__ __forceinline__ void lds_read(V &v, uint32_t addr) {
-    static_assert(OFF >= 0 && OFF < 65536, "ds_read offset range");
-    if constexpr (sizeof(V) == 16)
-        asm volatile("ds_read_b128 %0, %1 offset:%2" : "=v"(v) : "v"(addr), "i"(OFF));
-    else
-        asm volatile("ds_read_b64 %0, %1 offset:%2" : "=v"(v) : "v"(addr), "i"(OFF));
-}
-// s_waitcnt lgkmcnt(N), after which v (read by lds_read) may be used.
-template <int N, typename V>
-__device__ __forceinline__ void lds_wait(V &v) {
-    static_assert(N >= 0 && N < 16, "lgkmcnt range");
-    asm volatile("s_waitcnt lgkmcnt(%1)" : "+v"(v) : "i"(N));
-}
-
-// Marks a rarely taken branch body as having side effects, so the compiler
-// keeps the branch instead of executing the body on every page as selects.
-__device__ __forceinline__ void keep_branch() { asm volatile(""); }
-
-// Workgroup barrier for the page ring.  A workgroup-scope fence would also
-// wait for every direct global->LDS load in flight (they count as LDS
-// writes), draining the ring; instead each wave waits explicitly for the
-// loads and LDS reads that the barrier hands over, and the empty asm
-// statements keep the compiler from moving memory accesses across it.
-__device__ __forceinline__ void ring_barrier() {
-    asm volatile("" ::: "memory");
-    __builtin_amdgcn_s_barrier();
-    asm volatile("" ::: "memory");
-}
-
-// Maximum (sum) over the four 16-lane rows of the wave: lanes l, l^16, l^32
-// and l^48, exchanged with the lane-swap instructions instead of LDS.
-__device__ __forceinline__ float row_group_max(float x) {
-    const auto a = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
-    const float y = fmaxf(__uint_as_float(a[0]), __uint_as_float(a[1]));
-    const auto b = __builtin_amdgcn_permlane16_swap(__float_as_uint(y), __float_as_uint(y), false, false);
-    return fmaxf(__uint_as_float(b[0]), __uint_as_float(b[1]));
-}
-__device__ __forceinline__ float row_group_sum(float x) {
-    const auto a = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
-    const float y = __uint_as_float(a[0]) + __uint_as_float(a[1]);
-    const auto b = __builtin_amdgcn_permlane16_swap(__float_as_uint(y), __float_as_uint(y), false, false);
-    return __uint_as_float(b[0]) + __uint_as_float(b[1]);
-}
 
 template <int D, int NQT, bool PSPLIT, typename KV>
 __global__ __launch_bounds__(kRingWaves * kWave, 1)
@@ -209,11 +139,15 @@ void attention_ring(SplitArgs a) {
             if constexpr (ks % 2 == 0) s0 = mfma(kf[ks], qf[ks], s0);
             else s1 = mfma(kf[ks], qf[ks], s1);
         });
-        // V^T fragments of the same 16 keys (half of each 32-key fragment).
+        // V^T fragments of the same 16 keys (half of each 32-key fragment):
+        // the first half requested now, the second once it has landed (at
+        // most 15 LDS reads in flight).
+        constexpr int VB = DT / 2;
         V4 vf[DT];
-        static_for<0, DT>([&](auto dt) {
+        auto read_v = [&](auto dt) __attribute__((always_inline)) {
             lds_read<decltype(dt)::value * 1024>(vf[decltype(dt)::value], vbase);
-        });
+        };
+        static_for<0, VB>(read_v);
         // Online softmax over the wave's 16 keys of the page (lane: keys
         // 16kt + 4g + r for row l%16); keys past the row's limit (later
         // candidates, or past the last key) are masked.
@@ -254,6 +188,8 @@ void attention_ring(SplitArgs a) {
 #pragma unroll
             for (int dt = 0; dt < DT; ++dt) acc[dt] *= alpha;
         }
+        lds_wait<VB - 1>(vf[0]);
+        static_for<VB, DT>(read_v);
         if (p * 32 + 32 > a.n_keys) {
             // Last page: V slots past the last key are zeroed (stale pages
             // may hold anything, and 0 * NaN is NaN).
@@ -269,8 +205,7 @@ void attention_ring(SplitArgs a) {
         // O^T += V^T P^T over the 16 keys.
         static_for<0, DT>([&](auto dt_) {
             constexpr int dt = decltype(dt_)::value;
-            constexpr int later = DT - 1 - dt;
-            lds_wait<(later < 15 ? later : 15)>(vf[dt]);
+            lds_wait<DT - 1 - dt>(vf[dt]);
             acc[dt] = mfma(vf[dt], ph, acc[dt]);
             if constexpr (PSPLIT) acc[dt] = mfma(vf[dt], pl, acc[dt]);
         });
