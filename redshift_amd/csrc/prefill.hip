@@ -4,14 +4,14 @@
 // qvelox/server.py:187-191); this is the same causal GQA formula for long
 // token runs: row t sees keys 0..position+t.
 //
-// One workgroup (4 waves) owns 128 query rows of one KV head (row = token *
-// group + query head within the group); wave w owns rows 32w..32w+31 as two
-// 16-row tiles whose query fragments stay in registers.  The workgroup walks
+// One workgroup owns 192 query rows of one KV head (row = token * group +
+// query head within the group); each wave owns one 16-row tile (twelve
+// waves: three per SIMD) whose query fragments stay in registers.  The workgroup walks
 // the pages that its last row can see through a ring of four LDS buffers
 // ([K page | V page], 32 KiB at D=256) filled by direct global->LDS loads,
 // three pages ahead.  Since pages are stored in MFMA operand order, every
 // wave reads its A operands as conflict-free 16-byte LDS fragments, each one
-// feeding both of its tiles:
+// feeding all of its tiles:
 //   S^T[key][row] = K[key][:] . Q[row][:]     (A = K tile from LDS, B = Q)
 //   O^T[dim][row] += V^T[dim][key] P^T[key][row]  (A = V^T from LDS, B = P^T,
 //                                                  straight from S^T's C layout)
@@ -30,6 +30,7 @@
 
 #include <algorithm>
 #include <cmath>
+#include <cstdlib>
 
 namespace rs {
 namespace {
@@ -45,9 +46,8 @@ __device__ __forceinline__ f32x4 mfma(bf16x8 a, bf16x8 b, f32x4 c) {
     return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, 0, 0, 0);
 }
 
-constexpr int kPWaves = 4;                 // waves per prefill workgroup
-constexpr int kRowsPerWave = 32;           // two 16-row tiles
-constexpr int kRowsPerGroup = kPWaves * kRowsPerWave;
+// Waves per workgroup of ROWS query rows with RT 16-row tiles per wave.
+template <int ROWS, int RT> constexpr int prefill_waves() { return ROWS / (16 * RT); }
 constexpr float kLazy = 8.f;
 
 struct PrefillArgs {
@@ -64,15 +64,19 @@ __device__ __forceinline__ int v_slot_token(int g, int j) {
     return j < 4 ? 4 * g + j : 16 + 4 * g + j - 4;
 }
 
-template <int D, typename KV, bool PSPLIT, typename OUT>
-__global__ __launch_bounds__(kPWaves * kWave, 1)
+template <int D, typename KV, bool PSPLIT, typename OUT, int RT, int ROWS>
+__global__ __launch_bounds__((prefill_waves<ROWS, RT>() * kWave), 1)
 void attention_prefill(PrefillArgs a) {
     using V8 = typename Vec8<KV>::type;
-    constexpr int KS = D / 32, DT = D / 16, RT = kRowsPerWave / 16;
+    constexpr int kPWaves = prefill_waves<ROWS, RT>(), kRowsPerWave = 16 * RT, kRowsPerGroup = ROWS;
+    constexpr int KS = D / 32, DT = D / 16;
     constexpr int PAGE = 32 * D;                       // elements of one K (or V) page
     constexpr int CHUNKS = 2 * PAGE * 2 / 1024;        // 1 KiB chunks of K + V page
-    constexpr int CPW = CHUNKS / kPWaves;              // chunks (loads) per wave per page
-    static_assert(CHUNKS % kPWaves == 0, "chunks divide over the waves");
+    // Waves 0..kLoaders-1 copy the pages (the largest power of two of waves
+    // that divides the page's chunks).
+    constexpr int kLoaders = kPWaves >= 8 ? 8 : kPWaves;
+    constexpr int CPW = CHUNKS / kLoaders;             // chunks (loads) per loader wave per page
+    static_assert(CHUNKS % kLoaders == 0, "chunks divide over the loader waves");
     __shared__ __attribute__((aligned(16))) KV ring0[2 * PAGE];
     __shared__ __attribute__((aligned(16))) KV ring1[2 * PAGE];
     __shared__ __attribute__((aligned(16))) KV ring2[2 * PAGE];
@@ -111,8 +115,11 @@ void attention_prefill(PrefillArgs a) {
 
     const KV *kh = static_cast<const KV *>(a.k_pages) + (size_t)h * a.head_stride;
     const KV *vh = static_cast<const KV *>(a.v_pages) + (size_t)h * a.head_stride;
-    // Wave w copies 1 KiB chunks w*CPW .. of the [K | V] page p into `dst`.
+    // Loader wave w copies 1 KiB chunks w*CPW .. of the [K | V] page p into
+    // `dst` (the other waves have no loads in flight, so their page waits
+    // below return at once).
     auto stage = [&](int p, KV *dst) __attribute__((always_inline)) {
+        if (w >= kLoaders) return;
 #pragma unroll
         for (int c = 0; c < CPW; ++c) {
             const int chunk = w * CPW + c;
@@ -137,12 +144,12 @@ void attention_prefill(PrefillArgs a) {
     auto compute = [&](int p, const KV *cur) __attribute__((always_inline)) {
         const uint32_t kbase = lds_addr(cur) + lane * 16;
         const uint32_t vbase = lds_addr(cur) + PAGE * 2 + lane * 16;
-        // ---- S^T for both 16-key tiles of the page and both row tiles ----
-        // The 16 K fragments are requested in two batches of 8 (at most 15
-        // LDS reads in flight) and consumed as they arrive: four independent
+        // ---- S^T for both 16-key tiles of the page and all row tiles ----
+        // K fragments stream through a window of KW k-steps (2*KW reads in
+        // flight, at most 15): the pair of k-step ks+KW is requested as soon
+        // as that of ks has landed, and each pair feeds 2*RT independent
         // accumulation chains (row tile x key tile).
-        static_assert(KS == 8 || KS == 4, "head_dim 256 or 128");
-        constexpr int KB = KS / 2;                     // k-steps per batch
+        constexpr int KW = 2;
         V8 kf[KS][2];
         auto read_k = [&](auto ks) __attribute__((always_inline)) {
             static_for<0, 2>([&](auto kt) {
@@ -150,31 +157,30 @@ void attention_prefill(PrefillArgs a) {
                     kf[decltype(ks)::value][decltype(kt)::value], kbase);
             });
         };
-        static_for<0, KB>(read_k);
+        static_for<0, KW>(read_k);
         f32x4 s[RT][2];
 #pragma unroll
         for (int rt = 0; rt < RT; ++rt) s[rt][0] = s[rt][1] = f32x4{0.f, 0.f, 0.f, 0.f};
         static_for<0, KS>([&](auto ks_) {
             constexpr int ks = decltype(ks_)::value;
-            // Reads outstanding after the pair of k-step ks has landed.
-            constexpr int later = ks < KB ? 2 * (KB - 1 - ks) + (ks == 0 ? 0 : 2 * KB)
-                                          : 2 * (KS - 1 - ks);
+            // Reads issued after this pair: the rest of the window.
+            constexpr int later = 2 * (ks + KW <= KS ? KW - 1 : KS - 1 - ks);
             lds_wait<later>(kf[ks][0]);
             lds_wait<later>(kf[ks][1]);
-            if constexpr (ks == 0) static_for<KB, KS>(read_k);   // second batch
+            if constexpr (ks + KW < KS) read_k(std::integral_constant<int, ks + KW>{});
 #pragma unroll
             for (int kt = 0; kt < 2; ++kt)
 #pragma unroll
                 for (int rt = 0; rt < RT; ++rt) s[rt][kt] = mfma(kf[ks][kt], qf[rt][ks], s[rt][kt]);
         });
-        // The first half of the V fragments is requested now and arrives
-        // during the softmax; the second half once the first has landed.
-        constexpr int VB = DT / 2;
+        // The first VW V fragments are requested now and arrive during the
+        // softmax; the rest stream through the same window during O^T.
+        constexpr int VW = 4;
         V8 vf[DT];
         auto read_v = [&](auto dt) __attribute__((always_inline)) {
             lds_read<decltype(dt)::value * 1024>(vf[decltype(dt)::value], vbase);
         };
-        static_for<0, VB>(read_v);
+        static_for<0, VW>(read_v);
         // ---- online softmax; keys past a row's limit are masked ----
         V8 ph[RT], pl[RT];
         bool rescale = false;
@@ -221,24 +227,21 @@ void attention_prefill(PrefillArgs a) {
 #pragma unroll
                 for (int dt = 0; dt < DT; ++dt) acc[rt][dt] *= alpha[rt];
         }
-        lds_wait<VB - 1>(vf[0]);
-        static_for<VB, DT>(read_v);                    // second half
-        if (p * 32 + 32 > n_keys) {
-            // Last page: V slots past the last key are zeroed (stale pages may
-            // hold anything, and 0 * NaN is NaN).
-            keep_branch();
-            static_for<0, DT>([&](auto dt_) {
-                constexpr int dt = decltype(dt_)::value;
-                lds_wait<0>(vf[dt]);
-#pragma unroll
-                for (int j = 0; j < 8; ++j)
-                    if (p * 32 + v_slot_token(g, j) >= n_keys) vf[dt][j] = (KV)0.f;
-            });
-        }
+        // Last page: V slots past the last key are zeroed (stale pages may
+        // hold anything, and 0 * NaN is NaN).
+        const bool tail = p * 32 + 32 > n_keys;
         // ---- O^T += V^T P^T ----
         static_for<0, DT>([&](auto dt_) {
             constexpr int dt = decltype(dt_)::value;
-            lds_wait<DT - 1 - dt>(vf[dt]);
+            constexpr int later = dt + VW <= DT ? VW - 1 : DT - 1 - dt;
+            lds_wait<later>(vf[dt]);
+            if constexpr (dt + VW < DT) read_v(std::integral_constant<int, dt + VW>{});
+            if (tail) {
+                keep_branch();
+#pragma unroll
+                for (int j = 0; j < 8; ++j)
+                    if (p * 32 + v_slot_token(g, j) >= n_keys) vf[dt][j] = (KV)0.f;
+            }
 #pragma unroll
             for (int rt = 0; rt < RT; ++rt) {
                 acc[rt][dt] = mfma(vf[dt], ph[rt], acc[rt][dt]);
@@ -294,13 +297,33 @@ void attention_prefill(PrefillArgs a) {
     }
 }
 
-template <int D>
+// Row tiles per wave: one.  Rows per workgroup: 192 (twelve waves, three
+// per SIMD, whose softmax and matrix work overlap; and 2048 tokens of six
+// query heads per KV head make 64 workgroups per KV head, one round on 256
+// CUs) or 128 (RS_PREFILL_ROWS=128, for measurement).
+constexpr int kPrefillRT = 1;
+
+int prefill_rows() {
+    static const int rows = [] {
+        const char *v = std::getenv("RS_PREFILL_ROWS");
+        return v && std::atoi(v) == 128 ? 128 : 192;
+    }();
+    return rows;
+}
+
+template <int D, int ROWS>
 const void *prefill_kernel(Dtype dtype, bool out_f32) {
+    constexpr int RT = kPrefillRT;
     if (dtype == Dtype::BF16)
-        return out_f32 ? (const void *)&attention_prefill<D, __bf16, true, float>
-                       : (const void *)&attention_prefill<D, __bf16, true, __bf16>;
-    return out_f32 ? (const void *)&attention_prefill<D, _Float16, false, float>
-                   : (const void *)&attention_prefill<D, _Float16, false, _Float16>;
+        return out_f32 ? (const void *)&attention_prefill<D, __bf16, true, float, RT, ROWS>
+                       : (const void *)&attention_prefill<D, __bf16, true, __bf16, RT, ROWS>;
+    return out_f32 ? (const void *)&attention_prefill<D, _Float16, false, float, RT, ROWS>
+                   : (const void *)&attention_prefill<D, _Float16, false, _Float16, RT, ROWS>;
+}
+
+template <int D>
+const void *prefill_kernel(Dtype dtype, bool out_f32, int rows) {
+    return rows == 128 ? prefill_kernel<D, 128>(dtype, out_f32) : prefill_kernel<D, 192>(dtype, out_f32);
 }
 
 }  // namespace
@@ -318,13 +341,15 @@ void launch_prefill(const Shape &s, Dtype dtype, float scale, const void *q, con
     a.group = s.group();
     a.rows = s.group() * s.tokens;
     a.position = s.position;
-    a.n_tiles = (a.rows + kRowsPerGroup - 1) / kRowsPerGroup;
+    const int rows = prefill_rows();
+    a.n_tiles = (a.rows + rows - 1) / rows;
     a.scale_log2 = scale * 1.4426950408889634f;
-    const void *kernel = s.head_dim == 256 ? prefill_kernel<256>(dtype, out_f32)
-                       : s.head_dim == 128 ? prefill_kernel<128>(dtype, out_f32) : nullptr;
+    const void *kernel = s.head_dim == 256 ? prefill_kernel<256>(dtype, out_f32, rows)
+                       : s.head_dim == 128 ? prefill_kernel<128>(dtype, out_f32, rows) : nullptr;
     require(kernel != nullptr, "unsupported head_dim for the prefill kernel");
     void *args[] = {&a};
-    check(hipLaunchKernel(kernel, dim3(a.n_tiles * s.kv_heads), dim3(kPWaves * kWave), args, 0, stream));
+    const int threads = (rows / (16 * kPrefillRT)) * kWave;
+    check(hipLaunchKernel(kernel, dim3(a.n_tiles * s.kv_heads), dim3(threads), args, 0, stream));
 }
 
 }  // namespace rs
