@@ -31,6 +31,9 @@ COMMON_FLAGS = [
 # architectural VGPRs: with AGPR accumulators the compiler copies them out
 # and back on every page (for the rarely taken softmax rescale).
 SOURCE_FLAGS = {name: ['-mllvm', '-amdgpu-mfma-vgpr-form'] for name in ('ring.hip', 'prefill.hip')}
+# The prefill kernel masks keys to -inf and zeroes stale V slots explicitly,
+# so its maxima need no NaN quieting.
+SOURCE_FLAGS['prefill.hip'] = SOURCE_FLAGS['prefill.hip'] + ['-fno-honor-nans']
 
 
 def hipcc():

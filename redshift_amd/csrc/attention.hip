@@ -682,7 +682,13 @@ SplitPlan plan_split(const Shape &s, int tokens, Dtype dtype, bool precise) {
     // Fill every CU with as many workgroups as stay resident.
     const int resident = device_cu_count() *
                          blocks_per_cu(split_kernel(p, s.head_dim, dtype, precise), block_threads(p));
-    const int per_head = std::max(1, std::min(resident / s.kv_heads, kMaxSplits));
+    int per_head = std::max(1, std::min(resident / s.kv_heads, kMaxSplits));
+    // RS_SPLITS_PER_HEAD caps the split count (for measurement).
+    static const int cap = [] {
+        const char *v = std::getenv("RS_SPLITS_PER_HEAD");
+        return v ? std::max(1, std::atoi(v)) : 0;
+    }();
+    if (cap) per_head = std::min(per_head, cap);
     if (p.kind == SplitKind::Stream) {
         // Every wave gets at least one page on average.
         p.splits = std::max(1, std::min(per_head, (p.n_pages + kWaves - 1) / kWaves));

@@ -52,6 +52,12 @@ __device__ __forceinline__ void lds_wait(V &v) {
     static_assert(N >= 0 && N < 16, "lgkmcnt range");
     asm volatile("s_waitcnt lgkmcnt(%1)" : "+v"(v) : "i"(N));
 }
+// The same for two reads, a and b, with one wait.
+template <int N, typename V>
+__device__ __forceinline__ void lds_wait(V &a, V &b) {
+    static_assert(N >= 0 && N < 16, "lgkmcnt range");
+    asm volatile("s_waitcnt lgkmcnt(%2)" : "+v"(a), "+v"(b) : "i"(N));
+}
 
 // Marks a rarely taken branch body as having side effects, so the compiler
 // keeps the branch instead of executing the body on every page as selects.

@@ -6,20 +6,25 @@
 //
 // One workgroup owns 192 query rows of one KV head (row = token * group +
 // query head within the group); each wave owns one 16-row tile (twelve
-// waves: three per SIMD) whose query fragments stay in registers.  The workgroup walks
-// the pages that its last row can see through a ring of four LDS buffers
-// ([K page | V page], 32 KiB at D=256) filled by direct global->LDS loads,
-// three pages ahead.  Since pages are stored in MFMA operand order, every
-// wave reads its A operands as conflict-free 16-byte LDS fragments, each one
-// feeding all of its tiles:
+// waves: three per SIMD) whose query fragments stay in registers.  The
+// workgroup walks the pages that its last row can see through two rings of
+// four LDS buffers, one for K pages and one for V pages (16 KiB each at
+// D=256), filled by direct global->LDS loads three pages ahead.  Since pages
+// are stored in MFMA operand order, every wave reads its A operands as
+// conflict-free 16-byte LDS fragments:
 //   S^T[key][row] = K[key][:] . Q[row][:]     (A = K tile from LDS, B = Q)
 //   O^T[dim][row] += V^T[dim][key] P^T[key][row]  (A = V^T from LDS, B = P^T,
 //                                                  straight from S^T's C layout)
-// A page's 16 K fragments are requested at once and consumed as they arrive
-// (four independent accumulation chains), and its V fragments are requested
-// while the softmax runs.  Online softmax in base 2 with a lazily moved row
-// max (see ring.hip).  bf16 caches multiply by P split into hi + lo bf16
-// parts, fp16 caches by a single fp16 P.
+//
+// Software pipeline: step i computes the scores of page i+1 on the matrix
+// cores while the vector ALUs run the softmax of page i (whose scores the
+// previous step produced), then multiplies page i's V by its P.  The two
+// halves are interleaved chunk by chunk, so every wave keeps both units busy
+// instead of alternating between them in step with the other waves of its
+// SIMD.  Online softmax in base 2 with a lazily moved row max (see ring.hip);
+// the max is taken over raw scores and the scale is folded into the
+// exponent's fused multiply-add.  bf16 caches multiply by P split into hi +
+// lo bf16 parts, fp16 caches by a single fp16 P.
 //
 // Scheduling: workgroup i serves KV head i % kv_heads (with 4 KV heads the
 // round-robin dispatch over the 8 XCDs keeps every head on the same two XCDs,
@@ -46,8 +51,39 @@ __device__ __forceinline__ f32x4 mfma(bf16x8 a, bf16x8 b, f32x4 c) {
     return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, 0, 0, 0);
 }
 
-// Waves per workgroup of ROWS query rows with RT 16-row tiles per wave.
-template <int ROWS, int RT> constexpr int prefill_waves() { return ROWS / (16 * RT); }
+// The softmax values of a pipeline chunk are computed before this point: an
+// empty statement, ordered with the LDS reads and waits around it, that
+// takes them as operands (so they are not moved towards their later uses).
+template <typename T>
+__device__ __forceinline__ void pin1(T &v) {
+    asm volatile("" : "+v"(v));
+}
+template <typename... T>
+__device__ __forceinline__ void pin(T &...v) {
+    (pin1(v), ...);
+}
+
+__device__ __forceinline__ float max3(float a, float b, float c) {
+    return __builtin_fmaxf(__builtin_fmaxf(a, b), c);
+}
+
+// Two fp32 values as one dword of 16-bit values (element 0 in the low half).
+__device__ __forceinline__ uint32_t pack2(float a, float b, _Float16) {
+    typedef _Float16 h2 __attribute__((ext_vector_type(2)));
+    return __builtin_bit_cast(uint32_t, h2{(_Float16)a, (_Float16)b});
+}
+__device__ __forceinline__ uint32_t pack2(float a, float b, __bf16) {
+    typedef __bf16 b2 __attribute__((ext_vector_type(2)));
+    return __builtin_bit_cast(uint32_t, b2{(__bf16)a, (__bf16)b});
+}
+// The two bf16 halves of a packed word as fp32 values.  The low half is moved
+// up with a byte permute (bytes 1:0 to 3:2, zeros below), which keeps the
+// compiler from converting the fp32 input a second time instead.
+__device__ __forceinline__ float bf16_lo(uint32_t w) {
+    return __uint_as_float(__builtin_amdgcn_perm(0u, w, 0x01000c0cu));
+}
+__device__ __forceinline__ float bf16_hi(uint32_t w) { return __uint_as_float(w & 0xffff0000u); }
+
 constexpr float kLazy = 8.f;
 
 struct PrefillArgs {
@@ -64,245 +100,272 @@ __device__ __forceinline__ int v_slot_token(int g, int j) {
     return j < 4 ? 4 * g + j : 16 + 4 * g + j - 4;
 }
 
-template <int D, typename KV, bool PSPLIT, typename OUT, int RT, int ROWS>
-__global__ __launch_bounds__((prefill_waves<ROWS, RT>() * kWave), 1)
+template <int D, typename KV, bool PSPLIT, typename OUT, int ROWS>
+__global__ __launch_bounds__(ROWS / 16 * kWave, 1)
 void attention_prefill(PrefillArgs a) {
     using V8 = typename Vec8<KV>::type;
-    constexpr int kPWaves = prefill_waves<ROWS, RT>(), kRowsPerWave = 16 * RT, kRowsPerGroup = ROWS;
+    typedef uint32_t U4 __attribute__((ext_vector_type(4)));
+    constexpr int kPWaves = ROWS / 16;
     constexpr int KS = D / 32, DT = D / 16;
     constexpr int PAGE = 32 * D;                       // elements of one K (or V) page
-    constexpr int CHUNKS = 2 * PAGE * 2 / 1024;        // 1 KiB chunks of K + V page
-    // Waves 0..kLoaders-1 copy the pages (the largest power of two of waves
-    // that divides the page's chunks).
+    constexpr int PAGE_BYTES = PAGE * 2;
+    // Waves 0..kLoaders-1 copy the pages, H 1 KiB loads each per K (or V)
+    // page (the largest power of two of waves that divides a page's loads).
     constexpr int kLoaders = kPWaves >= 8 ? 8 : kPWaves;
-    constexpr int CPW = CHUNKS / kLoaders;             // chunks (loads) per loader wave per page
-    static_assert(CHUNKS % kLoaders == 0, "chunks divide over the loader waves");
-    __shared__ __attribute__((aligned(16))) KV ring0[2 * PAGE];
-    __shared__ __attribute__((aligned(16))) KV ring1[2 * PAGE];
-    __shared__ __attribute__((aligned(16))) KV ring2[2 * PAGE];
-    __shared__ __attribute__((aligned(16))) KV ring3[2 * PAGE];
+    constexpr int H = PAGE_BYTES / 1024 / kLoaders;
+    static_assert(H >= 1 && PAGE_BYTES / 1024 % kLoaders == 0, "loads divide over the loader waves");
+    __shared__ __attribute__((aligned(16))) KV kring[4 * PAGE];
+    __shared__ __attribute__((aligned(16))) KV vring[4 * PAGE];
 
-    const int lane = threadIdx.x & 63, w = threadIdx.x >> 6, g = lane >> 4;
+    const int lane = threadIdx.x & 63, g = lane >> 4;
+    const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);   // wave index (uniform)
     const int h = blockIdx.x % a.kv_heads;
     const int tile = a.n_tiles - 1 - blockIdx.x / a.kv_heads;        // heaviest first
-    const int row0 = tile * kRowsPerGroup + w * kRowsPerWave;
+    const int row0 = tile * ROWS + w * 16;
 
-    // Query fragments (B operand): tile rt, k-step ks of lane l holds row
-    // row0 + 16*rt + l%16, dims 32*ks + 8*(l/16) .. +7.  Padded rows repeat
-    // the last row; their results are not stored.  They are in registers
-    // before the first page is requested (a workgroup runs for hundreds of
-    // pages, so this one round trip is negligible, and the page loop never
-    // waits on them).
-    V8 qf[RT][KS];
-    int limit[RT];
-#pragma unroll
-    for (int rt = 0; rt < RT; ++rt) {
-        const int row = min(row0 + 16 * rt + (lane & 15), a.rows - 1);
+    // Query fragments (B operand): k-step ks of lane l holds row row0 + l%16,
+    // dims 32*ks + 8*(l/16) .. +7.  Padded rows repeat the last row; their
+    // results are not stored.  They are in registers before the first page
+    // is requested (a workgroup runs for hundreds of pages, so this one round
+    // trip is negligible, and the page loop never waits on them).
+    V8 qf[KS];
+    int limit;
+    {
+        const int row = min(row0 + (lane & 15), a.rows - 1);
         const int t = row / a.group, gg = row - t * a.group;
-        limit[rt] = a.position + t;
+        limit = a.position + t;
         const KV *src = static_cast<const KV *>(a.q) +
                         ((size_t)t * a.q_heads + (size_t)h * a.group + gg) * D + 8 * g;
 #pragma unroll
-        for (int ks = 0; ks < KS; ++ks) qf[rt][ks] = *reinterpret_cast<const V8 *>(src + 32 * ks);
+        for (int ks = 0; ks < KS; ++ks) qf[ks] = *reinterpret_cast<const V8 *>(src + 32 * ks);
     }
     wait_vmcnt<0>();
     // Keys this workgroup can see: 0 .. position + (token of its last row).
-    const int last_row = min(tile * kRowsPerGroup + kRowsPerGroup - 1, a.rows - 1);
+    const int last_row = min(tile * ROWS + ROWS - 1, a.rows - 1);
     const int n_keys = a.position + last_row / a.group + 1;
     const int n = (n_keys + 31) / 32;
-    // First page that any row of this wave masks (all rows see keys <= position).
+    // Pages from which on some row of this wave masks keys (every row sees
+    // the keys up to position + its first row's token).
     const int wave_first_limit = a.position + min(row0, a.rows - 1) / a.group;
 
     const KV *kh = static_cast<const KV *>(a.k_pages) + (size_t)h * a.head_stride;
     const KV *vh = static_cast<const KV *>(a.v_pages) + (size_t)h * a.head_stride;
-    // Loader wave w copies 1 KiB chunks w*CPW .. of the [K | V] page p into
-    // `dst` (the other waves have no loads in flight, so their page waits
-    // below return at once).
-    auto stage = [&](int p, KV *dst) __attribute__((always_inline)) {
+    // Loader wave w copies 1 KiB chunks w*H .. w*H+H-1 of page p into the
+    // ring's buffer p % 4.  Over a run the pages are requested in the order
+    // K0 V0 K1 V1 K2 V2 ..., which the waits below count on.
+    auto stage = [&](const KV *src, int p, KV *ring) __attribute__((always_inline)) {
         if (w >= kLoaders) return;
+        const KV *page = src + (size_t)p * PAGE + w * H * 512;       // uniform
+        KV *buf = ring + (p & 3) * PAGE + w * H * 512;
 #pragma unroll
-        for (int c = 0; c < CPW; ++c) {
-            const int chunk = w * CPW + c;
-            const int half = chunk / (CHUNKS / 2), off = (chunk % (CHUNKS / 2)) * 512;
-            const KV *src = (half ? vh : kh) + (size_t)p * PAGE + off + lane * 8;
-            __builtin_amdgcn_global_load_lds(reinterpret_cast<const void *>(src),
-                                             (__attribute__((address_space(3))) void *)(dst + half * PAGE + off),
-                                             16, 0, 0);
+        for (int c = 0; c < H; ++c)
+            __builtin_amdgcn_global_load_lds(reinterpret_cast<const void *>(page + c * 512 + lane * 8),
+                                             (__attribute__((address_space(3))) void *)(buf + c * 512), 16, 0, 0);
+    };
+    const uint32_t kring_lane = lds_addr(kring) + lane * 16;
+    const uint32_t vring_lane = lds_addr(vring) + lane * 16;
+
+    f32x4 acc[DT];
+#pragma unroll
+    for (int dt = 0; dt < DT; ++dt) acc[dt] = f32x4{0.f, 0.f, 0.f, 0.f};
+    float m = -INFINITY, l = 0.f;
+    f32x4 s[2];            // scores of the page whose softmax comes next
+
+    // ---- S^T of one page, chunk by chunk ----
+    // K fragments stream through a window of two k-steps (four reads in
+    // flight): the pair of k-step ks+2 is requested as soon as that of ks
+    // has landed; the two key tiles are two independent accumulation chains.
+    V8 kf[KS][2];
+    auto read_k = [&](auto ks_, uint32_t kb) __attribute__((always_inline)) {
+        constexpr int ks = decltype(ks_)::value;
+        if constexpr (ks < KS) {
+            lds_read<ks * 512 * 2>(kf[ks][0], kb);
+            lds_read<(16 * D + ks * 512) * 2>(kf[ks][1], kb);
+        }
+    };
+    auto qk_chunk = [&](auto ks_, uint32_t kb, f32x4 *sn) __attribute__((always_inline)) {
+        constexpr int ks = decltype(ks_)::value;
+        if constexpr (ks < KS) {
+            constexpr int later = ks + 2 < KS ? 2 : 2 * (KS - 1 - ks);
+            lds_wait<later>(kf[ks][0], kf[ks][1]);
+            read_k(std::integral_constant<int, ks + 2>{}, kb);
+            sn[0] = mfma(kf[ks][0], qf[ks], sn[0]);
+            sn[1] = mfma(kf[ks][1], qf[ks], sn[1]);
         }
     };
 
-    f32x4 acc[RT][DT];
-    float m[RT], l[RT];
+    // ---- one pipeline step: S^T of page i+1, softmax and P.V of page i ----
+    // (On a workgroup's last step the scores of the page after the last are
+    // computed from a stale buffer and dropped.)
+    auto step = [&](int i) __attribute__((always_inline)) {
+        const uint32_t kb = kring_lane + ((i + 1) & 3) * PAGE_BYTES;
+        const uint32_t vb = vring_lane + (i & 3) * PAGE_BYTES;
+        f32x4 sn[2] = {f32x4{0.f, 0.f, 0.f, 0.f}, f32x4{0.f, 0.f, 0.f, 0.f}};
+        read_k(std::integral_constant<int, 0>{}, kb);
+        read_k(std::integral_constant<int, 1>{}, kb);
+        // Scores of page i; keys past a row's limit are masked.
+        float x[8];
 #pragma unroll
-    for (int rt = 0; rt < RT; ++rt) {
-        m[rt] = -INFINITY;
-        l[rt] = 0.f;
-#pragma unroll
-        for (int dt = 0; dt < DT; ++dt) acc[rt][dt] = f32x4{0.f, 0.f, 0.f, 0.f};
-    }
-
-    auto compute = [&](int p, const KV *cur) __attribute__((always_inline)) {
-        const uint32_t kbase = lds_addr(cur) + lane * 16;
-        const uint32_t vbase = lds_addr(cur) + PAGE * 2 + lane * 16;
-        // ---- S^T for both 16-key tiles of the page and all row tiles ----
-        // K fragments stream through a window of KW k-steps (2*KW reads in
-        // flight, at most 15): the pair of k-step ks+KW is requested as soon
-        // as that of ks has landed, and each pair feeds 2*RT independent
-        // accumulation chains (row tile x key tile).
-        constexpr int KW = 2;
-        V8 kf[KS][2];
-        auto read_k = [&](auto ks) __attribute__((always_inline)) {
-            static_for<0, 2>([&](auto kt) {
-                lds_read<(decltype(kt)::value * 16 * D + decltype(ks)::value * 512) * 2>(
-                    kf[decltype(ks)::value][decltype(kt)::value], kbase);
-            });
-        };
-        static_for<0, KW>(read_k);
-        f32x4 s[RT][2];
-#pragma unroll
-        for (int rt = 0; rt < RT; ++rt) s[rt][0] = s[rt][1] = f32x4{0.f, 0.f, 0.f, 0.f};
-        static_for<0, KS>([&](auto ks_) {
-            constexpr int ks = decltype(ks_)::value;
-            // Reads issued after this pair: the rest of the window.
-            constexpr int later = 2 * (ks + KW <= KS ? KW - 1 : KS - 1 - ks);
-            lds_wait<later>(kf[ks][0]);
-            lds_wait<later>(kf[ks][1]);
-            if constexpr (ks + KW < KS) read_k(std::integral_constant<int, ks + KW>{});
-#pragma unroll
-            for (int kt = 0; kt < 2; ++kt)
-#pragma unroll
-                for (int rt = 0; rt < RT; ++rt) s[rt][kt] = mfma(kf[ks][kt], qf[rt][ks], s[rt][kt]);
-        });
-        // The first VW V fragments are requested now and arrive during the
-        // softmax; the rest stream through the same window during O^T.
-        constexpr int VW = 4;
-        V8 vf[DT];
-        auto read_v = [&](auto dt) __attribute__((always_inline)) {
-            lds_read<decltype(dt)::value * 1024>(vf[decltype(dt)::value], vbase);
-        };
-        static_for<0, VW>(read_v);
-        // ---- online softmax; keys past a row's limit are masked ----
-        V8 ph[RT], pl[RT];
-        bool rescale = false;
-        float alpha[RT];
-#pragma unroll
-        for (int rt = 0; rt < RT; ++rt) {
-            float x[8];
-#pragma unroll
-            for (int j = 0; j < 8; ++j) x[j] = s[rt][j >> 2][j & 3] * a.scale_log2;
-            if (p * 32 + 31 > wave_first_limit) {
-                keep_branch();
-#pragma unroll
-                for (int j = 0; j < 8; ++j)
-                    if (p * 32 + 16 * (j >> 2) + 4 * g + (j & 3) > limit[rt]) x[j] = -INFINITY;
-            }
-            const float bm = row_group_max(fmaxf(fmaxf(fmaxf(x[0], x[1]), fmaxf(x[2], x[3])),
-                                                 fmaxf(fmaxf(x[4], x[5]), fmaxf(x[6], x[7]))));
-            alpha[rt] = 1.f;
-            if (bm > m[rt] + kLazy) {
-                alpha[rt] = __builtin_amdgcn_exp2f(m[rt] - bm);
-                m[rt] = bm;
-                rescale = true;
-            }
-            const float mu = m[rt] == -INFINITY ? 0.f : m[rt];
-            float ps = 0.f;
-#pragma unroll
-            for (int j = 0; j < 8; ++j) {
-                const float e = __builtin_amdgcn_exp2f(x[j] - mu);
-                const KV eh = (KV)e;
-                ph[rt][j] = eh;
-                if constexpr (PSPLIT) {
-                    pl[rt][j] = (KV)(e - (float)eh);
-                    ps += e;
-                } else {
-                    ps += (float)eh;
-                }
-            }
-            l[rt] = l[rt] * alpha[rt] + ps;
-        }
-        if (__any(rescale)) {
+        for (int j = 0; j < 8; ++j) x[j] = s[j >> 2][j & 3];
+        if (i * 32 + 31 > wave_first_limit) {
             keep_branch();
 #pragma unroll
-            for (int rt = 0; rt < RT; ++rt)
+            for (int j = 0; j < 8; ++j)
+                if (i * 32 + 16 * (j >> 2) + 4 * g + (j & 3) > limit) x[j] = -INFINITY;
+        }
+        float mx = __builtin_fmaxf(max3(x[0], x[1], x[2]), max3(x[3], x[4], x[5]));
+        mx = max3(mx, x[6], x[7]);
+        pin(mx);
+        qk_chunk(std::integral_constant<int, 0>{}, kb, sn);
+        // Row max over the four lane groups (key subsets) of the row.
+        mx = row_group_max(mx);
+        pin(mx);
+        qk_chunk(std::integral_constant<int, 1>{}, kb, sn);
+        // Every row sees key 0, so the max is finite from the first page on.
+        const float bm = mx * a.scale_log2;
+        float alpha = 1.f;
+        const bool moved = bm > m + kLazy;
+        if (moved) alpha = __builtin_amdgcn_exp2f(m - bm);
+        m = moved ? bm : m;
+        float e[8];
+        pin(alpha, m);
+        qk_chunk(std::integral_constant<int, 2>{}, kb, sn);
 #pragma unroll
-                for (int dt = 0; dt < DT; ++dt) acc[rt][dt] *= alpha[rt];
+        for (int j = 0; j < 4; ++j) e[j] = __builtin_amdgcn_exp2f(__builtin_fmaf(x[j], a.scale_log2, -m));
+        pin(e[0], e[1], e[2], e[3]);
+        qk_chunk(std::integral_constant<int, 3>{}, kb, sn);
+#pragma unroll
+        for (int j = 4; j < 8; ++j) e[j] = __builtin_amdgcn_exp2f(__builtin_fmaf(x[j], a.scale_log2, -m));
+        pin(e[4], e[5], e[6], e[7]);
+        qk_chunk(std::integral_constant<int, 4>{}, kb, sn);
+        // P^T as B operands: hi parts (and lo parts, bf16).
+        uint32_t ph[4], pl[4] = {};
+#pragma unroll
+        for (int j = 0; j < 4; j += 2) {
+            ph[j / 2] = pack2(e[j], e[j + 1], KV{});
+            if constexpr (PSPLIT) {
+                pl[j / 2] = pack2(e[j] - bf16_lo(ph[j / 2]), e[j + 1] - bf16_hi(ph[j / 2]), KV{});
+            }
+        }
+        pin(ph[0], ph[1]);
+        if constexpr (PSPLIT) pin(pl[0], pl[1]);
+        qk_chunk(std::integral_constant<int, 5>{}, kb, sn);
+#pragma unroll
+        for (int j = 4; j < 8; j += 2) {
+            ph[j / 2] = pack2(e[j], e[j + 1], KV{});
+            if constexpr (PSPLIT) {
+                pl[j / 2] = pack2(e[j] - bf16_lo(ph[j / 2]), e[j + 1] - bf16_hi(ph[j / 2]), KV{});
+            }
+        }
+        pin(ph[2], ph[3]);
+        if constexpr (PSPLIT) pin(pl[2], pl[3]);
+        qk_chunk(std::integral_constant<int, 6>{}, kb, sn);
+        l = l * alpha + (((e[0] + e[1]) + (e[2] + e[3])) + ((e[4] + e[5]) + (e[6] + e[7])));
+        pin(l);
+        qk_chunk(std::integral_constant<int, 7>{}, kb, sn);
+        static_for<8, KS>([&](auto ks) { qk_chunk(ks, kb, sn); });
+        const V8 p_hi = __builtin_bit_cast(V8, U4{ph[0], ph[1], ph[2], ph[3]});
+        const V8 p_lo = __builtin_bit_cast(V8, U4{pl[0], pl[1], pl[2], pl[3]});
+
+        // ---- O^T += V^T P^T for page i ----
+        // V fragments stream through a window of VW reads.
+        constexpr int VW = 4;
+        V8 vf[DT];
+        auto read_v = [&](auto dt_) __attribute__((always_inline)) {
+            constexpr int dt = decltype(dt_)::value;
+            if constexpr (dt < DT) lds_read<dt * 1024>(vf[dt], vb);
+        };
+        static_for<0, VW>(read_v);
+        if (__any(moved)) {
+            keep_branch();
+#pragma unroll
+            for (int dt = 0; dt < DT; ++dt) acc[dt] *= alpha;
         }
         // Last page: V slots past the last key are zeroed (stale pages may
         // hold anything, and 0 * NaN is NaN).
-        const bool tail = p * 32 + 32 > n_keys;
-        // ---- O^T += V^T P^T ----
-        static_for<0, DT>([&](auto dt_) {
-            constexpr int dt = decltype(dt_)::value;
-            constexpr int later = dt + VW <= DT ? VW - 1 : DT - 1 - dt;
-            lds_wait<later>(vf[dt]);
-            if constexpr (dt + VW < DT) read_v(std::integral_constant<int, dt + VW>{});
+        const bool tail = i * 32 + 32 > n_keys;
+        // Pairs of tiles: the hi and lo products of a tile accumulate into
+        // the same registers, so they are issued two apart.
+        static_for<0, DT / 2>([&](auto dp_) {
+            constexpr int dt = 2 * decltype(dp_)::value;
+            constexpr int later = dt + 2 + VW <= DT + 2 ? VW - 2 : DT - 2 - dt;
+            lds_wait<later>(vf[dt], vf[dt + 1]);
+            read_v(std::integral_constant<int, dt + VW>{});
+            read_v(std::integral_constant<int, dt + VW + 1>{});
             if (tail) {
                 keep_branch();
 #pragma unroll
                 for (int j = 0; j < 8; ++j)
-                    if (p * 32 + v_slot_token(g, j) >= n_keys) vf[dt][j] = (KV)0.f;
+                    if (i * 32 + v_slot_token(g, j) >= n_keys) {
+                        vf[dt][j] = (KV)0.f;
+                        vf[dt + 1][j] = (KV)0.f;
+                    }
             }
-#pragma unroll
-            for (int rt = 0; rt < RT; ++rt) {
-                acc[rt][dt] = mfma(vf[dt], ph[rt], acc[rt][dt]);
-                if constexpr (PSPLIT) acc[rt][dt] = mfma(vf[dt], pl[rt], acc[rt][dt]);
+            acc[dt] = mfma(vf[dt], p_hi, acc[dt]);
+            acc[dt + 1] = mfma(vf[dt + 1], p_hi, acc[dt + 1]);
+            if constexpr (PSPLIT) {
+                acc[dt] = mfma(vf[dt], p_lo, acc[dt]);
+                acc[dt + 1] = mfma(vf[dt + 1], p_lo, acc[dt + 1]);
             }
         });
+        s[0] = sn[0];
+        s[1] = sn[1];
     };
 
-    auto wait_page = [&](int i) __attribute__((always_inline)) {
-        const int ahead = min(2, n - 1 - i);
-        if (ahead >= 2) wait_vmcnt<2 * CPW>();
-        else if (ahead == 1) wait_vmcnt<CPW>();
+    // ---- prologue: pages 0..3 requested, S^T of page 0 ----
+    stage(kh, 0, kring);
+    stage(vh, 0, vring);
+    if (n > 1) { stage(kh, 1, kring); stage(vh, 1, vring); }
+    if (n > 2) { stage(kh, 2, kring); stage(vh, 2, vring); }
+    if (n > 3) stage(kh, 3, kring);
+    // K0 has landed once at most the requests after it are in flight.
+    if (n > 3) wait_vmcnt<6 * H>();
+    else if (n > 2) wait_vmcnt<5 * H>();
+    else if (n > 1) wait_vmcnt<3 * H>();
+    else wait_vmcnt<H>();
+    ring_barrier();
+    s[0] = s[1] = f32x4{0.f, 0.f, 0.f, 0.f};
+    read_k(std::integral_constant<int, 0>{}, kring_lane);
+    read_k(std::integral_constant<int, 1>{}, kring_lane);
+    static_for<0, KS>([&](auto ks) { qk_chunk(ks, kring_lane, s); });
+
+    // Step i: K(i+1) and V(i) have landed (requests after K(i+1): V(i+1),
+    // K(i+2), V(i+2), K(i+3), those that exist), the waves meet (so K(i)
+    // and V(i-1) are consumed), V(i+3) and K(i+4) are requested into the
+    // buffers just freed, and the step runs.
+    for (int i = 0; i < n; ++i) {
+        const int ahead = n - 1 - i;
+        if (ahead >= 3) wait_vmcnt<4 * H>();
+        else if (ahead == 2) wait_vmcnt<3 * H>();
+        else if (ahead == 1) wait_vmcnt<H>();
         else wait_vmcnt<0>();
-    };
-    // Step i: this wave's share of page i has landed (pages i+1 and i+2 may
-    // stay in flight), the waves meet (page i complete, page i-1 consumed),
-    // the consumed buffer is refilled with page i+3, and page i is consumed.
-    auto step = [&](int i, const KV *cur, KV *fill) __attribute__((always_inline)) {
-        wait_page(i);
         ring_barrier();
-        if (i + 3 < n) stage(i + 3, fill);
-        compute(i, cur);
-    };
-
-    stage(0, ring0);
-    if (n > 1) stage(1, ring1);
-    if (n > 2) stage(2, ring2);
-    for (int i = 0; i < n; i += 4) {
-        step(i, ring0, ring3);
-        if (i + 1 < n) step(i + 1, ring1, ring0);
-        if (i + 2 < n) step(i + 2, ring2, ring1);
-        if (i + 3 < n) step(i + 3, ring3, ring2);
+        if (i + 3 < n) stage(vh, i + 3, vring);
+        if (i + 4 < n) stage(kh, i + 4, kring);
+        step(i);
     }
 
     // ---- normalise and store rows ----
+    l = row_group_sum(l);
+    const int row = row0 + (lane & 15);
+    if (row < a.rows) {
+        const int t = row / a.group, gg = row - t * a.group;
+        OUT *dst = static_cast<OUT *>(a.out) + ((size_t)t * a.q_heads + (size_t)h * a.group + gg) * D + 4 * g;
+        const float inv = 1.f / l;
 #pragma unroll
-    for (int rt = 0; rt < RT; ++rt) {
-        l[rt] = row_group_sum(l[rt]);
-        const int row = row0 + 16 * rt + (lane & 15);
-        if (row < a.rows) {
-            const int t = row / a.group, gg = row - t * a.group;
-            OUT *dst = static_cast<OUT *>(a.out) + ((size_t)t * a.q_heads + (size_t)h * a.group + gg) * D + 4 * g;
-            const float inv = 1.f / l[rt];
+        for (int dt = 0; dt < DT; ++dt) {
+            typedef OUT OUT4 __attribute__((ext_vector_type(4)));
+            OUT4 o;
 #pragma unroll
-            for (int dt = 0; dt < DT; ++dt) {
-                typedef OUT OUT4 __attribute__((ext_vector_type(4)));
-                OUT4 o;
-#pragma unroll
-                for (int r = 0; r < 4; ++r) o[r] = (OUT)(acc[rt][dt][r] * inv);
-                *reinterpret_cast<OUT4 *>(dst + dt * 16) = o;
-            }
+            for (int r = 0; r < 4; ++r) o[r] = (OUT)(acc[dt][r] * inv);
+            *reinterpret_cast<OUT4 *>(dst + dt * 16) = o;
         }
     }
 }
 
-// Row tiles per wave: one.  Rows per workgroup: 192 (twelve waves, three
-// per SIMD, whose softmax and matrix work overlap; and 2048 tokens of six
+// Rows per workgroup: 192 (twelve waves, three per SIMD; 2048 tokens of six
 // query heads per KV head make 64 workgroups per KV head, one round on 256
 // CUs) or 128 (RS_PREFILL_ROWS=128, for measurement).
-constexpr int kPrefillRT = 1;
-
 int prefill_rows() {
     static const int rows = [] {
         const char *v = std::getenv("RS_PREFILL_ROWS");
@@ -313,12 +376,11 @@ int prefill_rows() {
 
 template <int D, int ROWS>
 const void *prefill_kernel(Dtype dtype, bool out_f32) {
-    constexpr int RT = kPrefillRT;
     if (dtype == Dtype::BF16)
-        return out_f32 ? (const void *)&attention_prefill<D, __bf16, true, float, RT, ROWS>
-                       : (const void *)&attention_prefill<D, __bf16, true, __bf16, RT, ROWS>;
-    return out_f32 ? (const void *)&attention_prefill<D, _Float16, false, float, RT, ROWS>
-                   : (const void *)&attention_prefill<D, _Float16, false, _Float16, RT, ROWS>;
+        return out_f32 ? (const void *)&attention_prefill<D, __bf16, true, float, ROWS>
+                       : (const void *)&attention_prefill<D, __bf16, true, __bf16, ROWS>;
+    return out_f32 ? (const void *)&attention_prefill<D, _Float16, false, float, ROWS>
+                   : (const void *)&attention_prefill<D, _Float16, false, _Float16, ROWS>;
 }
 
 template <int D>
@@ -348,7 +410,7 @@ void launch_prefill(const Shape &s, Dtype dtype, float scale, const void *q, con
                        : s.head_dim == 128 ? prefill_kernel<128>(dtype, out_f32, rows) : nullptr;
     require(kernel != nullptr, "unsupported head_dim for the prefill kernel");
     void *args[] = {&a};
-    const int threads = (rows / (16 * kPrefillRT)) * kWave;
+    const int threads = (rows / 16) * kWave;
     check(hipLaunchKernel(kernel, dim3(a.n_tiles * s.kv_heads), dim3(threads), args, 0, stream));
 }
 
