@@ -128,7 +128,7 @@ int qv_attention_workspace(uint64_t *bytes, int q_heads, int kv_heads, int head_
  * 256; G <= 48; 1 <= tokens; position+tokens <= capacity. Up to 48 query
  * rows per KV head (G*tokens): split-K over all CUs plus a log-sum-exp
  * combine (qv_attention_split then qv_attention_combine). More rows (chunked
- * prefill): one workgroup per 128 rows streams the visible pages through LDS;
+ * prefill): one workgroup per 192 rows streams the visible pages through LDS;
  * the workspace is then 0 bytes and may be NULL. */
 int qv_attention(void *out, const void *q, const void *k_pages, const void *v_pages,
                  int dtype, int out_dtype, int q_heads, int kv_heads, int head_dim,
@@ -150,7 +150,10 @@ int qv_attention_fused_workspace(uint64_t *bytes, int batch, int position);
  * on the paged fp16 cache: RMSNorm + RoPE of q/k, fp16 append of k/v at
  * position..position+batch-1, causal GQA attention (scale 1/16), times
  * sigmoid(gate). Shapes as qv_test_attention, all float32 device buffers;
- * the caches are fp16 pages with 24/4/256 geometry. */
+ * the caches are fp16 pages with 24/4/256 geometry. batch is 1..8 as in the
+ * reference, or a prefill chunk of up to 8192 tokens (the reference's server
+ * prefills in 8-token steps, qvelox/server.py:177-192): more than 8 tokens
+ * run the chunked-prefill kernel with the same fp32-query precision. */
 int qv_attention_fused(float *out, void *k_pages, void *v_pages,
                        const float *q_gate, const float *key, const float *value,
                        const float *q_norm, const float *k_norm,

@@ -60,6 +60,11 @@ void download(void *host, const void *device, size_t size) {
 void batch_size(int batch) {
     require(batch >= 1 && batch <= 8, "batch must be between 1 and 8");
 }
+// The device fused entry also takes prefill chunks of up to kMaxFusedTokens.
+constexpr int kMaxFusedTokens = 8192;
+void fused_batch_size(int batch) {
+    require(batch >= 1 && batch <= kMaxFusedTokens, "batch must be between 1 and 8192");
+}
 void epsilon_value(float epsilon) {
     require(std::isfinite(epsilon) && epsilon > 0, "epsilon must be finite and positive");
 }
@@ -102,16 +107,17 @@ void fits_cache(const rs::Shape &s) {
     require((long long)s.position + s.tokens <= s.capacity, "position+tokens exceeds the cache capacity");
 }
 
-// Run split + combine over token chunks of at most kMaxRows query rows per
-// KV head; every chunk reuses the workspace in stream order.  q (and q_lo,
+// More than kMaxRows query rows per KV head: the prefill kernel.  Otherwise
+// split + combine over token chunks of at most kMaxRows query rows per KV
+// head; every chunk reuses the workspace in stream order.  q (and q_lo,
 // the lo part of a precise query) are 16-bit [tokens][q_heads][D].
 void run_attention(const rs::Shape &s, rs::Dtype dtype, bool precise, float scale,
                    const void *q, const void *q_lo, const void *k_pages, const void *v_pages,
                    void *workspace, void *out, bool out_f32, const float *gate,
                    hipStream_t stream) {
-    if (!precise && s.group() * s.tokens > rs::kMaxRows) {
+    if (s.group() * s.tokens > rs::kMaxRows) {
         // Long token runs (chunked prefill): one launch, no workspace.
-        rs::launch_prefill(s, dtype, scale, q, k_pages, v_pages, out, out_f32, stream);
+        rs::launch_prefill(s, dtype, precise, scale, q, q_lo, k_pages, v_pages, out, out_f32, gate, stream);
         return;
     }
     const size_t out_elem = out_f32 ? sizeof(float) : sizeof(uint16_t);
@@ -386,7 +392,7 @@ static size_t fused_workspace(int batch, int position) {
 extern "C" int qv_attention_fused_workspace(uint64_t *bytes, int batch, int position) {
     return call([&] {
         require(bytes != nullptr, "null bytes output");
-        batch_size(batch);
+        fused_batch_size(batch);
         require(position >= 0 && position <= rs::kModelCapacity - batch,
                 "attention context exceeds 139264");
         *bytes = fused_workspace(batch, position);
@@ -399,7 +405,7 @@ extern "C" int qv_attention_fused(float *out, void *k_pages, void *v_pages,
                                   int batch, int position, int capacity, float epsilon,
                                   void *workspace, uint64_t workspace_bytes, void *stream) {
     return call([&] {
-        batch_size(batch);
+        fused_batch_size(batch);
         epsilon_value(epsilon);
         require(position >= 0 && position <= rs::kModelCapacity - batch,
                 "attention context exceeds 139264");

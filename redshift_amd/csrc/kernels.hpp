@@ -73,9 +73,13 @@ void launch_combine(const Shape &s, const SplitPlan &plan, Dtype dtype,
                     hipStream_t stream);
 
 // Chunked prefill: all group*tokens query rows against the pages in one
-// launch (no workspace); `dtype` q and out, [tokens][q_heads][D].
-void launch_prefill(const Shape &s, Dtype dtype, float scale, const void *q, const void *k_pages,
-                    const void *v_pages, void *out, bool out_f32, hipStream_t stream);
+// launch (no workspace); `dtype` q and out, [tokens][q_heads][D].  A precise
+// call (fp16 pages) takes the query as hi + lo fp16 parts and writes fp32,
+// times sigmoid of the gate half of q_gate [tokens][q_heads][2D] when `gate`
+// is given.
+void launch_prefill(const Shape &s, Dtype dtype, bool precise, float scale, const void *q,
+                    const void *q_lo, const void *k_pages, const void *v_pages, void *out, bool out_f32,
+                    const float *gate, hipStream_t stream);
 
 // Whole pages 0 .. pages-1 of every KV head, K and V, from caches of
 // src_capacity tokens to caches of dst_capacity tokens (checkpoint/restore).

@@ -30,12 +30,14 @@
 // round-robin dispatch over the 8 XCDs keeps every head on the same two XCDs,
 // whose L2s then hold that head's pages for all of its workgroups), and row
 // tiles go heaviest (latest rows, most keys) first.
+#include "combine.hpp"
 #include "kernels.hpp"
 #include "lds.hpp"
 
 #include <algorithm>
 #include <cmath>
 #include <cstdlib>
+#include <type_traits>
 
 namespace rs {
 namespace {
@@ -76,18 +78,28 @@ __device__ __forceinline__ uint32_t pack2(float a, float b, __bf16) {
     typedef __bf16 b2 __attribute__((ext_vector_type(2)));
     return __builtin_bit_cast(uint32_t, b2{(__bf16)a, (__bf16)b});
 }
-// The two bf16 halves of a packed word as fp32 values.  The low half is moved
+// The two halves of a packed word as fp32 values.  A bf16 low half is moved
 // up with a byte permute (bytes 1:0 to 3:2, zeros below), which keeps the
 // compiler from converting the fp32 input a second time instead.
-__device__ __forceinline__ float bf16_lo(uint32_t w) {
+__device__ __forceinline__ float unpack_lo(uint32_t w, __bf16) {
     return __uint_as_float(__builtin_amdgcn_perm(0u, w, 0x01000c0cu));
 }
-__device__ __forceinline__ float bf16_hi(uint32_t w) { return __uint_as_float(w & 0xffff0000u); }
+__device__ __forceinline__ float unpack_hi(uint32_t w, __bf16) { return __uint_as_float(w & 0xffff0000u); }
+__device__ __forceinline__ float unpack_lo(uint32_t w, _Float16) {
+    typedef _Float16 h2 __attribute__((ext_vector_type(2)));
+    return (float)__builtin_bit_cast(h2, w)[0];
+}
+__device__ __forceinline__ float unpack_hi(uint32_t w, _Float16) {
+    typedef _Float16 h2 __attribute__((ext_vector_type(2)));
+    return (float)__builtin_bit_cast(h2, w)[1];
+}
 
 constexpr float kLazy = 8.f;
 
 struct PrefillArgs {
     const void *q;
+    const void *q_lo;       // lo parts of a precise (fp32) query, or null
+    const float *gate;      // q_gate of a gated output, or null
     const void *k_pages;
     const void *v_pages;
     void *out;
@@ -100,10 +112,14 @@ __device__ __forceinline__ int v_slot_token(int g, int j) {
     return j < 4 ? 4 * g + j : 16 + 4 * g + j - 4;
 }
 
-template <int D, typename KV, bool PSPLIT, typename OUT, int ROWS>
+// PSPLIT: P multiplies V as hi + lo 16-bit parts.  QSPLIT: the query is an
+// fp32 one given as hi + lo fp16 parts, both multiplied by K.  MODE: output
+// of the KV type, fp32, or fp32 times sigmoid(gate) (see combine.hpp).
+template <int D, typename KV, bool PSPLIT, bool QSPLIT, int MODE, int ROWS>
 __global__ __launch_bounds__(ROWS / 16 * kWave, 1)
 void attention_prefill(PrefillArgs a) {
     using V8 = typename Vec8<KV>::type;
+    using OUT = std::conditional_t<MODE == kOutSame, KV, float>;
     typedef uint32_t U4 __attribute__((ext_vector_type(4)));
     constexpr int kPWaves = ROWS / 16;
     constexpr int KS = D / 32, DT = D / 16;
@@ -128,7 +144,7 @@ void attention_prefill(PrefillArgs a) {
     // results are not stored.  They are in registers before the first page
     // is requested (a workgroup runs for hundreds of pages, so this one round
     // trip is negligible, and the page loop never waits on them).
-    V8 qf[KS];
+    V8 qf[KS], qlo[QSPLIT ? KS : 1];
     int limit;
     {
         const int row = min(row0 + (lane & 15), a.rows - 1);
@@ -138,6 +154,11 @@ void attention_prefill(PrefillArgs a) {
                         ((size_t)t * a.q_heads + (size_t)h * a.group + gg) * D + 8 * g;
 #pragma unroll
         for (int ks = 0; ks < KS; ++ks) qf[ks] = *reinterpret_cast<const V8 *>(src + 32 * ks);
+        if constexpr (QSPLIT) {
+            const KV *lo = static_cast<const KV *>(a.q_lo) + (src - static_cast<const KV *>(a.q));
+#pragma unroll
+            for (int ks = 0; ks < KS; ++ks) qlo[ks] = *reinterpret_cast<const V8 *>(lo + 32 * ks);
+        }
     }
     wait_vmcnt<0>();
     // Keys this workgroup can see: 0 .. position + (token of its last row).
@@ -191,6 +212,10 @@ void attention_prefill(PrefillArgs a) {
             read_k(std::integral_constant<int, ks + 2>{}, kb);
             sn[0] = mfma(kf[ks][0], qf[ks], sn[0]);
             sn[1] = mfma(kf[ks][1], qf[ks], sn[1]);
+            if constexpr (QSPLIT) {
+                sn[0] = mfma(kf[ks][0], qlo[ks], sn[0]);
+                sn[1] = mfma(kf[ks][1], qlo[ks], sn[1]);
+            }
         }
     };
 
@@ -244,7 +269,7 @@ void attention_prefill(PrefillArgs a) {
         for (int j = 0; j < 4; j += 2) {
             ph[j / 2] = pack2(e[j], e[j + 1], KV{});
             if constexpr (PSPLIT) {
-                pl[j / 2] = pack2(e[j] - bf16_lo(ph[j / 2]), e[j + 1] - bf16_hi(ph[j / 2]), KV{});
+                pl[j / 2] = pack2(e[j] - unpack_lo(ph[j / 2], KV{}), e[j + 1] - unpack_hi(ph[j / 2], KV{}), KV{});
             }
         }
         pin(ph[0], ph[1]);
@@ -254,7 +279,7 @@ void attention_prefill(PrefillArgs a) {
         for (int j = 4; j < 8; j += 2) {
             ph[j / 2] = pack2(e[j], e[j + 1], KV{});
             if constexpr (PSPLIT) {
-                pl[j / 2] = pack2(e[j] - bf16_lo(ph[j / 2]), e[j + 1] - bf16_hi(ph[j / 2]), KV{});
+                pl[j / 2] = pack2(e[j] - unpack_lo(ph[j / 2], KV{}), e[j + 1] - unpack_hi(ph[j / 2], KV{}), KV{});
             }
         }
         pin(ph[2], ph[3]);
@@ -352,12 +377,20 @@ void attention_prefill(PrefillArgs a) {
         const int t = row / a.group, gg = row - t * a.group;
         OUT *dst = static_cast<OUT *>(a.out) + ((size_t)t * a.q_heads + (size_t)h * a.group + gg) * D + 4 * g;
         const float inv = 1.f / l;
+        // Gated output: times sigmoid(q_gate[t][head][D + d]) (rows of 2D).
+        const float *gate = MODE == kOutGated
+            ? a.gate + ((size_t)t * a.q_heads + (size_t)h * a.group + gg) * 2 * D + D + 4 * g : nullptr;
 #pragma unroll
         for (int dt = 0; dt < DT; ++dt) {
             typedef OUT OUT4 __attribute__((ext_vector_type(4)));
             OUT4 o;
 #pragma unroll
             for (int r = 0; r < 4; ++r) o[r] = (OUT)(acc[dt][r] * inv);
+            if constexpr (MODE == kOutGated) {
+                const f32x4 gv = *reinterpret_cast<const f32x4 *>(gate + dt * 16);
+#pragma unroll
+                for (int r = 0; r < 4; ++r) o[r] *= 1.f / (1.f + expf(-gv[r]));
+            }
             *reinterpret_cast<OUT4 *>(dst + dt * 16) = o;
         }
     }
@@ -365,7 +398,9 @@ void attention_prefill(PrefillArgs a) {
 
 // Rows per workgroup: 192 (twelve waves, three per SIMD; 2048 tokens of six
 // query heads per KV head make 64 workgroups per KV head, one round on 256
-// CUs) or 128 (RS_PREFILL_ROWS=128, for measurement).
+// CUs) or 128 (RS_PREFILL_ROWS=128, for measurement).  A precise query (hi +
+// lo parts) needs twice the query registers: 128 rows (eight waves, two per
+// SIMD).
 int prefill_rows() {
     static const int rows = [] {
         const char *v = std::getenv("RS_PREFILL_ROWS");
@@ -377,10 +412,10 @@ int prefill_rows() {
 template <int D, int ROWS>
 const void *prefill_kernel(Dtype dtype, bool out_f32) {
     if (dtype == Dtype::BF16)
-        return out_f32 ? (const void *)&attention_prefill<D, __bf16, true, float, ROWS>
-                       : (const void *)&attention_prefill<D, __bf16, true, __bf16, ROWS>;
-    return out_f32 ? (const void *)&attention_prefill<D, _Float16, false, float, ROWS>
-                   : (const void *)&attention_prefill<D, _Float16, false, _Float16, ROWS>;
+        return out_f32 ? (const void *)&attention_prefill<D, __bf16, true, false, kOutF32, ROWS>
+                       : (const void *)&attention_prefill<D, __bf16, true, false, kOutSame, ROWS>;
+    return out_f32 ? (const void *)&attention_prefill<D, _Float16, false, false, kOutF32, ROWS>
+                   : (const void *)&attention_prefill<D, _Float16, false, false, kOutSame, ROWS>;
 }
 
 template <int D>
@@ -388,12 +423,25 @@ const void *prefill_kernel(Dtype dtype, bool out_f32, int rows) {
     return rows == 128 ? prefill_kernel<D, 128>(dtype, out_f32) : prefill_kernel<D, 192>(dtype, out_f32);
 }
 
+// The fused model path: fp16 pages, fp32 query as hi + lo parts, hi + lo P
+// (the same precision as the split kernels' precise instance).
+template <int D>
+const void *precise_prefill_kernel(bool gated) {
+    return gated ? (const void *)&attention_prefill<D, _Float16, true, true, kOutGated, 128>
+                 : (const void *)&attention_prefill<D, _Float16, true, true, kOutF32, 128>;
+}
+
 }  // namespace
 
-void launch_prefill(const Shape &s, Dtype dtype, float scale, const void *q, const void *k_pages,
-                    const void *v_pages, void *out, bool out_f32, hipStream_t stream) {
+void launch_prefill(const Shape &s, Dtype dtype, bool precise, float scale, const void *q,
+                    const void *q_lo, const void *k_pages, const void *v_pages, void *out, bool out_f32,
+                    const float *gate, hipStream_t stream) {
+    require(!gate || precise, "a gated prefill needs the precise query");
+    require(!precise || (dtype == Dtype::F16 && out_f32 && q_lo), "a precise prefill runs on fp16 pages with fp32 output");
     PrefillArgs a;
     a.q = q;
+    a.q_lo = q_lo;
+    a.gate = gate;
     a.k_pages = k_pages;
     a.v_pages = v_pages;
     a.out = out;
@@ -403,10 +451,11 @@ void launch_prefill(const Shape &s, Dtype dtype, float scale, const void *q, con
     a.group = s.group();
     a.rows = s.group() * s.tokens;
     a.position = s.position;
-    const int rows = prefill_rows();
+    const int rows = precise ? 128 : prefill_rows();
     a.n_tiles = (a.rows + rows - 1) / rows;
     a.scale_log2 = scale * 1.4426950408889634f;
-    const void *kernel = s.head_dim == 256 ? prefill_kernel<256>(dtype, out_f32, rows)
+    const void *kernel = precise ? (s.head_dim == 256 ? precise_prefill_kernel<256>(gate != nullptr) : nullptr)
+                       : s.head_dim == 256 ? prefill_kernel<256>(dtype, out_f32, rows)
                        : s.head_dim == 128 ? prefill_kernel<128>(dtype, out_f32, rows) : nullptr;
     require(kernel != nullptr, "unsupported head_dim for the prefill kernel");
     void *args[] = {&a};

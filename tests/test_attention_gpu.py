@@ -239,6 +239,50 @@ def test_fused_device_path_matches_oracle(gpu):
     assert_close(vc.float().cpu().numpy(), expected[2], 0)
 
 
+@pytest.mark.parametrize('batch,position', [(100, 300), (57, 1)])
+def test_fused_prefill_chunk_matches_oracle(gpu, batch, position):
+    """A prefill chunk through the fused entry (more than 8 tokens: prepare,
+    append, the precise prefill kernel and the gate) on the reference's
+    sine-wave fixture (tests/test_cuda.py:201-216), with that test's
+    tolerances: output 3e-4, appended K 2e-3, V exact."""
+    torch = gpu
+    c = kat.sine_wave_case(batch=batch, position=position)
+    expected = ref.fused_attention(c['key_cache'], c['value_cache'], c['q_gate'], c['key'], c['value'],
+                                   c['q_norm'], c['k_norm'], batch, position, c['epsilon'])
+    cache = A.PagedKV(4, 256, A.round_capacity(position + batch), torch.float16)
+    cache.pack(torch.from_numpy(c['key_cache']).cuda(), torch.from_numpy(c['value_cache']).cuda())
+    dev = [torch.from_numpy(f32(c[name])).cuda() for name in ('q_gate', 'key', 'value', 'q_norm', 'k_norm')]
+    assert A.fused_workspace_bytes(batch, position) == batch * 24 * 256 * 4   # q parts only
+    out = A.attention_fused(*dev, cache, position, c['epsilon'])
+    kc, vc = cache.unpack(0, position + batch)
+    torch.cuda.synchronize()
+    assert_close(out.cpu().numpy(), expected[0], 3e-4)
+    assert_close(kc.float().cpu().numpy(), expected[1], 2e-3)
+    assert_close(vc.float().cpu().numpy(), expected[2], 0)
+
+
+def test_fused_prefill_chunk_equals_eight_token_steps(gpu):
+    """One 64-token chunk (prefill kernel) against the same tokens in eight
+    8-token calls (split kernels), as the reference's grouped-vs-sequential
+    check (tests/test_cuda.py:222-235): outputs within 3e-5, caches bitwise."""
+    torch = gpu
+    position, batch = 200, 64
+    c = kat.sine_wave_case(batch=batch, position=position)
+    caches = []
+    for _ in range(2):
+        cache = A.PagedKV(4, 256, A.round_capacity(position + batch), torch.float16)
+        cache.pack(torch.from_numpy(c['key_cache']).cuda(), torch.from_numpy(c['value_cache']).cuda())
+        caches.append(cache)
+    dev = [torch.from_numpy(f32(c[name])).cuda() for name in ('q_gate', 'key', 'value', 'q_norm', 'k_norm')]
+    whole = A.attention_fused(*dev, caches[0], position, c['epsilon'])
+    steps = torch.cat([A.attention_fused(dev[0][t:t + 8], dev[1][t:t + 8], dev[2][t:t + 8], dev[3], dev[4],
+                                         caches[1], position + t, c['epsilon']) for t in range(0, batch, 8)])
+    torch.cuda.synchronize()
+    assert_close(whole.cpu().numpy(), steps.cpu().numpy(), 3e-5)
+    for a, b in zip(caches[0].unpack(0, position + batch), caches[1].unpack(0, position + batch)):
+        assert torch.equal(a.view(torch.int16), b.view(torch.int16))
+
+
 @pytest.mark.parametrize('T,position', [(1, 50000), (8, 2000)])
 def test_graph_replay_matches_eager(gpu, T, position):
     """The device entry points enqueue kernels only (no allocation, no

@@ -155,5 +155,12 @@ def test_device_entry_points_validate_before_touching_the_device(lib):
     assert lib.qv_error() == b'null KV cache'
     assert lib.qv_kv_copy(p, p, p, p, 4, 256, 64, 4096, -1, None) == -1
     assert b'non-negative' in lib.qv_error()
-    assert lib.qv_attention_fused(*([p] * 8), 9, 0, 128, 1e-6, p, ws, None) == -1
-    assert lib.qv_error() == b'batch must be between 1 and 8'
+    # The device fused entry also takes prefill chunks, up to 8192 tokens.
+    assert lib.qv_attention_fused(*([p] * 8), 8193, 0, 16384, 1e-6, p, ws, None) == -1
+    assert lib.qv_error() == b'batch must be between 1 and 8192'
+    assert lib.qv_attention_fused(*([p] * 8), 0, 0, 128, 1e-6, p, ws, None) == -1
+    assert lib.qv_error() == b'batch must be between 1 and 8192'
+    assert lib.qv_attention_fused(*([p] * 8), 100, 0, 64, 1e-6, p, ws, None) == -1
+    assert b'capacity' in lib.qv_error()
+    assert lib.qv_attention_fused(*([p] * 8), 100, 139200, 139264, 1e-6, p, ws, None) == -1
+    assert b'139264' in lib.qv_error()
