@@ -5,13 +5,15 @@
 // token runs: row t sees keys 0..position+t.
 //
 // One workgroup owns 192 query rows of one KV head (row = token * group +
-// query head within the group); each wave owns one 16-row tile (twelve
-// waves: three per SIMD) whose query fragments stay in registers.  The
-// workgroup walks the pages that its last row can see through two rings of
-// four LDS buffers, one for K pages and one for V pages (16 KiB each at
-// D=256), filled by direct global->LDS loads three pages ahead.  Since pages
-// are stored in MFMA operand order, every wave reads its A operands as
-// conflict-free 16-byte LDS fragments:
+// query head within the group): 128 from the end of the chunk and 64 from
+// its start, so that every workgroup has about the same number of (row, key)
+// pairs.  Each wave owns one 16-row tile (twelve waves: three per SIMD)
+// whose query fragments stay in registers.  The workgroup walks the pages
+// that its last row can see through two rings of four LDS buffers, one for
+// K pages and one for V pages (16 KiB each at D=256), filled by direct
+// global->LDS loads three pages ahead.  Since pages are stored in MFMA
+// operand order, every wave reads its A operands as conflict-free 16-byte
+// LDS fragments:
 //   S^T[key][row] = K[key][:] . Q[row][:]     (A = K tile from LDS, B = Q)
 //   O^T[dim][row] += V^T[dim][key] P^T[key][row]  (A = V^T from LDS, B = P^T,
 //                                                  straight from S^T's C layout)
@@ -28,8 +30,7 @@
 //
 // Scheduling: workgroup i serves KV head i % kv_heads (with 4 KV heads the
 // round-robin dispatch over the 8 XCDs keeps every head on the same two XCDs,
-// whose L2s then hold that head's pages for all of its workgroups), and row
-// tiles go heaviest (latest rows, most keys) first.
+// whose L2s then hold that head's pages for all of its workgroups).
 #include "combine.hpp"
 #include "kernels.hpp"
 #include "lds.hpp"
@@ -125,9 +126,13 @@ void attention_prefill(PrefillArgs a) {
     constexpr int KS = D / 32, DT = D / 16;
     constexpr int PAGE = 32 * D;                       // elements of one K (or V) page
     constexpr int PAGE_BYTES = PAGE * 2;
-    // Waves 0..kLoaders-1 copy the pages, H 1 KiB loads each per K (or V)
-    // page (the largest power of two of waves that divides a page's loads).
-    constexpr int kLoaders = kPWaves >= 8 ? 8 : kPWaves;
+    // Row pieces: the first L waves ("late" waves, two per SIMD of twelve,
+    // one per SIMD of eight) take LR rows from the end of the chunk, the
+    // others ER rows from its start (see below).  The late waves copy the
+    // pages, H 1 KiB loads each per K (or V) page.
+    constexpr int L = kPWaves == 12 ? 8 : kPWaves / 2;
+    constexpr int LR = 16 * L, ER = ROWS - LR;
+    constexpr int kLoaders = L;
     constexpr int H = PAGE_BYTES / 1024 / kLoaders;
     static_assert(H >= 1 && PAGE_BYTES / 1024 % kLoaders == 0, "loads divide over the loader waves");
     __shared__ __attribute__((aligned(16))) KV kring[4 * PAGE];
@@ -136,18 +141,29 @@ void attention_prefill(PrefillArgs a) {
     const int lane = threadIdx.x & 63, g = lane >> 4;
     const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);   // wave index (uniform)
     const int h = blockIdx.x % a.kv_heads;
-    const int tile = a.n_tiles - 1 - blockIdx.x / a.kv_heads;        // heaviest first
-    const int row0 = tile * ROWS + w * 16;
+    // Load balance: workgroup j of a KV head owns the late piece j, rows
+    // [R - LR(j+1), R - LR j), and the early piece j, rows [ER j, ER j + ER)
+    // below B = R - LR n_tiles (the late pieces cover [B, R)).  A late row
+    // sees more keys than an early one, and the pieces are paired so that
+    // every workgroup has about the same work: all waves run until the early
+    // piece's last page, then the late waves alone (at two thirds of the
+    // per-page cost) until the late piece's.  Rows outside [0, R) (and
+    // early rows from B on) are padding.
+    const int R = a.rows;
+    const int j = blockIdx.x / a.kv_heads;
+    const bool late = w < L;
+    const int row0 = late ? R - LR * (j + 1) + 16 * w : ER * j + 16 * (w - L);
+    const int row_end = late ? R : max(R - LR * a.n_tiles, 0);     // valid rows: [0, row_end)
 
     // Query fragments (B operand): k-step ks of lane l holds row row0 + l%16,
-    // dims 32*ks + 8*(l/16) .. +7.  Padded rows repeat the last row; their
+    // dims 32*ks + 8*(l/16) .. +7.  Padded rows load a valid row; their
     // results are not stored.  They are in registers before the first page
     // is requested (a workgroup runs for hundreds of pages, so this one round
     // trip is negligible, and the page loop never waits on them).
     V8 qf[KS], qlo[QSPLIT ? KS : 1];
     int limit;
     {
-        const int row = min(row0 + (lane & 15), a.rows - 1);
+        const int row = min(max(row0 + (lane & 15), 0), max(row_end, 1) - 1);
         const int t = row / a.group, gg = row - t * a.group;
         limit = a.position + t;
         const KV *src = static_cast<const KV *>(a.q) +
@@ -161,13 +177,16 @@ void attention_prefill(PrefillArgs a) {
         }
     }
     wait_vmcnt<0>();
-    // Keys this workgroup can see: 0 .. position + (token of its last row).
-    const int last_row = min(tile * ROWS + ROWS - 1, a.rows - 1);
-    const int n_keys = a.position + last_row / a.group + 1;
+    // Keys this workgroup can see: 0 .. position + (token of its last row,
+    // the late piece's last, which is valid).
+    const int n_keys = a.position + (R - LR * j - 1) / a.group + 1;
     const int n = (n_keys + 31) / 32;
+    // Pages of this wave: those its last valid row sees (none without one).
+    const int wave_last = min(row0 + 15, row_end - 1);
+    const int n_wave = wave_last >= max(row0, 0) ? (a.position + wave_last / a.group + 1 + 31) / 32 : 0;
     // Pages from which on some row of this wave masks keys (every row sees
     // the keys up to position + its first row's token).
-    const int wave_first_limit = a.position + min(row0, a.rows - 1) / a.group;
+    const int wave_first_limit = a.position + max(row0, 0) / a.group;
 
     const KV *kh = static_cast<const KV *>(a.k_pages) + (size_t)h * a.head_stride;
     const KV *vh = static_cast<const KV *>(a.v_pages) + (size_t)h * a.head_stride;
@@ -357,7 +376,8 @@ void attention_prefill(PrefillArgs a) {
     // Step i: K(i+1) and V(i) have landed (requests after K(i+1): V(i+1),
     // K(i+2), V(i+2), K(i+3), those that exist), the waves meet (so K(i)
     // and V(i-1) are consumed), V(i+3) and K(i+4) are requested into the
-    // buffers just freed, and the step runs.
+    // buffers just freed, and the step runs in the waves whose rows see page
+    // i.  Every wave takes part in every barrier.
     for (int i = 0; i < n; ++i) {
         const int ahead = n - 1 - i;
         if (ahead >= 3) wait_vmcnt<4 * H>();
@@ -367,13 +387,13 @@ void attention_prefill(PrefillArgs a) {
         ring_barrier();
         if (i + 3 < n) stage(vh, i + 3, vring);
         if (i + 4 < n) stage(kh, i + 4, kring);
-        step(i);
+        if (i < n_wave) step(i);
     }
 
     // ---- normalise and store rows ----
     l = row_group_sum(l);
     const int row = row0 + (lane & 15);
-    if (row < a.rows) {
+    if (row >= 0 && row < row_end) {
         const int t = row / a.group, gg = row - t * a.group;
         OUT *dst = static_cast<OUT *>(a.out) + ((size_t)t * a.q_heads + (size_t)h * a.group + gg) * D + 4 * g;
         const float inv = 1.f / l;
