@@ -690,6 +690,11 @@ SplitPlan plan_split(const Shape &s, int tokens, Dtype dtype, bool precise) {
     }();
     if (cap) per_head = std::min(per_head, cap);
     if (p.kind == SplitKind::Stream) {
+        // Decode streams fastest from three quarters of the CUs: on the
+        // 139,264-key decode (4 KV heads) 48 splits per head (192
+        // workgroups) take 95.5 us against 97.6 us for 64, and the combine
+        // has fewer partials to merge.
+        if (!cap) per_head = std::max(1, std::min(per_head, device_cu_count() * 3 / (4 * s.kv_heads)));
         // Every wave gets at least one page on average.
         p.splits = std::max(1, std::min(per_head, (p.n_pages + kWaves - 1) / kWaves));
     } else {
