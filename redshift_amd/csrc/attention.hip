@@ -607,7 +607,7 @@ const void *split_kernel(const SplitPlan &p, int D, Dtype dtype, bool precise) {
 }
 
 // Kernel of a plan: one query tile (decode) runs attention_stream, more run
-// attention_ring (16-bit queries) or attention_coop (fp32 queries).
+// attention_ring (16-bit queries, and fp32 ones as hi + lo parts).
 // RS_DECODE_KERNEL=coop|ring and RS_VERIFY_KERNEL=coop pick the alternatives
 // (for measurement).
 SplitKind env_kind(const char *name, SplitKind fallback) {
@@ -625,9 +625,9 @@ SplitKind kind_for(int nqt, bool precise) {
         return k == SplitKind::Stream ? SplitKind::Ring : k;
     }();
     const SplitKind k = nqt == 1 ? decode : verify;
-    // The ring kernel takes 16-bit queries only; fp32 (hi + lo) queries of
-    // several tiles use attention_coop.
-    return precise && k == SplitKind::Ring ? (nqt == 1 ? SplitKind::Stream : SplitKind::Coop) : k;
+    // One query tile of fp32 (hi + lo) queries streams; several use the
+    // ring kernel's precise instance (the fused model path, fp16, D=256).
+    return precise && k == SplitKind::Ring && nqt == 1 ? SplitKind::Stream : k;
 }
 
 }  // namespace

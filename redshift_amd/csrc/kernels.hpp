@@ -31,8 +31,8 @@ struct SplitArgs {
 };
 
 // attention_ring instance (ring.hip) for head_dim D and nqt query tiles
-// (1..4), or nullptr for fp32 (precise) queries.  It takes kRingThreads
-// threads and SplitArgs.
+// (1..4); precise (fp32 hi + lo) queries have an fp16, D=256 instance only
+// (nullptr otherwise).  It takes kRingThreads threads and SplitArgs.
 constexpr int kRingThreads = 512;
 const void *ring_kernel(int D, int nqt, Dtype dtype, bool precise);
 

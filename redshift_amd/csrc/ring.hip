@@ -18,7 +18,9 @@
 //                                             B = P^T straight from S^T's C
 //                                             layout)
 // The partials (m, l, unnormalised O) use the layout of the other split
-// kernels, so attention_combine merges them.
+// kernels, so attention_combine merges them.  A precise instance (QSPLIT)
+// takes an fp32 query as fp16 hi + lo parts (the fused path): S^T gets one
+// more MFMA per fragment and P is split into hi + lo parts as well.
 #include "kernels.hpp"
 #include "lds.hpp"
 
@@ -56,7 +58,7 @@ __device__ __forceinline__ f32x4 mfma(bf16x4 a, bf16x4 b, f32x4 c) {
 constexpr int kRingWaves = 8;
 constexpr float kLazy = 8.f;   // lazy row-max threshold, log2 units
 
-template <int D, int NQT, bool PSPLIT, typename KV>
+template <int D, int NQT, bool PSPLIT, typename KV, bool QSPLIT = false>
 __global__ __launch_bounds__(kRingWaves * kWave, 1)
 void attention_ring(SplitArgs a) {
     using V8 = typename Vec8<KV>::type;
@@ -101,22 +103,25 @@ void attention_ring(SplitArgs a) {
     // row and are never stored.  They travel through LDS (ring buffer 3, before
     // its first page), copied by the first wave of each tile: loaded into
     // registers from global memory they would make the compiler wait for every
-    // load in flight before the page loop.
+    // load in flight before the page loop.  The lo parts of a precise query
+    // travel through ring buffer 2, copied by the tile's second wave; page 2
+    // is then requested after the fragments have moved to registers.
     const int row = min(16 * qt + (lane & 15), a.rows - 1);
     const int t = row / a.group;
     const int limit = a.position + t;                            // last key of this row
     const int tile_limit = a.position + min(16 * qt, a.rows - 1) / a.group;
     static_assert(4 * KS * kWave * 8 <= 2 * PAGE, "query fragments fit one ring buffer");
-    if (computes && kt == 0) {
-        const KV *src = static_cast<const KV *>(a.q) +
+    if (computes && (kt == 0 || QSPLIT)) {
+        const KV *src = static_cast<const KV *>(kt == 0 ? a.q : a.q_lo) +
                         ((size_t)t * a.q_heads + (size_t)h * a.group + (row - t * a.group)) * D + 8 * g;
+        KV *dst = kt == 0 ? ring3 : ring2;
 #pragma unroll
         for (int ks = 0; ks < KS; ++ks)
             __builtin_amdgcn_global_load_lds(reinterpret_cast<const void *>(src + 32 * ks),
-                                             (__attribute__((address_space(3))) void *)(ring3 + (qt * KS + ks) * kWave * 8),
+                                             (__attribute__((address_space(3))) void *)(dst + (qt * KS + ks) * kWave * 8),
                                              16, 0, 0);
     }
-    V8 qf[KS];
+    V8 qf[KS], qlo[QSPLIT ? KS : 1];
 
     f32x4 acc[DT];
 #pragma unroll
@@ -131,13 +136,20 @@ void attention_ring(SplitArgs a) {
         static_for<0, KS>([&](auto ks) {
             lds_read<decltype(ks)::value * 1024>(kf[decltype(ks)::value], kbase);
         });
-        // Two accumulation chains (even and odd k-steps) halve the latency.
+        // Two accumulation chains (even and odd k-steps, or hi and lo query
+        // parts) halve the latency.
         f32x4 s0 = {0.f, 0.f, 0.f, 0.f}, s1 = {0.f, 0.f, 0.f, 0.f};
         static_for<0, KS>([&](auto ks_) {
             constexpr int ks = decltype(ks_)::value;
             lds_wait<KS - 1 - ks>(kf[ks]);
-            if constexpr (ks % 2 == 0) s0 = mfma(kf[ks], qf[ks], s0);
-            else s1 = mfma(kf[ks], qf[ks], s1);
+            if constexpr (QSPLIT) {
+                s0 = mfma(kf[ks], qf[ks], s0);
+                s1 = mfma(kf[ks], qlo[ks], s1);
+            } else if constexpr (ks % 2 == 0) {
+                s0 = mfma(kf[ks], qf[ks], s0);
+            } else {
+                s1 = mfma(kf[ks], qf[ks], s1);
+            }
         });
         // V^T fragments of the same 16 keys (half of each 32-key fragment):
         // the first half requested now, the second once it has landed (at
@@ -231,19 +243,33 @@ void attention_ring(SplitArgs a) {
     if (n > 0) {
         stage(p0, ring0);
         if (n > 1) stage(p0 + 1, ring1);
-        if (n > 2) stage(p0 + 2, ring2);
+        if (!QSPLIT && n > 2) stage(p0 + 2, ring2);
         // Step 0: page 0 and the query fragments (loaded first) have landed;
-        // the fragments move to registers before page 3 overwrites them.
-        wait_page(0);
+        // the fragments move to registers before pages 3 (and 2) overwrite
+        // them.
+        if (QSPLIT) {
+            if (n > 1) wait_vmcnt<CPW>();
+            else wait_vmcnt<0>();
+        } else {
+            wait_page(0);
+        }
         ring_barrier();
         if (computes) {
             const uint32_t qbase = lds_addr(ring3) + qt * KS * 1024 + lane * 16;
             static_for<0, KS>([&](auto ks) {
                 lds_read<decltype(ks)::value * 1024>(qf[decltype(ks)::value], qbase);
             });
+            if constexpr (QSPLIT) {
+                const uint32_t lbase = lds_addr(ring2) + qt * KS * 1024 + lane * 16;
+                static_for<0, KS>([&](auto ks) {
+                    lds_read<decltype(ks)::value * 1024>(qlo[decltype(ks)::value], lbase);
+                });
+                static_for<0, KS>([&](auto ks) { lds_wait<0>(qlo[decltype(ks)::value]); });
+            }
             static_for<0, KS>([&](auto ks) { lds_wait<0>(qf[decltype(ks)::value]); });
         }
         ring_barrier();
+        if (QSPLIT && 2 < n) stage(p0 + 2, ring2);
         if (3 < n) stage(p0 + 3, ring3);
         if (computes) compute(p0, ring0);
         for (int i = 1; i < n; i += 4) {
@@ -312,8 +338,20 @@ const void *pick_tiles(int nqt, Dtype dtype) {
 
 }  // namespace
 
+// fp32 queries (hi + lo fp16 parts): hi + lo P as well.
+template <int D>
+const void *pick_precise(int nqt) {
+    switch (nqt) {
+        case 1: return (const void *)&attention_ring<D, 1, true, _Float16, true>;
+        case 2: return (const void *)&attention_ring<D, 2, true, _Float16, true>;
+        case 3: return (const void *)&attention_ring<D, 3, true, _Float16, true>;
+        case 4: return (const void *)&attention_ring<D, 4, true, _Float16, true>;
+    }
+    return nullptr;
+}
+
 const void *ring_kernel(int D, int nqt, Dtype dtype, bool precise) {
-    if (precise) return nullptr;   // fp32 queries (hi + lo parts) use attention_coop
+    if (precise) return dtype == Dtype::F16 && D == 256 ? pick_precise<256>(nqt) : nullptr;
     if (D == 256) return pick_tiles<256>(nqt, dtype);
     if (D == 128) return pick_tiles<128>(nqt, dtype);
     return nullptr;

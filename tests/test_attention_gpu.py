@@ -239,6 +239,23 @@ def test_fused_device_path_matches_oracle(gpu):
     assert_close(vc.float().cpu().numpy(), expected[2], 0)
 
 
+@pytest.mark.parametrize('batch,position', [(5, 5000), (8, 20000), (3, 40)])
+def test_fused_verify_matches_oracle(gpu, batch, position):
+    """Fused verify batches of 3-8 tokens (the ring kernel's precise
+    instance: fp32 query as hi + lo parts) at split lengths of 1 to ~11
+    pages, on the reference's sine-wave fixture and tolerances."""
+    torch = gpu
+    c = kat.sine_wave_case(batch=batch, position=position)
+    expected = ref.fused_attention(c['key_cache'], c['value_cache'], c['q_gate'], c['key'], c['value'],
+                                   c['q_norm'], c['k_norm'], batch, position, c['epsilon'])
+    cache = A.PagedKV(4, 256, A.round_capacity(position + batch), torch.float16)
+    cache.pack(torch.from_numpy(c['key_cache']).cuda(), torch.from_numpy(c['value_cache']).cuda())
+    dev = [torch.from_numpy(f32(c[name])).cuda() for name in ('q_gate', 'key', 'value', 'q_norm', 'k_norm')]
+    out = A.attention_fused(*dev, cache, position, c['epsilon'])
+    torch.cuda.synchronize()
+    assert_close(out.cpu().numpy(), expected[0], 3e-4)
+
+
 @pytest.mark.parametrize('batch,position', [(100, 300), (57, 1)])
 def test_fused_prefill_chunk_matches_oracle(gpu, batch, position):
     """A prefill chunk through the fused entry (more than 8 tokens: prepare,
