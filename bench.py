@@ -8,7 +8,9 @@ pages, then the log-sum-exp combine.  `value` is the achieved HBM bandwidth
 over the algorithmic K+V bytes (each key read once) of the whole step
 replayed as a HIP graph; `roofline` is the split-K kernel alone, timed with
 HIP events on the stream it runs on.  Secondary workloads (speculative
-verify-8 on a 16K prefix, decode at 4K, chunked prefill) are under `extra`.
+verify-8 on a 16K prefix, decode at 4K, chunked prefill, and the device
+drop-in of the reference's fused k_attention at verify-8/16K and decode/139K)
+are under `extra`.
 
 The CPU baseline is the numpy fp32 restatement of the reference's CPU
 attention (oracle/attention_ref.py), run on this host on one layer's decode.
@@ -184,6 +186,52 @@ def drop_in_rate(lib, cases=((1, 139263), (8, 16384), (1, 4095)), repeats=5):
     return rows
 
 
+def time_fused(torch, A, w, layers, steps, warmup, seed):
+    """Times the device drop-in of the reference's k_attention
+    (qv_attention_fused: prepare + append + attention + gate, fp32 q_gate /
+    key / value of the 24/4/256 model) on `layers` caches of workload `w`,
+    one call per layer, replayed as a HIP graph.  Returns ms per step."""
+    caches, _ = make_layers(torch, A, w, layers, seed)
+    gen = torch.Generator(device='cuda')
+    gen.manual_seed(seed + 1)
+    batch = w.tokens
+    q_gate = [torch.randn((batch, 24, 512), generator=gen, device='cuda') for _ in range(layers)]
+    key = [torch.randn((batch, 4, 256), generator=gen, device='cuda') for _ in range(layers)]
+    value = [torch.randn((batch, 4, 256), generator=gen, device='cuda') for _ in range(layers)]
+    norm = torch.ones(256, device='cuda')
+    out = torch.empty((batch, 24, 256), device='cuda')
+    ws = A.workspace(A.fused_workspace_bytes(batch, w.position))
+
+    def step():
+        for i in range(layers):
+            A.attention_fused(q_gate[i], key[i], value[i], norm, norm, caches[i], w.position, 1e-6,
+                              out=out, ws=ws)
+
+    for _ in range(warmup):
+        step()
+    graph = torch.cuda.CUDAGraph()
+    capture_stream = torch.cuda.Stream()
+    capture_stream.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(capture_stream):
+        step()
+        torch.cuda.synchronize()
+        with torch.cuda.graph(graph, stream=capture_stream):
+            step()
+    torch.cuda.current_stream().wait_stream(capture_stream)
+    for _ in range(warmup):
+        graph.replay()
+    torch.cuda.synchronize()
+    start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    start.record()
+    for _ in range(steps):
+        graph.replay()
+    end.record()
+    torch.cuda.synchronize()
+    del graph, caches
+    torch.cuda.empty_cache()
+    return start.elapsed_time(end) / steps
+
+
 def cpu_baseline(w, target_s=8.0):
     """The numpy fp32 restatement of the reference's CPU attention (oracle),
     one layer's decode, timed single-threaded and on all host cores (capped
@@ -239,7 +287,7 @@ def main():
     ap.add_argument('--layers', type=int, default=LAYERS)
     ap.add_argument('--no-cpu', action='store_true', help='skip the CPU baseline')
     ap.add_argument('--no-extra', action='store_true', help='skip the secondary workloads')
-    ap.add_argument('--extras', default='verify8_16k,decode_4k,prefill_2k',
+    ap.add_argument('--extras', default='verify8_16k,decode_4k,prefill_2k,fused_verify8_16k,fused_decode_139k',
                     help='comma-separated secondary workloads to run')
     ap.add_argument('--drop-in', action='store_true',
                     help='only time the host-buffer qv_test_attention (PCIe-inclusive) and exit')
@@ -317,6 +365,16 @@ def main():
                                    'TFLOP/s': round(wp.flops() / kernel_s / 1e12, 1),
                                    'frac_mfma_peak': round(wp.flops() / kernel_s / MFMA_BF16_PEAK, 4),
                                    'flops_per_layer': wp.flops()}
+        for name in ('fused_verify8_16k', 'fused_decode_139k'):
+            if name not in chosen:
+                continue
+            wf = WORKLOADS[name[len('fused_'):]]
+            log(f'{name}: {args.layers} layers')
+            us = 1000 * time_fused(torch, A, wf, args.layers, args.steps, args.warmup, seed=4) / args.layers
+            extra[name] = {'us_per_layer': round(us, 2),
+                           'GB/s': round(wf.kv_bytes() / (us * 1e-6) / 1e9, 1),
+                           'frac_hbm': round(wf.kv_bytes() / (us * 1e-6) / 1e9 / HBM_PEAK_GBS, 4),
+                           'what': 'qv_attention_fused per layer: prepare + append + attention + gate'}
         result['extra'] = extra
     if not args.no_cpu:
         log('cpu baseline (numpy fp32, 1 thread, one layer)')
