@@ -138,6 +138,22 @@ void run_attention(const rs::Shape &s, rs::Dtype dtype, bool precise, float scal
     }
 }
 
+// The reference's k_attention on device buffers of the 24/4/256 model:
+// the prepare kernel writes the query's hi + lo parts to q_hilo (2 * batch *
+// 24 * 256 fp16) and appends the new K/V to the pages, then attention (with
+// the sigmoid gate) runs on them.
+void fused_attention(float *out, void *k_pages, void *v_pages, const float *q_gate, const float *key,
+                     const float *value, const float *q_norm, const float *k_norm, int batch,
+                     int position, int capacity, float epsilon, uint16_t *q_hilo, void *partials,
+                     hipStream_t stream) {
+    constexpr int H = rs::kModelQHeads, HKV = rs::kModelKvHeads, D = rs::kModelHeadDim;
+    const rs::Shape s{H, HKV, D, batch, position, capacity};
+    rs::launch_prepare(q_hilo, k_pages, v_pages, q_gate, key, value, q_norm, k_norm, batch, position,
+                       capacity, epsilon, stream);
+    run_attention(s, rs::Dtype::F16, true, 1.0f / 16.0f, q_hilo, q_hilo + (size_t)batch * H * D, k_pages,
+                  v_pages, partials, out, true, q_gate, stream);
+}
+
 [[noreturn]] void not_in_library(const char *name) {
     char message[200];
     std::snprintf(message, sizeof(message),
@@ -201,13 +217,9 @@ extern "C" int qv_test_attention(float *out, void *key_cache, void *value_cache,
         upload(kn.data(), k_norm, D * sizeof(float));
         rs::launch_pack(k_pages.data(), v_pages.data(), k_rows.data(), v_rows.data(), HKV, D,
                         capacity, 0, position, stream);
-        rs::launch_prepare(q.data(), k_pages.data(), v_pages.data(), qg.floats(), k.floats(),
-                           v.floats(), qn.floats(), kn.floats(), batch, position, capacity,
-                           epsilon, stream);
-        run_attention(shape, rs::Dtype::F16, true, 1.0f / 16.0f, q.data(),
-                      static_cast<uint16_t *>(q.data()) + (size_t)batch * H * D,
-                      k_pages.data(), v_pages.data(), workspace.data(), output.data(),
-                      true, qg.floats(), stream);
+        fused_attention(output.floats(), k_pages.data(), v_pages.data(), qg.floats(), k.floats(),
+                        v.floats(), qn.floats(), kn.floats(), batch, position, capacity, epsilon,
+                        static_cast<uint16_t *>(q.data()), workspace.data(), stream);
         rs::launch_unpack(k_rows.data(), v_rows.data(), k_pages.data(), v_pages.data(), HKV, D,
                           capacity, 0, n, stream);
         check(hipGetLastError());
@@ -420,9 +432,7 @@ extern "C" int qv_attention_fused(float *out, void *k_pages, void *v_pages,
         hipStream_t st = static_cast<hipStream_t>(stream);
         uint16_t *q = static_cast<uint16_t *>(workspace);   // hi then lo fp16 parts
         void *partials = static_cast<char *>(workspace) + align256((size_t)batch * H * D * sizeof(float));
-        rs::launch_prepare(q, k_pages, v_pages, q_gate, key, value, q_norm, k_norm, batch, position,
-                           capacity, epsilon, st);
-        run_attention(s, rs::Dtype::F16, true, 1.0f / 16.0f, q, q + (size_t)batch * H * D, k_pages,
-                      v_pages, partials, out, true, q_gate, st);
+        fused_attention(out, k_pages, v_pages, q_gate, key, value, q_norm, k_norm, batch, position,
+                        capacity, epsilon, q, partials, st);
     });
 }

@@ -1,6 +1,7 @@
 // KV page maintenance: token-major <-> page conversion, and the fused prepare
 // step (RMSNorm + RoPE of q and k, fp16 append of k and v into the pages).
 #include "kernels.hpp"
+#include "prep.hpp"
 
 #include <cmath>
 
@@ -50,72 +51,44 @@ void convert(void *k_pages, void *v_pages, const void *k_rows, const void *v_row
     }
 }
 
-// RoPE frequencies 1e7^(-i/32), i = 0..31 (base 1e7 over 64 rotary dims,
-// qvelox/model.py:13), as doubles.
-__constant__ double kRopeFreq[32] = {
-    0x1.0000000000000p+0, 0x1.3566562253c7ep-1, 0x1.75f034d79e965p-2, 0x1.c3f06b4e265cep-3,
-    0x1.111aedafb9a9dp-3, 0x1.4a12ad8379eb8p-4, 0x1.8eec7def5d56cp-5, 0x1.e222ec75094e2p-6,
-    0x1.235a71c5ee5ccp-6, 0x1.6020a364b1284p-7, 0x1.a99428b3d26b3p-8, 0x1.012cfaad0da13p-8,
-    0x1.36d219065ac0cp-9, 0x1.77a7d87ee61b0p-10, 0x1.c603c39630446p-11, 0x1.125c04ab2d71fp-11,
-    0x1.4b96be9c2da2cp-12, 0x1.90c181b38fe22p-13, 0x1.e459c57e28a47p-14, 0x1.24b0fd0e890d4p-14,
-    0x1.61bea2721385fp-15, 0x1.ab88830de4ad5p-16, 0x1.025b57369650bp-16, 0x1.383f8796f72a9p-17,
-    0x1.7961810874a9fp-18, 0x1.c8198c91f9fccp-19, 0x1.139e9527f964ep-19, 0x1.4d1c97f4e952fp-20,
-    0x1.9298ace36f12ep-21, 0x1.e69338f8adcd3p-22, 0x1.26091b11c8665p-22, 0x1.635e883bbc816p-23,
-};
-
-// One workgroup per (head, token): heads 0..23 are query heads, 24..27 the KV
-// heads (the reference's attn_prepare grid, src/kernels.cu:416-434).
-// RMSNorm over 256 dims with gamma, then rotate pairs (i, i+32), i < 32, by
-// (position+t) * 1e7^(-i/32).  The angle is evaluated and reduced to
-// [-pi, pi] in double precision (the reference rounds the angle to fp32,
-// which at position 139,263 is off by up to 2^-7 rad); its sine and cosine
-// and the rotation are fp32.  Every global load is issued first and the
-// angle computed while they are in flight; the pairs (i, i+32) sit in wave
-// 0, which swaps them with a lane shuffle, so one barrier (the norm's
-// cross-wave sum) remains.
-__global__ __launch_bounds__(256)
+// One wave per (head, token): heads 0..23 are query heads, 24..27 the KV
+// heads (the reference's attn_prepare grid, src/kernels.cu:416-434), lane l
+// owning dims l, 64+l, 128+l, 192+l.  Every global load is issued first and
+// the RoPE angle computed while they are in flight.
+__global__ __launch_bounds__(kWave)
 void prepare_kernel(_Float16 *q_hilo, _Float16 *k_pages, _Float16 *v_pages, const float *q_gate,
                     const float *key, const float *value, const float *q_norm,
                     const float *k_norm, int position, size_t head_stride, float epsilon) {
     constexpr int D = kModelHeadDim, H = kModelQHeads, HKV = kModelKvHeads;
-    static_assert(D == 4 * kWave, "four waves of one dim each");
-    const int h = blockIdx.x, t = blockIdx.y, i = threadIdx.x;
+    static_assert(D == 4 * kWave, "four dims per lane");
+    const int h = blockIdx.x, t = blockIdx.y, lane = threadIdx.x;
     const bool is_q = h < H;
     const int kh = h - H;
     const float *src = is_q ? q_gate + ((size_t)t * H + h) * 2 * D : key + ((size_t)t * HKV + kh) * D;
-    const float x = src[i];
-    const float gamma = (is_q ? q_norm : k_norm)[i];
-    const float v = is_q ? 0.f : value[((size_t)t * HKV + kh) * D + i];
-    float c = 1.f, sn = 0.f;
-    if (i < 32) {
-        constexpr double kTwoPi = 6.283185307179586476925286766559;
-        const double theta = (double)(position + t) * kRopeFreq[i];
-        const double r = theta - kTwoPi * rint(theta * (1.0 / kTwoPi));
-        sincosf((float)r, &sn, &c);
-    }
-    __shared__ float red[D / kWave];
-    const float ss = wave_sum(x * x);
-    if ((i & (kWave - 1)) == 0) red[i / kWave] = ss;
-    __syncthreads();
-    float total = 0.f;
+    const float *gamma_src = is_q ? q_norm : k_norm;
+    float x[1][4], gamma[4], v[4];
 #pragma unroll
-    for (int w = 0; w < D / kWave; ++w) total += red[w];
-    const float inv = rsqrtf(total / D + epsilon);
-    float y = x * inv * gamma;
-    // Lane i < 32 of wave 0 holds a = y_i, lane i + 32 holds b = y_{i+32}.
-    const float other = __shfl_xor(y, 32, kWave);
-    if (i < 32) y = y * c - other * sn;                      // a c - b s
-    const float cs = __shfl_xor(c, 32, kWave), ss2 = __shfl_xor(sn, 32, kWave);
-    if (i >= 32 && i < 64) y = other * ss2 + y * cs;         // a s + b c
-    if (is_q) {
-        const size_t idx = ((size_t)t * H + h) * D + i;
-        const _Float16 hi = (_Float16)y;
-        q_hilo[idx] = hi;
-        q_hilo[(size_t)gridDim.y * H * D + idx] = (_Float16)(y - (float)hi);
-    } else {
-        const int token = position + t;
-        k_pages[(size_t)kh * head_stride + k_page_offset(token, i, D)] = (_Float16)y;
-        v_pages[(size_t)kh * head_stride + v_page_offset(token, i, D)] = (_Float16)v;
+    for (int w = 0; w < 4; ++w) {
+        x[0][w] = src[64 * w + lane];
+        gamma[w] = gamma_src[64 * w + lane];
+        v[w] = is_q ? 0.f : value[((size_t)t * HKV + kh) * D + 64 * w + lane];
+    }
+    float c[1] = {1.f}, s[1] = {0.f};
+    if (lane < 32) rope_cos_sin(position + t, rope_freq(lane), c[0], s[0]);
+    norm_rope_rows(x, gamma, c, s, epsilon, lane);
+#pragma unroll
+    for (int w = 0; w < 4; ++w) {
+        const int d = 64 * w + lane;
+        if (is_q) {
+            const size_t idx = ((size_t)t * H + h) * D + d;
+            const _Float16 hi = (_Float16)x[0][w];
+            q_hilo[idx] = hi;
+            q_hilo[(size_t)gridDim.y * H * D + idx] = (_Float16)(x[0][w] - (float)hi);
+        } else {
+            const int token = position + t;
+            k_pages[(size_t)kh * head_stride + k_page_offset(token, d, D)] = (_Float16)x[0][w];
+            v_pages[(size_t)kh * head_stride + v_page_offset(token, d, D)] = (_Float16)v[w];
+        }
     }
 }
 
@@ -169,7 +142,7 @@ void launch_prepare(void *q_hilo, void *k_pages, void *v_pages, const float *q_g
                     const float *k_norm, int batch, int position, int capacity,
                     float epsilon, hipStream_t stream) {
     hipLaunchKernelGGL(prepare_kernel, dim3(kModelQHeads + kModelKvHeads, batch),
-                       dim3(kModelHeadDim), 0, stream, static_cast<_Float16 *>(q_hilo),
+                       dim3(kWave), 0, stream, static_cast<_Float16 *>(q_hilo),
                        static_cast<_Float16 *>(k_pages),
                        static_cast<_Float16 *>(v_pages), q_gate, key, value, q_norm, k_norm,
                        position, (size_t)capacity * kModelHeadDim, epsilon);

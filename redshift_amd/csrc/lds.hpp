@@ -59,6 +59,18 @@ __device__ __forceinline__ void lds_wait(V &a, V &b) {
     asm volatile("s_waitcnt lgkmcnt(%2)" : "+v"(a), "+v"(b) : "i"(N));
 }
 
+// Values v are computed (or loaded) before this point: an empty statement,
+// ordered with the explicit LDS and memory waits around it, that takes them
+// as operands, so their uses are not moved above it.
+template <typename T>
+__device__ __forceinline__ void pin1(T &v) {
+    asm volatile("" : "+v"(v));
+}
+template <typename... T>
+__device__ __forceinline__ void pin(T &...v) {
+    (pin1(v), ...);
+}
+
 // Marks a rarely taken branch body as having side effects, so the compiler
 // keeps the branch instead of executing the body on every page as selects.
 __device__ __forceinline__ void keep_branch() { asm volatile(""); }

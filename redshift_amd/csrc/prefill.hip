@@ -54,18 +54,6 @@ __device__ __forceinline__ f32x4 mfma(bf16x8 a, bf16x8 b, f32x4 c) {
     return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, 0, 0, 0);
 }
 
-// The softmax values of a pipeline chunk are computed before this point: an
-// empty statement, ordered with the LDS reads and waits around it, that
-// takes them as operands (so they are not moved towards their later uses).
-template <typename T>
-__device__ __forceinline__ void pin1(T &v) {
-    asm volatile("" : "+v"(v));
-}
-template <typename... T>
-__device__ __forceinline__ void pin(T &...v) {
-    (pin1(v), ...);
-}
-
 __device__ __forceinline__ float max3(float a, float b, float c) {
     return __builtin_fmaxf(__builtin_fmaxf(a, b), c);
 }
