@@ -16,8 +16,9 @@ enum { kOutSame = 0, kOutF32 = 1, kOutGated = 2 };
 // barriers).  Lane l owns head dims DV*l .. DV*l+DV-1 (DV = D/64);
 // wave w4 takes splits w4, w4+4, ... and issues the loads of up to kBatch of
 // them (their m, l and partial row) at once, so a combine over up to
-// 4*kBatch splits costs one memory round trip.  The waves then agree on the
-// row max and reduce through `scratch` (4*(D+1) + 4 floats of LDS per group).
+// 4*kBatch splits costs one memory round trip (non-temporal: each partial
+// row is read once).  The waves then agree on the row max and reduce through
+// `scratch` (4*(D+1) + 4 floats of LDS per group).
 template <int D, typename KV>
 __device__ __forceinline__ void combine_row(const float *part_o, const float *part_ml, int splits,
                                             int rows, int group, int q_heads, int row, int h,
@@ -46,7 +47,7 @@ __device__ __forceinline__ void combine_row(const float *part_o, const float *pa
             const int sc = min(s0 + w4 + 4 * i, splits - 1);
             mv[i] = ml[(size_t)sc * 2 * rows];
             lv[i] = ml[(size_t)sc * 2 * rows + rows];
-            ov[i] = *reinterpret_cast<const OV *>(po + (size_t)sc * stride);
+            ov[i] = __builtin_nontemporal_load(reinterpret_cast<const OV *>(po + (size_t)sc * stride));
         }
 #pragma unroll
         for (int i = 0; i < kBatch; ++i) {
