@@ -547,19 +547,21 @@ void attention_coop(SplitArgs a) {
 }
 
 struct CombineArgs {
-    const float *part_o, *part_ml;
+    const void *part_o;   // float or _Float16 rows (SplitPlan::half_parts)
+    const float *part_ml;
     void *out;
     const float *gate;   // gated output: q_gate rows of 2*D floats, gate at +D
     int q_heads, group, rows, splits;
 };
 
 // Standalone combine: one workgroup (4 waves) per (row, KV head).
-template <int D, typename KV, int OUT>
+template <int D, typename KV, int OUT, typename PT>
 __global__ __launch_bounds__(kWaves * kWave)
 void attention_combine(CombineArgs c) {
     __shared__ float scratch[4 * (D + 1) + 4];
-    combine_row<D, KV>(c.part_o, c.part_ml, c.splits, c.rows, c.group, c.q_heads, blockIdx.x, blockIdx.y,
-                       true, threadIdx.x >> 6, threadIdx.x & 63, scratch, c.out, c.gate, OUT);
+    combine_row<D, KV, PT>(static_cast<const PT *>(c.part_o), c.part_ml, c.splits, c.rows, c.group, c.q_heads,
+                           blockIdx.x, blockIdx.y, true, threadIdx.x >> 6, threadIdx.x & 63, scratch, c.out,
+                           c.gate, OUT);
 }
 
 // Kernel instance for a plan.  Raw fp16: 16-bit P; raw bf16: hi+lo P (bf16's
@@ -577,12 +579,18 @@ const void *pick(bool stream, Dtype dtype, bool precise) {
     return (const void *)&attention_coop<D, NQT, false, false, _Float16, kCoopWaves>;
 }
 
-template <int D>
+template <int D, typename PT>
 const void *combine_kernel(Dtype dtype, bool out_f32, bool gated) {
-    if (gated) return (const void *)&attention_combine<D, _Float16, kOutGated>;
-    if (out_f32) return (const void *)&attention_combine<D, _Float16, kOutF32>;
-    return dtype == Dtype::BF16 ? (const void *)&attention_combine<D, __bf16, kOutSame>
-                                : (const void *)&attention_combine<D, _Float16, kOutSame>;
+    if (gated) return (const void *)&attention_combine<D, _Float16, kOutGated, PT>;
+    if (out_f32) return (const void *)&attention_combine<D, _Float16, kOutF32, PT>;
+    return dtype == Dtype::BF16 ? (const void *)&attention_combine<D, __bf16, kOutSame, PT>
+                                : (const void *)&attention_combine<D, _Float16, kOutSame, PT>;
+}
+
+template <int D>
+const void *combine_kernel(Dtype dtype, bool out_f32, bool gated, bool half_parts) {
+    return half_parts ? combine_kernel<D, _Float16>(dtype, out_f32, gated)
+                      : combine_kernel<D, float>(dtype, out_f32, gated);
 }
 
 const void *split_kernel(const SplitPlan &p, int D, Dtype dtype, bool precise) {
@@ -681,6 +689,7 @@ SplitPlan plan_split(const Shape &s, int tokens, Dtype dtype, bool precise) {
     const long long n_keys = (long long)s.position + tokens;
     p.n_pages = (int)((n_keys + kPageTokens - 1) / kPageTokens);
     p.splits = 1;
+    p.half_parts = false;
     // Fill every CU with as many workgroups as stay resident.
     const int resident = device_cu_count() *
                          blocks_per_cu(split_kernel(p, s.head_dim, dtype, precise), block_threads(p));
@@ -705,6 +714,9 @@ SplitPlan plan_split(const Shape &s, int tokens, Dtype dtype, bool precise) {
         const int longest = (p.n_pages + per_head - 1) / per_head;
         p.splits = (p.n_pages + longest - 1) / longest;
     }
+    // The raw fp16 ring kernel stores its partial rows as fp16 O / l: half
+    // the partial traffic, which every workgroup writes at once at the end.
+    p.half_parts = p.kind == SplitKind::Ring && dtype == Dtype::F16 && !precise;
     return p;
 }
 
@@ -755,8 +767,8 @@ void launch_combine(const Shape &s, const SplitPlan &plan, Dtype dtype,
                     const void *workspace, void *out, bool out_f32, const float *gate,
                     hipStream_t stream) {
     CombineArgs c;
-    c.part_o = static_cast<const float *>(workspace);
-    c.part_ml = c.part_o + (size_t)s.kv_heads * plan.splits * plan.rows * s.head_dim;
+    c.part_o = workspace;
+    c.part_ml = static_cast<const float *>(workspace) + (size_t)s.kv_heads * plan.splits * plan.rows * s.head_dim;
     c.out = out;
     c.gate = gate;
     c.q_heads = s.q_heads;
@@ -764,8 +776,8 @@ void launch_combine(const Shape &s, const SplitPlan &plan, Dtype dtype,
     c.rows = plan.rows;
     c.splits = plan.splits;
     const dim3 grid(plan.rows, s.kv_heads);
-    const void *kernel = s.head_dim == 256 ? combine_kernel<256>(dtype, out_f32, gate != nullptr)
-                       : s.head_dim == 128 ? combine_kernel<128>(dtype, out_f32, gate != nullptr)
+    const void *kernel = s.head_dim == 256 ? combine_kernel<256>(dtype, out_f32, gate != nullptr, plan.half_parts)
+                       : s.head_dim == 128 ? combine_kernel<128>(dtype, out_f32, gate != nullptr, plan.half_parts)
                                            : nullptr;
     require(kernel != nullptr, "unsupported head_dim for the combine kernel");
     void *args[] = {&c};

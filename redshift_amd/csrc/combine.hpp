@@ -4,6 +4,7 @@
 #include "kernels.hpp"
 
 #include <cmath>
+#include <type_traits>
 
 namespace rs {
 
@@ -18,9 +19,11 @@ enum { kOutSame = 0, kOutF32 = 1, kOutGated = 2 };
 // them (their m, l and partial row) at once, so a combine over up to
 // 4*kBatch splits costs one memory round trip (non-temporal: each partial
 // row is read once).  The waves then agree on the row max and reduce through
-// `scratch` (4*(D+1) + 4 floats of LDS per group).
-template <int D, typename KV>
-__device__ __forceinline__ void combine_row(const float *part_o, const float *part_ml, int splits,
+// `scratch` (4*(D+1) + 4 floats of LDS per group).  PT is the type of the
+// partial rows: float (unnormalised O) or _Float16 (O / l, weighted by l
+// here).
+template <int D, typename KV, typename PT>
+__device__ __forceinline__ void combine_row(const PT *part_o, const float *part_ml, int splits,
                                             int rows, int group, int q_heads, int row, int h,
                                             bool valid, int w4, int lane, float *scratch,
                                             void *out, const float *gate, int out_mode) {
@@ -30,7 +33,8 @@ __device__ __forceinline__ void combine_row(const float *part_o, const float *pa
     float *wmax = scratch + 4 * (D + 1);     // [4]
     const int rc = valid ? row : rows - 1;   // in-bounds reads for a padding group
     const float *ml = part_ml + (size_t)h * splits * 2 * rows + rc;
-    const float *po = part_o + ((size_t)h * splits * rows + rc) * D + lane * DV;
+    const PT *po = part_o + ((size_t)h * splits * rows + rc) * D + lane * DV;
+    constexpr bool kNormalised = !std::is_same<PT, float>::value;
     const size_t stride = (size_t)rows * D;
 
     float M = -INFINITY, L = 0.f, acc[DV] = {};
@@ -39,7 +43,7 @@ __device__ __forceinline__ void combine_row(const float *part_o, const float *pa
         // Every load is issued unconditionally (splits past the end re-read
         // the last one) so that all of them are in flight together; the
         // surplus ones are discarded afterwards.
-        typedef float OV __attribute__((ext_vector_type(DV)));
+        typedef PT OV __attribute__((ext_vector_type(DV)));
         float mv[kBatch], lv[kBatch];
         OV ov[kBatch];
 #pragma unroll
@@ -70,8 +74,9 @@ __device__ __forceinline__ void combine_row(const float *part_o, const float *pa
         for (int i = 0; i < kBatch; ++i) {
             const float wgt = __builtin_amdgcn_exp2f(mv[i] - mu);
             L += wgt * lv[i];
+            const float wo = kNormalised ? wgt * lv[i] : wgt;
 #pragma unroll
-            for (int d = 0; d < DV; ++d) acc[d] += wgt * ov[i][d];
+            for (int d = 0; d < DV; ++d) acc[d] += wo * (float)ov[i][d];
         }
         M = rm;
     }

@@ -43,6 +43,7 @@ struct SplitPlan {
     int rows;        // valid query rows per KV head
     int n_pages;     // 32-key pages per KV head holding keys 0..n_keys-1
     int splits;      // workgroups per KV head
+    bool half_parts; // partial rows stored as fp16 O / l (the raw fp16 ring kernel)
 };
 
 // Largest number of query rows (group * tokens) per KV head that one launch of
@@ -59,8 +60,9 @@ size_t attention_workspace_bytes(const Shape &s, Dtype dtype, bool precise);
 // Split-K partial kernel over the pages of every KV head.  q is 16-bit of
 // `dtype`, [tokens][q_heads][D]; when `precise` (fp16 only) q and q_lo are
 // the hi and lo parts of an fp32 query.
-// Partial buffers of one plan: o [kv_heads][splits][rows][D], then m and l
-// [kv_heads][splits][2][rows], all float32.
+// Partial buffers of one plan: o [kv_heads][splits][rows][D] float32
+// (unnormalised), or fp16 O / l in the first half of that region when
+// plan.half_parts, then m and l [kv_heads][splits][2][rows] float32.
 size_t plan_bytes(const Shape &s, const SplitPlan &p);
 void launch_split(const Shape &s, const SplitPlan &plan, Dtype dtype, bool precise,
                   float scale, const void *q, const void *q_lo, const void *k_pages,

@@ -56,6 +56,7 @@ __device__ __forceinline__ f32x4 mfma(bf16x4 a, bf16x4 b, f32x4 c) {
 }
 
 constexpr int kRingWaves = 8;
+constexpr int kRingBuffers = 4;   // NBUF-1 pages in flight while one is consumed
 // Cache policy of the page loads: non-temporal (each page is read once).
 // The partials are stored and read back non-temporally as well: split +
 // combine at verify-8 on a 16K prefix take 21.0-21.3 us that way, against
@@ -71,15 +72,17 @@ void attention_ring(SplitArgs a) {
     using V4 = typename Vec4<KV>::type;
     constexpr int KS = D / 32, DT = D / 16;
     constexpr int PAGE = 32 * D;                   // elements of one K (or V) page
+    // Raw fp16: partial rows stored as fp16 O / l (SplitPlan::half_parts).
+    constexpr bool HALF = !QSPLIT && std::is_same<KV, _Float16>::value;
     constexpr int CHUNKS = 2 * PAGE * 2 / 1024;    // 1 KiB chunks of [K | V]
     constexpr int CPW = CHUNKS / kRingWaves;       // chunks (loads) per wave per page
     static_assert(CHUNKS % kRingWaves == 0, "chunks divide over the waves");
     static_assert(NQT >= 1 && NQT <= 4, "four query tiles at most");
-    // The ring: four buffers of one [K page | V page] each.
-    __shared__ __attribute__((aligned(16))) KV ring0[2 * PAGE];
-    __shared__ __attribute__((aligned(16))) KV ring1[2 * PAGE];
-    __shared__ __attribute__((aligned(16))) KV ring2[2 * PAGE];
-    __shared__ __attribute__((aligned(16))) KV ring3[2 * PAGE];
+    // The ring: NBUF buffers of one [K page | V page] each (all 160 KiB of
+    // LDS at D=256).
+    constexpr int NBUF = kRingBuffers;
+    __shared__ __attribute__((aligned(16))) KV ring[NBUF][2 * PAGE];
+    KV *const ring0 = ring[0], *const ring1 = ring[1], *const ring2 = ring[2];
 
     const int lane = threadIdx.x & 63, w = threadIdx.x >> 6, g = lane >> 4;
     const int qt = w & 3, kt = w >> 2;             // query tile, key half of every page
@@ -120,7 +123,7 @@ void attention_ring(SplitArgs a) {
     if (computes && (kt == 0 || QSPLIT)) {
         const KV *src = static_cast<const KV *>(kt == 0 ? a.q : a.q_lo) +
                         ((size_t)t * a.q_heads + (size_t)h * a.group + (row - t * a.group)) * D + 8 * g;
-        KV *dst = kt == 0 ? ring3 : ring2;
+        KV *dst = kt == 0 ? ring[NBUF - 1] : ring[NBUF - 2];
 #pragma unroll
         for (int ks = 0; ks < KS; ++ks)
             __builtin_amdgcn_global_load_lds(reinterpret_cast<const void *>(src + 32 * ks),
@@ -229,44 +232,49 @@ void attention_ring(SplitArgs a) {
         });
     };
 
+    // Before step i's barrier, pages i+1 .. i+NBUF-2 may stay in flight
+    // (vector-memory counters retire in issue order).
     auto wait_page = [&](int i) __attribute__((always_inline)) {
-        const int ahead = min(2, n - 1 - i);
-        if (ahead >= 2) wait_vmcnt<2 * CPW>();
-        else if (ahead == 1) wait_vmcnt<CPW>();
-        else wait_vmcnt<0>();
+        const int ahead = min(NBUF - 2, n - 1 - i);
+        static_for<0, NBUF - 1>([&](auto k) {
+            if (ahead == decltype(k)::value) wait_vmcnt<decltype(k)::value * CPW>();
+        });
     };
-    // Step i: wait for this wave's share of page i (pages i+1 and i+2 may
-    // stay in flight; vector-memory counters retire in issue order), meet
-    // the other waves (page i complete, page i-1 consumed), refill the
-    // consumed buffer with page i+3, then consume page i.
-    auto step = [&](int i, const KV *cur, KV *fill) __attribute__((always_inline)) {
+    // Step i: wait for this wave's share of page i, meet the other waves
+    // (page i complete, page i-1 consumed), refill the consumed buffer with
+    // page i+NBUF-1, then consume page i.
+    auto step = [&](int i, auto b) __attribute__((always_inline)) {
+        constexpr int B = decltype(b)::value;   // i % NBUF
         wait_page(i);
         ring_barrier();
-        if (i + 3 < n) stage(p0 + i + 3, fill);
-        if (computes) compute(p0 + i, cur);
+        if (i + NBUF - 1 < n) stage(p0 + i + NBUF - 1, ring[(B + NBUF - 1) % NBUF]);
+        if (computes) compute(p0 + i, ring[B]);
     };
 
     if (n > 0) {
-        stage(p0, ring0);
-        if (n > 1) stage(p0 + 1, ring1);
-        if (!QSPLIT && n > 2) stage(p0 + 2, ring2);
+        // Pages 0 .. NBUF-2 (NBUF-3 with a precise query, whose lo parts
+        // occupy buffer NBUF-2) are requested after the query fragments.
+        constexpr int FIRST = QSPLIT ? NBUF - 2 : NBUF - 1;
+        static_for<0, FIRST>([&](auto k) {
+            if (decltype(k)::value < n) stage(p0 + decltype(k)::value, ring[decltype(k)::value]);
+        });
         // Step 0: page 0 and the query fragments (loaded first) have landed;
-        // the fragments move to registers before pages 3 (and 2) overwrite
-        // them.
-        if (QSPLIT) {
-            if (n > 1) wait_vmcnt<CPW>();
-            else wait_vmcnt<0>();
-        } else {
-            wait_page(0);
+        // the fragments move to registers before the last buffers are
+        // refilled with pages.
+        {
+            const int ahead = min(FIRST - 1, n - 1);
+            static_for<0, FIRST>([&](auto k) {
+                if (ahead == decltype(k)::value) wait_vmcnt<decltype(k)::value * CPW>();
+            });
         }
         ring_barrier();
         if (computes) {
-            const uint32_t qbase = lds_addr(ring3) + qt * KS * 1024 + lane * 16;
+            const uint32_t qbase = lds_addr(ring[NBUF - 1]) + qt * KS * 1024 + lane * 16;
             static_for<0, KS>([&](auto ks) {
                 lds_read<decltype(ks)::value * 1024>(qf[decltype(ks)::value], qbase);
             });
             if constexpr (QSPLIT) {
-                const uint32_t lbase = lds_addr(ring2) + qt * KS * 1024 + lane * 16;
+                const uint32_t lbase = lds_addr(ring[NBUF - 2]) + qt * KS * 1024 + lane * 16;
                 static_for<0, KS>([&](auto ks) {
                     lds_read<decltype(ks)::value * 1024>(qlo[decltype(ks)::value], lbase);
                 });
@@ -275,14 +283,15 @@ void attention_ring(SplitArgs a) {
             static_for<0, KS>([&](auto ks) { lds_wait<0>(qf[decltype(ks)::value]); });
         }
         ring_barrier();
-        if (QSPLIT && 2 < n) stage(p0 + 2, ring2);
-        if (3 < n) stage(p0 + 3, ring3);
-        if (computes) compute(p0, ring0);
-        for (int i = 1; i < n; i += 4) {
-            step(i, ring1, ring0);
-            if (i + 1 < n) step(i + 1, ring2, ring1);
-            if (i + 2 < n) step(i + 2, ring3, ring2);
-            if (i + 3 < n) step(i + 3, ring0, ring3);
+        static_for<FIRST, NBUF>([&](auto k) {
+            if (decltype(k)::value < n) stage(p0 + decltype(k)::value, ring[decltype(k)::value]);
+        });
+        if (computes) compute(p0, ring[0]);
+        for (int i = 1; i < n; i += NBUF) {
+            static_for<0, NBUF>([&](auto k) {
+                constexpr int B = (decltype(k)::value + 1) % NBUF;
+                if (i + decltype(k)::value < n) step(i + decltype(k)::value, std::integral_constant<int, B>{});
+            });
         }
     }
 
@@ -309,18 +318,37 @@ void attention_ring(SplitArgs a) {
         const int r = 16 * qt + (lane & 15);
         if (r < a.rows) {
             float *pml = a.part_ml + ((size_t)h * a.splits + split) * 2 * a.rows;
-            float *po = a.part_o + (((size_t)h * a.splits + split) * a.rows + r) * D + 4 * g;
+            const size_t prow = (((size_t)h * a.splits + split) * a.rows + r) * D + 4 * g;
+            const float L = l * f0 + l1 * f1;
             if (lane < 16) {
                 pml[r] = M;
-                pml[a.rows + r] = l * f0 + l1 * f1;
+                pml[a.rows + r] = L;
             }
+            if constexpr (HALF) {
+                // O / L is a convex combination of the split's V rows, so it
+                // lies within their range and fp16 holds it to 2^-11
+                // relative.  A row that sees none of the split's keys (a
+                // split of candidate keys only) has L = 0 and stores zeros.
+                const float inv = L > 0.f ? 1.f / L : 0.f;
+                _Float16 *po = static_cast<_Float16 *>(static_cast<void *>(a.part_o)) + prow;
 #pragma unroll
-            for (int dt = 0; dt < DT; ++dt) {
-                const f32x4 o1 = *reinterpret_cast<const f32x4 *>(xacc + (dt * kWave + lane) * 4);
-                __builtin_nontemporal_store(acc[dt] * f0 + o1 * f1, reinterpret_cast<f32x4 *>(po + dt * 16));
+                for (int dt = 0; dt < DT; ++dt) {
+                    const f32x4 o1 = *reinterpret_cast<const f32x4 *>(xacc + (dt * kWave + lane) * 4);
+                    const f32x4 o = (acc[dt] * f0 + o1 * f1) * inv;
+                    const f16x4 v = {(_Float16)o[0], (_Float16)o[1], (_Float16)o[2], (_Float16)o[3]};
+                    __builtin_nontemporal_store(v, reinterpret_cast<f16x4 *>(po + dt * 16));
+                }
+            } else {
+                float *po = a.part_o + prow;
+#pragma unroll
+                for (int dt = 0; dt < DT; ++dt) {
+                    const f32x4 o1 = *reinterpret_cast<const f32x4 *>(xacc + (dt * kWave + lane) * 4);
+                    __builtin_nontemporal_store(acc[dt] * f0 + o1 * f1, reinterpret_cast<f32x4 *>(po + dt * 16));
+                }
             }
         }
     }
+    // end of attention_ring
 }
 
 // Raw fp16: 16-bit P; raw bf16: hi + lo P (bf16's 8-bit significand alone

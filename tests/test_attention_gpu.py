@@ -174,7 +174,7 @@ def test_raw_attention_prefill_shape_sampled_rows(gpu):
 
 
 @pytest.mark.parametrize('T,position', [(1, 0), (1, 31), (1, 32), (2, 30), (3, 5), (5, 1000),
-                                        (8, 0), (8, 4089), (7, 139257)])
+                                        (8, 0), (8, 28), (8, 31), (8, 4089), (7, 139257)])
 def test_raw_attention_edges_and_stale_pages(gpu, T, position):
     """Ragged last page, first page, capacity boundary; pages past the last
     key hold NaN, which must never reach the result."""
@@ -182,6 +182,18 @@ def test_raw_attention_edges_and_stale_pages(gpu, T, position):
     q, k, v, _ = make_inputs(w)
     got = gpu_attention(w, q, k, v, gpu, fill_nan=True)
     assert_parity(got, ref.gqa_attention(q, k, v, w.position, w.scale))
+
+
+def test_verify_peaked_softmax(gpu):
+    """Verify-8 whose softmax is dominated by a few keys scaled x8: the
+    output is then close to single V rows, the largest values the fp16
+    partial rows of the verify kernel (O / l) and the fp16 output can hold;
+    both roundings stay inside the bounds."""
+    w = Workload('peaked', 24, 4, 256, 8, 5000, 1 / 16, 'f16', 41, q_std=1.0, kv_std=0.5, outliers=16)
+    q, k, v, _ = make_inputs(w)
+    want = ref.gqa_attention(q, k, v, w.position, w.scale)
+    assert np.abs(want).max() > 0.5   # some rows follow single keys
+    assert_parity(gpu_attention(w, q, k, v, gpu, fill_nan=True), want)
 
 
 def test_raw_attention_grouped_equals_sequential(gpu):
