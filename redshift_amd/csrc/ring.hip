@@ -37,6 +37,8 @@ template <> struct Vec8<__bf16> { using type = bf16x8; };
 typedef _Float16 f16x4 __attribute__((ext_vector_type(4)));
 typedef __bf16 bf16x4 __attribute__((ext_vector_type(4)));
 typedef short i16x4 __attribute__((ext_vector_type(4)));
+typedef unsigned u32x2 __attribute__((ext_vector_type(2)));
+typedef unsigned u32x4 __attribute__((ext_vector_type(4)));
 template <typename T> struct Vec4;
 template <> struct Vec4<_Float16> { using type = f16x4; };
 template <> struct Vec4<__bf16> { using type = bf16x4; };
@@ -330,13 +332,28 @@ void attention_ring(SplitArgs a) {
                 // relative.  A row that sees none of the split's keys (a
                 // split of candidate keys only) has L = 0 and stores zeros.
                 const float inv = L > 0.f ? 1.f / L : 0.f;
-                _Float16 *po = static_cast<_Float16 *>(static_cast<void *>(a.part_o)) + prow;
-#pragma unroll
-                for (int dt = 0; dt < DT; ++dt) {
+                // Lane group g holds dims 4g..4g+3 of every 16-dim tile.
+                // For each pair of tiles (dt0, dt0+1) the groups g and g^1
+                // swap halves (permlane16_swap exchanges lane groups 0<->1
+                // and 2<->3), so that every lane holds 8 consecutive dims:
+                // group 0 dims 0-7 of dt0, group 2 dims 8-15 of dt0, groups
+                // 1 and 3 the same of dt0+1.  Each store then writes 16 B
+                // per lane and 64 contiguous bytes per row.
+                _Float16 *po = static_cast<_Float16 *>(static_cast<void *>(a.part_o)) +
+                               (prow - 4 * g) + 16 * (g & 1) + 4 * (g & 2);
+                auto half4 = [&](int dt) __attribute__((always_inline)) {
                     const f32x4 o1 = *reinterpret_cast<const f32x4 *>(xacc + (dt * kWave + lane) * 4);
                     const f32x4 o = (acc[dt] * f0 + o1 * f1) * inv;
                     const f16x4 v = {(_Float16)o[0], (_Float16)o[1], (_Float16)o[2], (_Float16)o[3]};
-                    __builtin_nontemporal_store(v, reinterpret_cast<f16x4 *>(po + dt * 16));
+                    return __builtin_bit_cast(u32x2, v);
+                };
+#pragma unroll
+                for (int dt = 0; dt < DT; dt += 2) {
+                    const u32x2 x = half4(dt), y = half4(dt + 1);
+                    const auto s0 = __builtin_amdgcn_permlane16_swap(x[0], y[0], false, false);
+                    const auto s1 = __builtin_amdgcn_permlane16_swap(x[1], y[1], false, false);
+                    const u32x4 v = {s0[0], s1[0], s0[1], s1[1]};
+                    __builtin_nontemporal_store(v, reinterpret_cast<u32x4 *>(po + dt * 16));
                 }
             } else {
                 float *po = a.part_o + prow;
