@@ -232,6 +232,36 @@ def time_fused(torch, A, w, layers, steps, warmup, seed):
     return start.elapsed_time(end) / steps
 
 
+def time_kv_copy(torch, A, w, layers, steps, warmup, seed):
+    """The KV-cache manager's checkpoint copy (qv_kv_copy, the reference's
+    copy_state prefix copy, src/runtime.cu:455-485) of a full `w.keys`-token
+    prefix, every page of K and V, from each of `layers` caches to a snapshot
+    cache.  Returns microseconds per layer (one copy: two kernels, K and V)."""
+    from redshift_amd.kvcache import copy_prefix
+    caches, _ = make_layers(torch, A, w, layers, seed)
+    dtype = caches[0].dtype
+    snaps = [A.PagedKV(w.kv_heads, w.head_dim, caches[0].capacity, dtype) for _ in range(layers)]
+
+    def step():
+        for i in range(layers):
+            copy_prefix(snaps[i], caches[i], w.keys)
+
+    for _ in range(warmup):
+        step()
+    torch.cuda.synchronize()
+    start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    start.record()
+    for _ in range(steps):
+        step()
+    end.record()
+    torch.cuda.synchronize()
+    ok = all(torch.equal(snaps[i].k[:caches[i].k.numel()], caches[i].k) for i in (0, layers - 1))
+    del caches, snaps
+    torch.cuda.empty_cache()
+    assert ok, 'checkpoint copy differs from its source'
+    return 1000 * start.elapsed_time(end) / (steps * layers)
+
+
 def cpu_baseline(w, target_s=8.0):
     """The numpy fp32 restatement of the reference's CPU attention (oracle),
     one layer's decode, timed single-threaded and on all host cores (capped
@@ -287,7 +317,8 @@ def main():
     ap.add_argument('--layers', type=int, default=LAYERS)
     ap.add_argument('--no-cpu', action='store_true', help='skip the CPU baseline')
     ap.add_argument('--no-extra', action='store_true', help='skip the secondary workloads')
-    ap.add_argument('--extras', default='verify8_16k,decode_4k,prefill_2k,fused_verify8_16k,fused_decode_139k',
+    ap.add_argument('--extras', default='verify8_16k,decode_4k,prefill_2k,fused_verify8_16k,fused_decode_139k,'
+                                        'kv_checkpoint_139k',
                     help='comma-separated secondary workloads to run')
     ap.add_argument('--drop-in', action='store_true',
                     help='only time the host-buffer qv_test_attention (PCIe-inclusive) and exit')
@@ -375,6 +406,14 @@ def main():
                            'GB/s': round(wf.kv_bytes() / (us * 1e-6) / 1e9, 1),
                            'frac_hbm': round(wf.kv_bytes() / (us * 1e-6) / 1e9 / HBM_PEAK_GBS, 4),
                            'what': 'qv_attention_fused per layer: prepare + append + attention + gate'}
+        if 'kv_checkpoint_139k' in chosen:
+            log('kv_checkpoint_139k: 4 layers')
+            us = time_kv_copy(torch, A, w, 4, max(5, args.steps // 2), 2, seed=5)
+            moved = 2 * w.kv_bytes()   # every byte of K and V read once and written once
+            extra['kv_checkpoint_139k'] = {
+                'us_per_layer': round(us, 1), 'GB/s': round(moved / (us * 1e-6) / 1e9, 1),
+                'frac_hbm': round(moved / (us * 1e-6) / 1e9 / HBM_PEAK_GBS, 4),
+                'what': 'qv_kv_copy of a 139,264-token prefix (K and V pages, read + write bytes)'}
         result['extra'] = extra
     if not args.no_cpu:
         log('cpu baseline (numpy fp32, 1 thread, one layer)')

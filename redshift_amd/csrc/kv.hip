@@ -94,16 +94,29 @@ void prepare_kernel(_Float16 *q_hilo, _Float16 *k_pages, _Float16 *v_pages, cons
 
 // Copy of whole pages: for every KV head, elements [0, n) of its run (the
 // pages of tokens 0 .. n/D-1) from a cache of stride src_stride to one of
-// stride dst_stride, 16 bytes per lane.
-__global__ __launch_bounds__(256)
+// stride dst_stride.  Each thread moves kCopyUnroll 16-byte pieces of one
+// head, all loads issued before the stores, non-temporal (every byte is
+// touched once).  n is a whole number of pages, so per_head (16-byte pieces
+// per head) is a multiple of 32 * D / 8 = 512 (D = 128) or 1024 (D = 256),
+// and thus of kCopyUnroll * kCopyThreads.
+constexpr int kCopyUnroll = 4, kCopyThreads = 128;
+__global__ __launch_bounds__(kCopyThreads)
 void copy_pages(uint4 *dst, const uint4 *src, size_t dst_stride, size_t src_stride, size_t n,
                 int kv_heads) {
     const size_t per_head = n / 8;   // uint4 per head
-    const size_t total = per_head * kv_heads;
-    for (size_t e = (size_t)blockIdx.x * blockDim.x + threadIdx.x; e < total;
-         e += (size_t)gridDim.x * blockDim.x) {
-        const size_t h = e / per_head, i = e - h * per_head;
-        dst[h * (dst_stride / 8) + i] = src[h * (src_stride / 8) + i];
+    const size_t chunk = (size_t)kCopyUnroll * blockDim.x;
+    const size_t chunks = per_head / chunk * kv_heads;
+    for (size_t c = blockIdx.x; c < chunks; c += gridDim.x) {
+        const size_t first = c * chunk;
+        const size_t h = first / per_head, i0 = first - h * per_head + threadIdx.x;
+        typedef unsigned u32x4 __attribute__((ext_vector_type(4)));
+        const u32x4 *s = reinterpret_cast<const u32x4 *>(src + h * (src_stride / 8) + i0);
+        u32x4 *d = reinterpret_cast<u32x4 *>(dst + h * (dst_stride / 8) + i0);
+        u32x4 v[kCopyUnroll];
+#pragma unroll
+        for (int u = 0; u < kCopyUnroll; ++u) v[u] = __builtin_nontemporal_load(s + u * blockDim.x);
+#pragma unroll
+        for (int u = 0; u < kCopyUnroll; ++u) __builtin_nontemporal_store(v[u], d + u * blockDim.x);
     }
 }
 
@@ -113,13 +126,14 @@ void launch_copy(void *dst_k, void *dst_v, const void *src_k, const void *src_v,
                  int head_dim, int dst_capacity, int src_capacity, int pages, hipStream_t stream) {
     const size_t n = (size_t)pages * kPageTokens * head_dim;   // 16-bit elements per head
     if (!n) return;
-    const size_t total = n / 8 * kv_heads;
-    const unsigned blocks = (unsigned)std::min<size_t>((total + 255) / 256, 4096);
+    require((n / 8) % (kCopyUnroll * kCopyThreads) == 0, "page copy needs whole 512-piece chunks per head");
+    const size_t chunks = n / 8 / (kCopyUnroll * kCopyThreads) * kv_heads;
+    const unsigned blocks = (unsigned)std::min<size_t>(chunks, 16384);
     const size_t ds = (size_t)dst_capacity * head_dim, ss = (size_t)src_capacity * head_dim;
-    hipLaunchKernelGGL(copy_pages, dim3(blocks), dim3(256), 0, stream, static_cast<uint4 *>(dst_k),
+    hipLaunchKernelGGL(copy_pages, dim3(blocks), dim3(kCopyThreads), 0, stream, static_cast<uint4 *>(dst_k),
                        static_cast<const uint4 *>(src_k), ds, ss, n, kv_heads);
     check(hipGetLastError());
-    hipLaunchKernelGGL(copy_pages, dim3(blocks), dim3(256), 0, stream, static_cast<uint4 *>(dst_v),
+    hipLaunchKernelGGL(copy_pages, dim3(blocks), dim3(kCopyThreads), 0, stream, static_cast<uint4 *>(dst_v),
                        static_cast<const uint4 *>(src_v), ds, ss, n, kv_heads);
     check(hipGetLastError());
 }
