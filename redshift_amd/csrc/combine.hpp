@@ -37,6 +37,14 @@ __device__ __forceinline__ void combine_row(const PT *part_o, const float *part_
     constexpr bool kNormalised = !std::is_same<PT, float>::value;
     const size_t stride = (size_t)rows * D;
 
+    const int t = row / group, hq = h * group + (row - t * group);
+    // The gate of a gated output is requested with the partials, so it has
+    // landed by the final store instead of costing one more round trip.
+    typedef float GV __attribute__((ext_vector_type(DV)));
+    GV gv = {};
+    if (out_mode == kOutGated && w4 == 0 && valid)
+        gv = *reinterpret_cast<const GV *>(gate + ((size_t)t * q_heads + hq) * 2 * D + D + lane * DV);
+
     float M = -INFINITY, L = 0.f, acc[DV] = {};
     // Rounds of 4*kBatch splits (one round for up to 64 splits).
     for (int s0 = 0; s0 < splits; s0 += 4 * kBatch) {
@@ -91,15 +99,13 @@ __device__ __forceinline__ void combine_row(const PT *part_o, const float *part_
     __syncthreads();
     if (w4 == 0 && valid) {
         const float Lt = part[D] + part[(D + 1) + D] + part[2 * (D + 1) + D] + part[3 * (D + 1) + D];
-        const int t = row / group, hq = h * group + (row - t * group);
         const size_t idx = ((size_t)t * q_heads + hq) * D + lane * DV;
 #pragma unroll
         for (int d = 0; d < DV; ++d) {
             const int j = lane * DV + d;
             const float o = (part[j] + part[(D + 1) + j] + part[2 * (D + 1) + j] + part[3 * (D + 1) + j]) / Lt;
             if (out_mode == kOutGated) {
-                const float gv = gate[((size_t)t * q_heads + hq) * 2 * D + D + j];
-                static_cast<float *>(out)[idx + d] = o * (1.f / (1.f + expf(-gv)));
+                static_cast<float *>(out)[idx + d] = o * (1.f / (1.f + expf(-gv[d])));
             } else if (out_mode == kOutF32) {
                 static_cast<float *>(out)[idx + d] = o;
             } else {
