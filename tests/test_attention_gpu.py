@@ -184,6 +184,17 @@ def test_raw_attention_edges_and_stale_pages(gpu, T, position):
     assert_parity(got, ref.gqa_attention(q, k, v, w.position, w.scale))
 
 
+@pytest.mark.parametrize('T,position,dtype', [(1, 20000, 'f16'), (1, 20000, 'bf16'), (3, 3000, 'f16')])
+def test_single_kv_head_many_splits(gpu, T, position, dtype):
+    """One KV head spreads a row's keys over many splits (157 at 20,000
+    keys, more than one combine round of 64), fp32 partials of the decode
+    kernel and fp16 ones of the verify kernel."""
+    w = Workload('one_head', 24, 1, 256, T, position, 1 / 16, dtype, 600 + T, 1.0, 0.5)
+    q, k, v, _ = make_inputs(w)
+    want = ref.gqa_attention(to_float(q, dtype), to_float(k, dtype), to_float(v, dtype), position, w.scale)
+    assert_parity(gpu_attention(w, q, k, v, gpu, fill_nan=True, out_dtype=gpu.float32), want)
+
+
 def test_verify_peaked_softmax(gpu):
     """Verify-8 whose softmax is dominated by a few keys scaled x8: the
     output is then close to single V rows, the largest values the fp16
