@@ -135,7 +135,11 @@ int qv_attention(void *out, const void *q, const void *k_pages, const void *v_pa
                  int tokens, int position, int capacity, float scale,
                  void *workspace, uint64_t workspace_bytes, void *stream);
 /* The two phases of qv_attention for one token chunk (G*tokens <= 48), for
- * callers that time or schedule them separately. */
+ * callers that time or schedule them separately. The workspace carries each
+ * split's row max and sum (fp32) and its partial output rows: fp32, or, on
+ * fp16 pages with 17..48 rows per KV head, fp16 rows normalised by their sum
+ * (2^-11 relative, like the fp16 output). A combine reads what the split of
+ * the same shape and dtype wrote. */
 int qv_attention_split(const void *q, const void *k_pages, const void *v_pages,
                        int dtype, int q_heads, int kv_heads, int head_dim,
                        int tokens, int position, int capacity, float scale,
