@@ -365,7 +365,6 @@ void attention_ring(SplitArgs a) {
             }
         }
     }
-    // end of attention_ring
 }
 
 // Raw fp16: 16-bit P; raw bf16: hi + lo P (bf16's 8-bit significand alone
