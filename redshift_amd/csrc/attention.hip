@@ -17,7 +17,8 @@
 // Two partial kernels share that arithmetic:
 //   attention_stream  one query tile (<= 16 rows, decode).  Every wave streams
 //                     its own run of pages with a private softmax state; the
-//                     four waves merge through LDS once at the end.
+//                     four waves merge through LDS once at the end (one
+//                     barrier: each wave's state in its own slot).
 //   attention_coop    up to three query tiles (<= 48 rows, verification).
 //                     Eight waves split each 128-key block (four pages) by
 //                     keys for Q.K^T and by head dims for P.V, exchanging the
@@ -124,7 +125,7 @@ void attention_stream(SplitArgs a) {
     using V8 = typename Vec8<KV>::type;
     using QS = QueryStage<D, 1, QSPLIT, KV>;
     constexpr int KS = D / 32, DT = D / 16, NQ = QSPLIT ? 2 : 1;
-    __shared__ f32x4 so[DT * kWave];       // merge buffer
+    __shared__ f32x4 so[kWaves][DT * kWave];   // merge slots, one per wave
     __shared__ V8 sq[QS::N * kWave];       // query fragments
     __shared__ float sml[kWaves][2][16];
 
@@ -248,45 +249,44 @@ void attention_stream(SplitArgs a) {
     }
 
     // ---- merge the waves of this workgroup -------------------------------
+    // One barrier: every wave leaves its (m, l) and its unscaled
+    // accumulators in its own LDS slot; then every thread merges the four
+    // slots of its output elements (row-major, D contiguous floats per row,
+    // so each store instruction writes whole rows).  Element (row, 4*d4 ..
+    // +3) is the f32x4 of lane (row%16) + 16*(d4%4) in fragment d4/4.
     l += __shfl_xor(l, 16, kWave);
     l += __shfl_xor(l, 32, kWave);
     if (lane < 16) {
         sml[w][0][lane] = m;
         sml[w][1][lane] = l;
     }
-    lds_barrier();   // every wave is past the loop: smem may now hold `so`
-    float *pml = a.part_ml + ((size_t)h * a.splits + split) * 2 * a.rows;
-    const int row = lane & 15;
-    float M = -INFINITY;
 #pragma unroll
-    for (int ww = 0; ww < kWaves; ++ww) M = fmaxf(M, sml[ww][0][row]);
-    const float mu = M == -INFINITY ? 0.f : M;
-    const float f = exp2f(m - mu);
+    for (int dt = 0; dt < DT; ++dt) so[w][dt * kWave + lane] = acc[dt];
+    lds_barrier();
+    if (w == 0 && lane < a.rows && lane < 16) {
+        float M = -INFINITY;
 #pragma unroll
-    for (int dt = 0; dt < DT; ++dt) acc[dt] *= f;
-    if (w == 0 && lane < 16 && row < a.rows) {
+        for (int ww = 0; ww < kWaves; ++ww) M = fmaxf(M, sml[ww][0][lane]);
+        const float mu = M == -INFINITY ? 0.f : M;
         float L = 0.f;
 #pragma unroll
-        for (int ww = 0; ww < kWaves; ++ww) L += sml[ww][1][row] * exp2f(sml[ww][0][row] - mu);
-        pml[row] = M;
-        pml[a.rows + row] = L;
+        for (int ww = 0; ww < kWaves; ++ww) L += sml[ww][1][lane] * exp2f(sml[ww][0][lane] - mu);
+        float *pml = a.part_ml + ((size_t)h * a.splits + split) * 2 * a.rows;
+        pml[lane] = M;
+        pml[a.rows + lane] = L;
     }
-    for (int step = 0; step < kWaves; ++step) {
-        if (w == step) {
-#pragma unroll
-            for (int dt = 0; dt < DT; ++dt) {
-                f32x4 &dst = so[dt * kWave + lane];
-                dst = step ? dst + acc[dt] : acc[dt];
-            }
-        }
-        lds_barrier();
-    }
-    // Row-major store of the merged partial: element (row, 4*d4 .. +3) is the
-    // f32x4 of lane (row%16) + 16*(d4%4) in fragment d4/4.
     f32x4 *po = reinterpret_cast<f32x4 *>(a.part_o + ((size_t)h * a.splits + split) * a.rows * D);
     for (int e = threadIdx.x; e < a.rows * (D / 4); e += kWaves * kWave) {
         const int r = e / (D / 4), d4 = e - r * (D / 4);
-        __builtin_nontemporal_store(so[(d4 >> 2) * kWave + r + 16 * (d4 & 3)], po + e);
+        const int idx = (d4 >> 2) * kWave + r + 16 * (d4 & 3);
+        float M = -INFINITY;
+#pragma unroll
+        for (int ww = 0; ww < kWaves; ++ww) M = fmaxf(M, sml[ww][0][r]);
+        const float mu = M == -INFINITY ? 0.f : M;
+        f32x4 o = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int ww = 0; ww < kWaves; ++ww) o += so[ww][idx] * exp2f(sml[ww][0][r] - mu);
+        __builtin_nontemporal_store(o, po + e);
     }
 }
 
