@@ -13,13 +13,13 @@ namespace rs {
 enum { kOutSame = 0, kOutF32 = 1, kOutGated = 2 };
 
 // One row of one KV head, combined by the four waves w4 = 0..3 of a
-// workgroup (every wave must call it, `valid` or not: it holds two workgroup
-// barriers).  Lane l owns head dims DV*l .. DV*l+DV-1 (DV = D/64);
+// workgroup (every wave must call it, `valid` or not: it holds a workgroup
+// barrier).  Lane l owns head dims DV*l .. DV*l+DV-1 (DV = D/64);
 // wave w4 takes splits w4, w4+4, ... and issues the loads of up to kBatch of
 // them (their m, l and partial row) at once, so a combine over up to
 // 4*kBatch splits costs one memory round trip (non-temporal: each partial
-// row is read once).  The waves then agree on the row max and reduce through
-// `scratch` (4*(D+1) + 4 floats of LDS per group).  PT is the type of the
+// row is read once).  The waves then merge through `scratch` (4*(D+1) + 4
+// floats of LDS per group), each thread one head dim.  PT is the type of the
 // partial rows: float (unnormalised O) or _Float16 (O / l, weighted by l
 // here).
 template <int D, typename KV, typename PT>
@@ -38,12 +38,13 @@ __device__ __forceinline__ void combine_row(const PT *part_o, const float *part_
     const size_t stride = (size_t)rows * D;
 
     const int t = row / group, hq = h * group + (row - t * group);
-    // The gate of a gated output is requested with the partials, so it has
-    // landed by the final store instead of costing one more round trip.
-    typedef float GV __attribute__((ext_vector_type(DV)));
-    GV gv = {};
-    if (out_mode == kOutGated && w4 == 0 && valid)
-        gv = *reinterpret_cast<const GV *>(gate + ((size_t)t * q_heads + hq) * 2 * D + D + lane * DV);
+    // This thread's head dim in the final merge.  The gate of a gated
+    // output is requested with the partials, so it has landed by the final
+    // store instead of costing one more round trip.
+    const int jd = w4 * kWave + lane;
+    float gv = 0.f;
+    if (out_mode == kOutGated && valid && jd < D)
+        gv = gate[((size_t)t * q_heads + hq) * 2 * D + D + jd];
 
     float M = -INFINITY, L = 0.f, acc[DV] = {};
     // Rounds of 4*kBatch splits (one round for up to 64 splits).
@@ -88,29 +89,34 @@ __device__ __forceinline__ void combine_row(const PT *part_o, const float *part_
         }
         M = rm;
     }
-    if (lane == 0) wmax[w4] = M;
-    __syncthreads();
-    const float G = fmaxf(fmaxf(wmax[0], wmax[1]), fmaxf(wmax[2], wmax[3]));
-    const float gu = G == -INFINITY ? 0.f : G;
-    const float f = __builtin_amdgcn_exp2f(M - gu);
+    // One barrier: every wave leaves its (M, L) and its unscaled
+    // accumulators in its slot; then thread j of the workgroup merges head
+    // dim j of the four slots and stores it.
 #pragma unroll
-    for (int d = 0; d < DV; ++d) part[w4 * (D + 1) + lane * DV + d] = acc[d] * f;
-    if (lane == 0) part[w4 * (D + 1) + D] = L * f;
+    for (int d = 0; d < DV; ++d) part[w4 * (D + 1) + lane * DV + d] = acc[d];
+    if (lane == 0) {
+        wmax[w4] = M;
+        part[w4 * (D + 1) + D] = L;
+    }
     __syncthreads();
-    if (w4 == 0 && valid) {
-        const float Lt = part[D] + part[(D + 1) + D] + part[2 * (D + 1) + D] + part[3 * (D + 1) + D];
-        const size_t idx = ((size_t)t * q_heads + hq) * D + lane * DV;
+    if (valid && jd < D) {
+        const float G = fmaxf(fmaxf(wmax[0], wmax[1]), fmaxf(wmax[2], wmax[3]));
+        const float gu = G == -INFINITY ? 0.f : G;
+        float Lt = 0.f, o = 0.f;
 #pragma unroll
-        for (int d = 0; d < DV; ++d) {
-            const int j = lane * DV + d;
-            const float o = (part[j] + part[(D + 1) + j] + part[2 * (D + 1) + j] + part[3 * (D + 1) + j]) / Lt;
-            if (out_mode == kOutGated) {
-                static_cast<float *>(out)[idx + d] = o * (1.f / (1.f + expf(-gv[d])));
-            } else if (out_mode == kOutF32) {
-                static_cast<float *>(out)[idx + d] = o;
-            } else {
-                static_cast<KV *>(out)[idx + d] = (KV)o;
-            }
+        for (int ww = 0; ww < 4; ++ww) {
+            const float f = __builtin_amdgcn_exp2f(wmax[ww] - gu);
+            Lt += part[ww * (D + 1) + D] * f;
+            o += part[ww * (D + 1) + jd] * f;
+        }
+        o /= Lt;
+        const size_t idx = ((size_t)t * q_heads + hq) * D + jd;
+        if (out_mode == kOutGated) {
+            static_cast<float *>(out)[idx] = o * (1.f / (1.f + expf(-gv)));
+        } else if (out_mode == kOutF32) {
+            static_cast<float *>(out)[idx] = o;
+        } else {
+            static_cast<KV *>(out)[idx] = (KV)o;
         }
     }
 }
