@@ -318,7 +318,7 @@ def main():
     ap.add_argument('--no-cpu', action='store_true', help='skip the CPU baseline')
     ap.add_argument('--no-extra', action='store_true', help='skip the secondary workloads')
     ap.add_argument('--extras', default='verify8_16k,decode_4k,prefill_2k,fused_verify8_16k,fused_decode_139k,'
-                                        'kv_checkpoint_139k',
+                                        'fused_prefill_2k,kv_checkpoint_139k',
                     help='comma-separated secondary workloads to run')
     ap.add_argument('--drop-in', action='store_true',
                     help='only time the host-buffer qv_test_attention (PCIe-inclusive) and exit')
@@ -334,7 +334,7 @@ def main():
 
     from redshift_amd import attention as A
     from redshift_amd.runtime import load_library
-    from redshift_amd.workloads import WORKLOADS
+    from redshift_amd.workloads import WORKLOADS, Workload
 
     assert torch.cuda.is_available(), 'bench.py needs a GPU'
     torch.cuda.set_device(0)
@@ -406,6 +406,18 @@ def main():
                            'GB/s': round(wf.kv_bytes() / (us * 1e-6) / 1e9, 1),
                            'frac_hbm': round(wf.kv_bytes() / (us * 1e-6) / 1e9 / HBM_PEAK_GBS, 4),
                            'what': 'qv_attention_fused per layer: prepare + append + attention + gate'}
+        if 'fused_prefill_2k' in chosen:
+            # The fused drop-in on a 2048-token prefill chunk at position 6144
+            # (fp16 pages, the model's fp32 q_gate/key/value), one call per layer.
+            wq = Workload('fused_prefill_2k', 24, 4, 256, 2048, 6144, 1 / 16, 'f16', 2, kv_std=0.5)
+            log('fused_prefill_2k: 4 layers')
+            ms = time_fused(torch, A, wq, 4, max(3, args.steps // 4), 2, seed=6)
+            us = 1000 * ms / 4
+            extra['fused_prefill_2k'] = {'us_per_layer': round(us, 1),
+                                         'TFLOP/s': round(wq.flops() / (us * 1e-6) / 1e12, 1),
+                                         'frac_mfma_peak': round(wq.flops() / (us * 1e-6) / MFMA_BF16_PEAK, 4),
+                                         'what': 'qv_attention_fused on a 2048-token chunk at 6144: prepare + '
+                                                 'append + precise prefill (fp32 q as fp16 hi + lo, hi + lo P) + gate'}
         if 'kv_checkpoint_139k' in chosen:
             log('kv_checkpoint_139k: 4 layers')
             us = time_kv_copy(torch, A, w, 4, max(5, args.steps // 2), 2, seed=5)
