@@ -435,16 +435,17 @@ def test_one_workspace_across_shapes_and_phases(gpu):
 
 # ---- KV-cache manager (checkpoint / restore / commit) ----------------------
 
-def test_kv_copy_prefix_bitwise(gpu):
+@pytest.mark.parametrize('head_dim,kv_heads', [(256, 4), (128, 2)])
+def test_kv_copy_prefix_bitwise(gpu, head_dim, kv_heads):
     """qv_kv_copy moves the pages of a prefix between caches of different
     capacities, every value bit for bit; a snapshot of 1000 tokens needs 1024."""
     from redshift_amd.kvcache import copy_prefix
     rng = np.random.default_rng(7)
-    rows = gpu.from_numpy(rng.standard_normal((3000, 4, 256)).astype(np.float16)).cuda()
-    big = A.PagedKV(4, 256, 4096, gpu.float16).pack(rows, -rows)
-    snap = A.PagedKV(4, 256, 1024, gpu.float16)
+    rows = gpu.from_numpy(rng.standard_normal((3000, kv_heads, head_dim)).astype(np.float16)).cuda()
+    big = A.PagedKV(kv_heads, head_dim, 4096, gpu.float16).pack(rows, -rows)
+    snap = A.PagedKV(kv_heads, head_dim, 1024, gpu.float16)
     copy_prefix(snap, big, 1000)
-    other = A.PagedKV(4, 256, 2048, gpu.float16)
+    other = A.PagedKV(kv_heads, head_dim, 2048, gpu.float16)
     other.k.fill_(float('nan'))
     other.v.fill_(float('nan'))
     copy_prefix(other, snap, 1000)
