@@ -24,7 +24,10 @@ Pinning status (what checks each function, see tests/test_oracle.py):
   rope            one-hot closed form (rotate-half pairs (i, i+32), base 1e7).
   fused_attention closed-form long-context KAT at positions 2047 (T=3),
                   32767 and 139263 (the reference's own KAT), plus the
-                  grouped == sequential invariant and prefix preservation.
+                  grouped == sequential invariant and prefix preservation;
+                  and the reference's own output on its sine-wave fixture
+                  (tests/golden/fused_attention.npz), which it matches bit
+                  for bit after rounding to fp32.
   gqa_attention   torch's scaled_dot_product_attention in float64 (an
                   independent library routine), brute force on tiny shapes,
                   single-key / uniform-key / causal invariants.

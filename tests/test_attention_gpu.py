@@ -101,6 +101,23 @@ def test_attention_long_context_against_closed_form(lib, gpu, position, batch):
     np.testing.assert_array_equal(vc[:n].view(np.uint16), c['value_cache'].reshape(-1).view(np.uint16))
 
 
+@pytest.mark.parametrize('batch,position', [(3, 5), (8, 40)])
+def test_drop_in_matches_reference_vectors(lib, gpu, batch, position):
+    """qv_test_attention against the output of the reference's own CPU
+    attention (tests/cpu_reference.py) on its sine-wave fixture, committed
+    in tests/golden/fused_attention.npz, with the reference test's
+    tolerances (tests/test_cuda.py:218-221)."""
+    from pathlib import Path
+    z = np.load(Path(__file__).resolve().parent / 'golden' / 'fused_attention.npz')
+    g = {k[len(f'b{batch}_p{position}_'):]: z[k] for k in z.files if k.startswith(f'b{batch}_p{position}_')}
+    out, kc, vc = run_test_attention(lib, g['kc'][:position], g['vc'][:position], g['q_gate'], g['key'],
+                                     g['value'], g['q_norm'], g['k_norm'], batch, position, 1e-6)
+    assert_close(out, g['out'], 3e-4)
+    assert_close(kc.astype(np.float64), g['kc'].astype(np.float64), 2e-3)
+    np.testing.assert_array_equal(vc, g['vc'].reshape(-1))
+    np.testing.assert_array_equal(kc[:position * 1024], g['kc'][:position].reshape(-1))
+
+
 def test_error_is_cleared_after_a_successful_call(lib, gpu):
     """tests/test_cuda.py:85-87."""
     one = np.ones(1, np.float32)

@@ -6,8 +6,11 @@
   sign of the rotation, the base 1e7 and the order RMS -> gamma -> RoPE)
 * torch's scaled_dot_product_attention in float64 for the raw GQA core
 * invariants: single key, equal keys, causality, grouped == sequential
+* input/output vectors of the reference's own CPU attention on its sine-wave
+  fixture (tests/golden/fused_attention.npz, written by the script beside it)
 """
 import math
+from pathlib import Path
 
 import numpy as np
 import pytest
@@ -155,3 +158,29 @@ def test_cpu_plumbing_workload_against_sdpa():
     want = _sdpa_reference(to_float(q, w.dtype), to_float(k, w.dtype), to_float(v, w.dtype), w.position, w.scale)
     np.testing.assert_allclose(ref.gqa_attention(q, k, v, w.position, w.scale), want, atol=1e-12)
     np.testing.assert_allclose(ref.gqa_attention_fp32(q, k, v, w.position, w.scale), want, atol=2e-5)
+
+
+GOLDEN = Path(__file__).resolve().parent / 'golden' / 'fused_attention.npz'
+
+
+def golden_cases():
+    z = np.load(GOLDEN)
+    for batch, position in z['cases']:
+        tag = f'b{batch}_p{position}'
+        yield int(batch), int(position), {k[len(tag) + 1:]: z[k] for k in z.files if k.startswith(tag + '_')}
+
+
+@pytest.mark.parametrize('case', list(golden_cases()), ids=lambda c: f'b{c[0]}_p{c[1]}')
+def test_fused_attention_matches_reference_vectors(case):
+    """The oracle against the reference's own tests/cpu_reference.py output
+    on its sine-wave fixture (RoPE on q and k at positions 5..47, norm
+    weights 1 +- i/512, gate): output to the float32 storage of the vectors,
+    appended K/V rows bit for bit."""
+    batch, position, g = case
+    out, kc, vc = ref.fused_attention(g['kc'][:position].astype(np.float64), g['vc'][:position].astype(np.float64),
+                                      g['q_gate'], g['key'], g['value'], g['q_norm'], g['k_norm'],
+                                      batch, position, 1e-6)
+    e = g['out'].astype(np.float64).reshape(-1)
+    assert np.max(np.abs(out - e) / (1 + np.abs(e))) < 1e-7   # the float32 storage's own rounding
+    np.testing.assert_array_equal(np.asarray(kc, np.float64), g['kc'].astype(np.float64).reshape(-1))
+    np.testing.assert_array_equal(np.asarray(vc, np.float64), g['vc'].astype(np.float64).reshape(-1))
