@@ -122,10 +122,29 @@ def time_workload(torch, A, w, layers, steps, warmup, seed):
     for _ in range(warmup):
         graph.replay()
     graph_ms = timed(lambda s: graph.replay(), steps)
-    del graph, caches
+    del graph
+    split_graph_us = None
+    if one_chunk:
+        # The split kernels alone, replayed as one graph: the kernel's time
+        # without the host launch overhead that eager events include.
+        def splits_only():
+            for i in range(layers):
+                A.attention_split(queries[i], caches[i], w.position, w.scale, ws)
+        sgraph = torch.cuda.CUDAGraph()
+        with torch.cuda.stream(capture_stream):
+            splits_only()
+            torch.cuda.synchronize()
+            with torch.cuda.graph(sgraph, stream=capture_stream):
+                splits_only()
+        torch.cuda.current_stream().wait_stream(capture_stream)
+        for _ in range(warmup):
+            sgraph.replay()
+        split_graph_us = 1000.0 * timed(lambda s: sgraph.replay(), steps) / layers
+        del sgraph
+    del caches
     torch.cuda.empty_cache()
     return dict(ms_per_step=graph_ms, eager_ms_per_step=eager_ms,
-                split_us=1000.0 * sum(split_ms) / len(split_ms))
+                split_us=1000.0 * sum(split_ms) / len(split_ms), split_graph_us=split_graph_us)
 
 
 def measured_traffic():
@@ -385,6 +404,9 @@ def main():
                            'eager_us_per_layer': round(1000 * rx['eager_ms_per_step'] / args.layers, 2),
                            'split_kernel_us': round(rx['split_us'], 2),
                            'split_kernel_GB/s': round(wx.kv_bytes() / (rx['split_us'] * 1e-6) / 1e9, 1),
+                           'split_graph_us': round(rx['split_graph_us'], 2),
+                           'split_graph_frac_hbm': round(wx.kv_bytes() / (rx['split_graph_us'] * 1e-6) / 1e9
+                                                         / HBM_PEAK_GBS, 4),
                            'frac_hbm': round(wx.kv_bytes() / (us * 1e-6) / 1e9 / HBM_PEAK_GBS, 4)}
         if 'prefill_2k' in chosen:
             wp = WORKLOADS['prefill_2k']
