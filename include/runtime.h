@@ -125,7 +125,8 @@ int qv_attention_workspace(uint64_t *bytes, int q_heads, int kv_heads, int head_
  * q: [tokens][q_heads][head_dim] of `dtype` (QV_F16 or QV_BF16), like the
  * pages; out: same shape, of `out_dtype` (`dtype`, or QV_F32 as the
  * reference's float output); fp32 softmax and accumulation. head_dim 128 or
- * 256; G <= 48; 1 <= tokens; position+tokens <= capacity. Up to 48 query
+ * 256; G <= 48; 1 <= tokens; q_heads*tokens <= 2^28; position+tokens <=
+ * capacity. Up to 48 query
  * rows per KV head (G*tokens): split-K over all CUs plus a log-sum-exp
  * combine (qv_attention_split then qv_attention_combine). More rows (chunked
  * prefill): one workgroup per 192 rows streams the visible pages through LDS;

@@ -40,6 +40,20 @@ def _ptr(t):
     return ct.c_void_p(t.data_ptr())
 
 
+def _require(condition, message):
+    if not condition:
+        raise ValueError(message)
+
+
+def _same_device(tensors, device):
+    for name, t in tensors:
+        _require(t.device == device, f'{name} is on {t.device}, the cache on {device}')
+
+
+def _nbytes(t):
+    return t.numel() * t.element_size()
+
+
 class PagedKV:
     """K and V caches of one attention layer in the library's page layout:
     per KV head, `capacity` tokens in 32-token pages (include/runtime.h)."""
@@ -55,9 +69,12 @@ class PagedKV:
     def pack(self, k_rows, v_rows, first=0):
         """Write token-major rows [count][kv_heads][head_dim] at tokens first..."""
         lib = library()
+        shape = (self.kv_heads, self.head_dim)
+        _require(k_rows.dim() == 3 and k_rows.shape == v_rows.shape and tuple(k_rows.shape[1:]) == shape,
+                 f'K and V rows must both be [count, {shape[0]}, {shape[1]}]')
+        _same_device([('k_rows', k_rows), ('v_rows', v_rows)], self.k.device)
         k_rows = k_rows.to(self.dtype).contiguous()
         v_rows = v_rows.to(self.dtype).contiguous()
-        assert k_rows.shape == v_rows.shape and k_rows.shape[1:] == (self.kv_heads, self.head_dim)
         check(lib, lib.qv_kv_pack(_ptr(self.k), _ptr(self.v), _ptr(k_rows), _ptr(v_rows),
                                   self.kv_heads, self.head_dim, self.capacity, first,
                                   k_rows.shape[0], _stream()))
@@ -90,35 +107,61 @@ def attention(q, cache, position, scale, out=None, ws=None, out_dtype=None):
     row t sees keys 0..position+t of `cache` (a PagedKV).  The output has
     q's dtype, or float32 when out_dtype (or out's dtype) says so."""
     lib = library()
+    _check_query(q, cache)
     q = q.contiguous()
     tokens, q_heads, head_dim = q.shape
     if out is None:
         out = torch.empty(q.shape, dtype=out_dtype or q.dtype, device=q.device)
+    _check_output(out, q)
     if ws is None:
         ws = workspace(attention_workspace_bytes(q_heads, cache.kv_heads, head_dim, tokens, position), q.device)
+    _same_device([('workspace', ws)], cache.k.device)
     check(lib, lib.qv_attention(_ptr(out), _ptr(q), _ptr(cache.k), _ptr(cache.v), dtype_code(q.dtype),
                                 out_code(out.dtype), q_heads, cache.kv_heads, head_dim, tokens,
-                                position, cache.capacity, float(scale), _ptr(ws), ws.numel(),
+                                position, cache.capacity, float(scale), _ptr(ws), _nbytes(ws),
                                 _stream()))
     return out
+
+
+def _check_query(q, cache):
+    """The query must be [tokens, q_heads, head_dim] of the cache's 16-bit
+    type on the cache's device (the library sees untyped pointers)."""
+    _require(q.dim() == 3, 'q must be [tokens, q_heads, head_dim]')
+    _require(q.dtype == cache.dtype, f'q is {q.dtype}, the cache holds {cache.dtype}')
+    _require(q.shape[2] == cache.head_dim, f'q has head_dim {q.shape[2]}, the cache {cache.head_dim}')
+    _same_device([('q', q)], cache.k.device)
+
+
+def _check_output(out, q):
+    _require(tuple(out.shape) == tuple(q.shape), f'out must have the shape of q, {tuple(q.shape)}')
+    _require(out.dtype in (q.dtype, torch.float32), f'out must be {q.dtype} or float32, not {out.dtype}')
+    _require(out.is_contiguous(), 'out must be contiguous')
+    _same_device([('out', out)], q.device)
 
 
 def attention_split(q, cache, position, scale, ws):
     """Phase 1 of `attention` for one chunk (split-K partials into ws)."""
     lib = library()
+    _check_query(q, cache)
+    q = q.contiguous()
     tokens, q_heads, head_dim = q.shape
+    _same_device([('workspace', ws)], cache.k.device)
     check(lib, lib.qv_attention_split(_ptr(q), _ptr(cache.k), _ptr(cache.v), dtype_code(q.dtype),
                                       q_heads, cache.kv_heads, head_dim, tokens, position,
-                                      cache.capacity, float(scale), _ptr(ws), ws.numel(), _stream()))
+                                      cache.capacity, float(scale), _ptr(ws), _nbytes(ws), _stream()))
 
 
 def attention_combine(out, cache, position, ws):
     """Phase 2 of `attention` for one chunk (log-sum-exp combine into out)."""
     lib = library()
+    _require(out.dim() == 3 and out.shape[2] == cache.head_dim, 'out must be [tokens, q_heads, head_dim]')
+    _require(out.dtype in (cache.dtype, torch.float32), f'out must be {cache.dtype} or float32')
+    _require(out.is_contiguous(), 'out must be contiguous')
+    _same_device([('out', out), ('workspace', ws)], cache.k.device)
     tokens, q_heads, head_dim = out.shape
     check(lib, lib.qv_attention_combine(_ptr(out), dtype_code(cache.dtype), out_code(out.dtype), q_heads,
                                         cache.kv_heads, head_dim, tokens, position, _ptr(ws),
-                                        ws.numel(), _stream()))
+                                        _nbytes(ws), _stream()))
 
 
 def fused_workspace_bytes(batch, position):
@@ -133,13 +176,26 @@ def attention_fused(q_gate, key, value, q_norm, k_norm, cache, position, epsilon
     k_attention): prepares q/k, appends k/v at position.., attends and gates.
     All inputs float32 device tensors; `cache` is an fp16 PagedKV(4, 256, ...)."""
     lib = library()
+    _require((cache.dtype, cache.kv_heads, cache.head_dim) == (torch.float16, 4, 256),
+             'the fused path runs on an fp16 PagedKV(4, 256, ...)')
     batch = q_gate.shape[0]
+    shapes = {'q_gate': (batch, 24, 512), 'key': (batch, 4, 256), 'value': (batch, 4, 256),
+              'q_norm': (256,), 'k_norm': (256,)}
+    named = list(zip(shapes, (q_gate, key, value, q_norm, k_norm)))
+    for name, t in named:
+        _require(t.dtype == torch.float32, f'{name} must be float32, not {t.dtype}')
+        _require(t.numel() == torch.Size(shapes[name]).numel(),
+                 f'{name} must hold {shapes[name]} values, not {tuple(t.shape)}')
+    _same_device(named, cache.k.device)
     if out is None:
         out = torch.empty((batch, 24, 256), dtype=torch.float32, device=q_gate.device)
+    _require(out.dtype == torch.float32 and out.numel() == batch * 24 * 256 and out.is_contiguous(),
+             'out must be a contiguous float32 [batch, 24, 256]')
     if ws is None:
         ws = workspace(fused_workspace_bytes(batch, position), q_gate.device)
-    tensors = [t.contiguous() for t in (q_gate, key, value, q_norm, k_norm)]
+    _same_device([('out', out), ('workspace', ws)], cache.k.device)
+    tensors = [t.contiguous() for _, t in named]
     check(lib, lib.qv_attention_fused(_ptr(out), _ptr(cache.k), _ptr(cache.v),
                                       *[_ptr(t) for t in tensors], batch, position, cache.capacity,
-                                      float(epsilon), _ptr(ws), ws.numel(), _stream()))
+                                      float(epsilon), _ptr(ws), _nbytes(ws), _stream()))
     return out

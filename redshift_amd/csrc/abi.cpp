@@ -99,6 +99,9 @@ rs::Shape attention_shape(int q_heads, int kv_heads, int head_dim, int tokens,
     require(head_dim == 128 || head_dim == 256, "head_dim must be 128 or 256");
     require(tokens >= 1, "tokens must be positive");
     require(position >= 0, "position must be non-negative");
+    // Row counts (q_heads * tokens) and the prefill launch's work-items
+    // (about 4 per row) stay within 32 bits.
+    require((long long)q_heads * tokens <= rs::kMaxQueryRows, "q_heads*tokens exceeds 2^28 query rows");
     return rs::Shape{q_heads, kv_heads, head_dim, tokens, position, capacity};
 }
 

@@ -49,6 +49,8 @@ struct SplitPlan {
 // Largest number of query rows (group * tokens) per KV head that one launch of
 // the split kernel holds; longer token runs are processed in chunks.
 constexpr int kMaxRows = 48;
+// Largest q_heads * tokens of one raw attention call.
+constexpr long long kMaxQueryRows = 1LL << 28;
 
 int device_cu_count();
 SplitPlan plan_split(const Shape &s, int chunk_tokens, Dtype dtype, bool precise);

@@ -468,6 +468,7 @@ void launch_prefill(const Shape &s, Dtype dtype, bool precise, float scale, cons
     require(kernel != nullptr, "unsupported head_dim for the prefill kernel");
     void *args[] = {&a};
     const int threads = (rows / 16) * kWave;
+    require((long long)a.n_tiles * s.kv_heads * threads < (1LL << 32), "prefill launch exceeds 2^32 work-items");
     check(hipLaunchKernel(kernel, dim3(a.n_tiles * s.kv_heads), dim3(threads), args, 0, stream));
 }
 

@@ -144,6 +144,9 @@ def test_device_entry_points_validate_before_touching_the_device(lib):
     assert call(out=None) == -1 and lib.qv_error() == b'null attention buffer'
     assert call(out=ct.c_void_p(4098)) == -1 and b'aligned' in lib.qv_error()
     assert call(dtype=QV_BF16, q_heads=24 * 17, kv_heads=1) == -1 and b'48 query heads' in lib.qv_error()
+    rows = 2 ** 28 // 48 + 1      # q_heads*tokens past 2^28 (32-bit row and launch arithmetic)
+    assert call(q_heads=48, kv_heads=1, tokens=rows, position=0, capacity=-(-rows // 32) * 32) == -1
+    assert b'2^28' in lib.qv_error()
     assert lib.qv_kv_pack(p, p, p, p, 4, 256, 128, 100, 29, None) == -1
     assert b'capacity' in lib.qv_error()
     assert lib.qv_kv_pack(p, None, None, p, 4, 256, 128, 0, 1, None) == -1
@@ -164,3 +167,31 @@ def test_device_entry_points_validate_before_touching_the_device(lib):
     assert b'capacity' in lib.qv_error()
     assert lib.qv_attention_fused(*([p] * 8), 100, 139200, 139264, 1e-6, p, ws, None) == -1
     assert b'139264' in lib.qv_error()
+
+
+def test_front_end_rejects_mismatched_tensors(lib):
+    """The torch front end checks what the untyped C ABI cannot see (dtype,
+    shape and device of every tensor) before any library call."""
+    import torch
+    import redshift_amd.attention as A
+    cache = A.PagedKV(4, 256, 64, torch.float16, device='cpu')
+    q = torch.zeros((1, 24, 256), dtype=torch.float16)
+    with pytest.raises(ValueError, match='the cache holds'):
+        A.attention(q.to(torch.bfloat16), cache, 0, 1 / 16)
+    with pytest.raises(ValueError, match='head_dim'):
+        A.attention(torch.zeros((1, 24, 128), dtype=torch.float16), cache, 0, 1 / 16)
+    with pytest.raises(ValueError, match=r'\[tokens, q_heads, head_dim\]'):
+        A.attention(torch.zeros((24, 256), dtype=torch.float16), cache, 0, 1 / 16)
+    with pytest.raises(ValueError, match='shape of q'):
+        A.attention(q, cache, 0, 1 / 16, out=torch.zeros((2, 24, 256), dtype=torch.float16))
+    with pytest.raises(ValueError, match='or float32'):
+        A.attention(q, cache, 0, 1 / 16, out=torch.zeros((1, 24, 256), dtype=torch.bfloat16))
+    with pytest.raises(ValueError, match='K and V rows'):
+        cache.pack(torch.zeros((2, 4, 256)), torch.zeros((3, 4, 256)))
+    with pytest.raises(ValueError, match='fp16 PagedKV'):
+        A.attention_fused(*([None] * 5), A.PagedKV(4, 256, 64, torch.bfloat16, device='cpu'), 0, 1e-6)
+    inputs = [torch.zeros(s) for s in ((1, 24, 512), (1, 4, 256), (1, 4, 256), (256,), (256,))]
+    with pytest.raises(ValueError, match='q_gate must be float32'):
+        A.attention_fused(inputs[0].half(), *inputs[1:], cache, 0, 1e-6)
+    with pytest.raises(ValueError, match='value must hold'):
+        A.attention_fused(*inputs[:2], torch.zeros((2, 4, 256)), *inputs[3:], cache, 0, 1e-6)
