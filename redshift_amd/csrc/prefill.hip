@@ -5,10 +5,10 @@
 // token runs: row t sees keys 0..position+t.
 //
 // One workgroup owns 192 query rows of one KV head (row = token * group +
-// query head within the group): 128 from the end of the chunk and 64 from
-// its start, so that every workgroup has about the same number of (row, key)
-// pairs.  Each wave owns one 16-row tile (twelve waves: three per SIMD)
-// whose query fragments stay in registers.  The workgroup walks the pages
+// query head within the group) as twelve 16-row tiles, one per wave (three
+// per SIMD), whose query fragments stay in registers.  The tiles are dealt
+// out so that every SIMD has about the same number of (row, key) pairs (see
+// the kernel).  The workgroup walks the pages
 // that its last row can see through two rings of four LDS buffers, one for
 // K pages and one for V pages (16 KiB each at D=256), filled by direct
 // global->LDS loads three pages ahead.  Since pages are stored in MFMA
@@ -114,13 +114,9 @@ void attention_prefill(PrefillArgs a) {
     constexpr int KS = D / 32, DT = D / 16;
     constexpr int PAGE = 32 * D;                       // elements of one K (or V) page
     constexpr int PAGE_BYTES = PAGE * 2;
-    // Row pieces: the first L waves ("late" waves, two per SIMD of twelve,
-    // one per SIMD of eight) take LR rows from the end of the chunk, the
-    // others ER rows from its start (see below).  The late waves copy the
-    // pages, H 1 KiB loads each per K (or V) page.
-    constexpr int L = kPWaves == 12 ? 8 : kPWaves / 2;
-    constexpr int LR = 16 * L, ER = ROWS - LR;
-    constexpr int kLoaders = L;
+    // The first kLoaders waves (two per SIMD of twelve, one per SIMD of
+    // eight) copy the pages, H 1 KiB loads each per K (or V) page.
+    constexpr int kLoaders = kPWaves == 12 ? 8 : kPWaves / 2;
     constexpr int H = PAGE_BYTES / 1024 / kLoaders;
     static_assert(H >= 1 && PAGE_BYTES / 1024 % kLoaders == 0, "loads divide over the loader waves");
     __shared__ __attribute__((aligned(16))) KV kring[4 * PAGE];
@@ -129,19 +125,25 @@ void attention_prefill(PrefillArgs a) {
     const int lane = threadIdx.x & 63, g = lane >> 4;
     const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);   // wave index (uniform)
     const int h = blockIdx.x % a.kv_heads;
-    // Load balance: workgroup j of a KV head owns the late piece j, rows
-    // [R - LR(j+1), R - LR j), and the early piece j, rows [ER j, ER j + ER)
-    // below B = R - LR n_tiles (the late pieces cover [B, R)).  A late row
-    // sees more keys than an early one, and the pieces are paired so that
-    // every workgroup has about the same work: all waves run until the early
-    // piece's last page, then the late waves alone (at two thirds of the
-    // per-page cost) until the late piece's.  Rows outside [0, R) (and
-    // early rows from B on) are padding.
+    // Load balance.  The R rows of a KV head form T = ceil(R/16) tiles of 16
+    // rows; a later tile sees more keys.  Wave w of workgroup j runs on SIMD
+    // w % 4 and serves slot k = 4j + w%4 (K = 4 n_tiles slots per head) in
+    // round w / 4, which deals the tiles out serpentine-wise:
+    //   round 0: tile T-1-k    (the last K tiles, the latest first)
+    //   round 1: tile T-2K+k   (the K before them, in rising order)
+    //   round 2: tile T-3K+k   (the rest, rising)
+    // Rounds 0 and 1 give every slot the same key count; round 2 rises with
+    // k, while the stretch in which only the round-0 wave still has pages
+    // shrinks with k.  So every SIMD, and every workgroup, has about the
+    // same work.  Negative tiles are padding, and rows from R on are not
+    // stored.  Workgroup j's last row lies in its round-0 tile of slot 4j.
     const int R = a.rows;
     const int j = blockIdx.x / a.kv_heads;
-    const bool late = w < L;
-    const int row0 = late ? R - LR * (j + 1) + 16 * w : ER * j + 16 * (w - L);
-    const int row_end = late ? R : max(R - LR * a.n_tiles, 0);     // valid rows: [0, row_end)
+    static_assert(kPWaves % 4 == 0 && kPWaves / 4 <= 3, "one to three rounds of four waves");
+    const int T = (R + 15) / 16, K = 4 * a.n_tiles, slot = 4 * j + (w & 3), round = w >> 2;
+    const int tile = round == 0 ? T - 1 - slot : round == 1 ? T - 2 * K + slot : T - 3 * K + slot;
+    const int row0 = 16 * tile;
+    const int row_end = R;                                              // valid rows: [0, row_end)
 
     // Query fragments (B operand): k-step ks of lane l holds row row0 + l%16,
     // dims 32*ks + 8*(l/16) .. +7.  Padded rows load a valid row; their
@@ -166,8 +168,8 @@ void attention_prefill(PrefillArgs a) {
     }
     wait_vmcnt<0>();
     // Keys this workgroup can see: 0 .. position + (token of its last row,
-    // the late piece's last, which is valid).
-    const int n_keys = a.position + (R - LR * j - 1) / a.group + 1;
+    // the last valid row of tile T-1-4j).
+    const int n_keys = a.position + (min(16 * (T - 4 * j), R) - 1) / a.group + 1;
     const int n = (n_keys + 31) / 32;
     // Pages of this wave: those its last valid row sees (none without one).
     const int wave_last = min(row0 + 15, row_end - 1);
