@@ -17,12 +17,14 @@ enum { kOutSame = 0, kOutF32 = 1, kOutGated = 2 };
 // barrier).  Lane l owns head dims DV*l .. DV*l+DV-1 (DV = D/64);
 // wave w4 takes splits w4, w4+4, ... and issues the loads of up to kBatch of
 // them (their m, l and partial row) at once, so a combine over up to
-// 4*kBatch splits costs one memory round trip (non-temporal: each partial
-// row is read once).  The waves then merge through `scratch` (4*(D+1) + 4
-// floats of LDS per group), each thread one head dim.  PT is the type of the
-// partial rows: float (unnormalised O) or _Float16 (O / l, weighted by l
-// here).
-template <int D, typename KV, typename PT>
+// 4*kBatch splits costs one memory round trip.  The waves then merge through
+// `scratch` (4*(D+1) + 4 floats of LDS per group), each thread one head dim.
+// PT is the type of the partial rows: float (unnormalised O) or _Float16
+// (O / l, weighted by l here).  NT: the partial rows are loaded
+// non-temporally, matching partials that were stored that way (the load
+// policy of the combine follows the store policy of the split kernel: the
+// mixed pairs measured slower).
+template <int D, typename KV, typename PT, bool NT>
 __device__ __forceinline__ void combine_row(const PT *part_o, const float *part_ml, int splits,
                                             int rows, int group, int q_heads, int row, int h,
                                             bool valid, int w4, int lane, float *scratch,
@@ -60,7 +62,11 @@ __device__ __forceinline__ void combine_row(const PT *part_o, const float *part_
             const int sc = min(s0 + w4 + 4 * i, splits - 1);
             mv[i] = ml[(size_t)sc * 2 * rows];
             lv[i] = ml[(size_t)sc * 2 * rows + rows];
-            ov[i] = __builtin_nontemporal_load(reinterpret_cast<const OV *>(po + (size_t)sc * stride));
+            const OV *src = reinterpret_cast<const OV *>(po + (size_t)sc * stride);
+            if constexpr (NT)
+                ov[i] = __builtin_nontemporal_load(src);
+            else
+                ov[i] = *src;
         }
 #pragma unroll
         for (int i = 0; i < kBatch; ++i) {
