@@ -427,7 +427,10 @@ def main():
             extra[name] = {'us_per_layer': round(us, 2),
                            'GB/s': round(wf.kv_bytes() / (us * 1e-6) / 1e9, 1),
                            'frac_hbm': round(wf.kv_bytes() / (us * 1e-6) / 1e9 / HBM_PEAK_GBS, 4),
-                           'what': 'qv_attention_fused per layer: prepare + append + attention + gate'}
+                           'what': 'qv_attention_fused per layer: prepare + append + attention + gate'
+                                   + (' (one token: query prepared in the split kernel, key and value '
+                                      'prepared, attended and appended in the combine; two launches)'
+                                      if wf.tokens == 1 else '')}
         if 'fused_prefill_2k' in chosen:
             # The fused drop-in on a 2048-token prefill chunk at position 6144
             # (fp16 pages, the model's fp32 q_gate/key/value), one call per layer.

@@ -5,6 +5,7 @@
 // thread-local message; qv_error() returns "" after a success.
 #include "runtime.h"
 
+#include <algorithm>
 #include <cmath>
 #include <cstdio>
 #include <cstring>
@@ -141,15 +142,32 @@ void run_attention(const rs::Shape &s, rs::Dtype dtype, bool precise, float scal
     }
 }
 
-// The reference's k_attention on device buffers of the 24/4/256 model:
-// the prepare kernel writes the query's hi + lo parts to q_hilo (2 * batch *
-// 24 * 256 fp16) and appends the new K/V to the pages, then attention (with
-// the sigmoid gate) runs on them.
+// The reference's k_attention on device buffers of the 24/4/256 model.  One
+// token after at least one cached key (decode): two launches, the split
+// kernel preparing the query itself and the combine adding and appending
+// the new key.  Otherwise the prepare kernel writes the query's hi + lo
+// parts to q_hilo (2 * batch * 24 * 256 fp16) and appends the new K/V to
+// the pages, then attention (with the sigmoid gate) runs on them.
 void fused_attention(float *out, void *k_pages, void *v_pages, const float *q_gate, const float *key,
                      const float *value, const float *q_norm, const float *k_norm, int batch,
                      int position, int capacity, float epsilon, uint16_t *q_hilo, void *partials,
                      hipStream_t stream) {
     constexpr int H = rs::kModelQHeads, HKV = rs::kModelKvHeads, D = rs::kModelHeadDim;
+    if (batch == 1 && position >= 1) {
+        rs::FusedToken tok;
+        tok.q_gate = q_gate;
+        tok.key = key;
+        tok.value = value;
+        tok.q_norm = q_norm;
+        tok.k_norm = k_norm;
+        tok.k_pages = k_pages;
+        tok.v_pages = v_pages;
+        tok.head_stride = (size_t)capacity * D;
+        tok.epsilon = epsilon;
+        tok.position = position;
+        rs::launch_fused_decode(tok, capacity, partials, out, stream);
+        return;
+    }
     const rs::Shape s{H, HKV, D, batch, position, capacity};
     rs::launch_prepare(q_hilo, k_pages, v_pages, q_gate, key, value, q_norm, k_norm, batch, position,
                        capacity, epsilon, stream);
@@ -398,10 +416,14 @@ extern "C" int qv_attention_combine(void *out, int dtype, int out_dtype, int q_h
     });
 }
 
+// The query's hi + lo parts, then the partials; a fused decode uses only the
+// partials region (no larger than the prepared path's).
 static size_t fused_workspace(int batch, int position) {
     constexpr int H = rs::kModelQHeads, HKV = rs::kModelKvHeads, D = rs::kModelHeadDim;
     const rs::Shape s{H, HKV, D, batch, position, 0};
-    return align256((size_t)batch * H * D * sizeof(float)) + rs::attention_workspace_bytes(s, rs::Dtype::F16, true);
+    size_t parts = rs::attention_workspace_bytes(s, rs::Dtype::F16, true);
+    if (batch == 1 && position >= 1) parts = std::max(parts, rs::fused_decode_workspace_bytes(position));
+    return align256((size_t)batch * H * D * sizeof(float)) + parts;
 }
 
 extern "C" int qv_attention_fused_workspace(uint64_t *bytes, int batch, int position) {

@@ -27,6 +27,7 @@
 //                     replicated.
 #include "combine.hpp"
 #include "kernels.hpp"
+#include "prep.hpp"
 
 #include <algorithm>
 #include <cmath>
@@ -122,12 +123,20 @@ __device__ __forceinline__ int v_slot_token(int g, int j) {
 // way: that pair takes 0.5 us less per decode layer than non-temporal
 // stores and loads.
 // ---------------------------------------------------------------------------
-template <int D, bool QSPLIT, bool PSPLIT, typename KV>
+//
+// PREP (the fused decode of one new token): the query is not read from q but
+// prepared here from a.tok (RMSNorm, gamma, RoPE at a.tok.position, hi + lo
+// fp16 parts; the same functions as the prepare kernel, so the same bits).
+// Wave w prepares the group's rows w and w + 4 while the first K page is in
+// flight, and writes them into the fragment slots of the LDS hand-over.
+template <int D, bool QSPLIT, bool PSPLIT, typename KV, bool PREP>
 __global__ __launch_bounds__(kWaves * kWave)
 void attention_stream(SplitArgs a) {
     using V8 = typename Vec8<KV>::type;
     using QS = QueryStage<D, 1, QSPLIT, KV>;
     constexpr int KS = D / 32, DT = D / 16, NQ = QSPLIT ? 2 : 1;
+    static_assert(!PREP || (D == 4 * kWave && QSPLIT && std::is_same<KV, _Float16>::value),
+                  "the prepared query is the fp32 query of the 256-dim fp16 model, as hi + lo parts");
     __shared__ f32x4 so[kWaves][DT * kWave];   // merge slots, one per wave
     __shared__ V8 sq[QS::N * kWave];       // query fragments
     __shared__ float sml[kWaves][2][16];
@@ -135,7 +144,20 @@ void attention_stream(SplitArgs a) {
     const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
     const int split = blockIdx.x % a.splits, h = blockIdx.x / a.splits;
     QS qs;
-    qs.issue(a, h, lane, w);
+    float xq[2][4], gq[4];   // PREP: rows w and w + 4, lane l holding dims 64i + l
+    if constexpr (PREP) {
+#pragma unroll
+        for (int r = 0; r < 2; ++r) {
+            const int row = min(w + 4 * r, a.rows - 1);
+            const float *src = a.tok.q_gate + (size_t)(h * a.group + row) * 2 * D;
+#pragma unroll
+            for (int i = 0; i < 4; ++i) xq[r][i] = src[64 * i + lane];
+        }
+#pragma unroll
+        for (int i = 0; i < 4; ++i) gq[i] = a.tok.q_norm[64 * i + lane];
+    } else {
+        qs.issue(a, h, lane, w);
+    }
 
     // Pages are dealt out round-robin over the waves of all splits of this
     // head: step j of wave wi is page j*waves_total + wi, so waves running in
@@ -243,9 +265,53 @@ void attention_stream(SplitArgs a) {
     // The first K load is unconditional (a wave without pages re-reads the
     // head's last page), so every wave issues it before waiting on the query.
     load_k(min(wi, a.n_pages - 1));
-    qs.publish(sq, lane, w);
+    // PREP: the prepared rows are staged in LDS as fp32, row-major with a
+    // stride of D + 4 floats (the fragment slots' LDS, unused here), so the
+    // writes (lane l: dims 64i + l) and the fragment reads (16 rows, 32 bytes
+    // each) are both free of bank conflicts; hi and lo parts are split while
+    // gathering.
+    constexpr int kStage = D + 4;
+    static_assert(!PREP || 8 * kStage * sizeof(float) <= sizeof(sq), "the staged rows fit the fragment slots");
+    float *stage = reinterpret_cast<float *>(sq);
+    if constexpr (PREP) {
+        float c = 1.f, sn = 0.f;
+        if (lane < 32) rope_cos_sin(a.tok.position, rope_freq(lane), c, sn);
+        const float cr[2] = {c, c}, sr[2] = {sn, sn};
+        norm_rope_rows<2>(xq, gq, cr, sr, a.tok.epsilon, lane);
+#pragma unroll
+        for (int r = 0; r < 2; ++r) {
+            const int row = w + 4 * r;
+            if (row < a.rows) {
+#pragma unroll
+                for (int i = 0; i < 4; ++i) stage[row * kStage + 64 * i + lane] = xq[r][i];
+            }
+        }
+    } else {
+        qs.publish(sq, lane, w);
+    }
     lds_barrier();
-    QS::gather(sq, lane, qf1);
+    if constexpr (PREP) {
+        // Fragment ks of lane l: row l%16, dims 32ks + 8(l/16) .. +7, as
+        // hi = fp16(q) and lo = fp16(q - hi).  Rows past the group are zero
+        // (their results are never stored).
+        const int row = lane & 15;
+        const bool live = row < a.rows;
+#pragma unroll
+        for (int ks = 0; ks < KS; ++ks) {
+            const float *src = stage + row * kStage + 32 * ks + 8 * (lane >> 4);
+            const f32x4 lo4 = live ? *reinterpret_cast<const f32x4 *>(src) : f32x4{0.f, 0.f, 0.f, 0.f};
+            const f32x4 hi4 = live ? *reinterpret_cast<const f32x4 *>(src + 4) : f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+            for (int j = 0; j < 8; ++j) {
+                const float x = j < 4 ? lo4[j] : hi4[j - 4];
+                const _Float16 hi = (_Float16)x;
+                qf1[0][0][ks][j] = hi;
+                qf1[NQ - 1][0][ks][j] = (_Float16)(x - (float)hi);
+            }
+        }
+    } else {
+        QS::gather(sq, lane, qf1);
+    }
     if (n_steps > 0) {
         for (int j = 0; j + 1 < n_steps; ++j) page(j * waves_total + wi, std::true_type{});
         page((n_steps - 1) * waves_total + wi, std::false_type{});
@@ -555,16 +621,18 @@ struct CombineArgs {
     void *out;
     const float *gate;   // gated output: q_gate rows of 2*D floats, gate at +D
     int q_heads, group, rows, splits;
+    float scale_log2;     // NEWKEY: the new key's score scale
+    FusedToken tok;       // NEWKEY: the new token
 };
 
 // Standalone combine: one workgroup (4 waves) per (row, KV head).
-template <int D, typename KV, int OUT, typename PT, bool NT>
+template <int D, typename KV, int OUT, typename PT, bool NT, bool NEWKEY>
 __global__ __launch_bounds__(kWaves * kWave)
 void attention_combine(CombineArgs c) {
     __shared__ float scratch[4 * (D + 1) + 4];
-    combine_row<D, KV, PT, NT>(static_cast<const PT *>(c.part_o), c.part_ml, c.splits, c.rows, c.group, c.q_heads,
-                           blockIdx.x, blockIdx.y, true, threadIdx.x >> 6, threadIdx.x & 63, scratch, c.out,
-                           c.gate, OUT);
+    combine_row<D, KV, PT, NT, NEWKEY>(static_cast<const PT *>(c.part_o), c.part_ml, c.splits, c.rows, c.group,
+                                       c.q_heads, blockIdx.x, blockIdx.y, true, threadIdx.x >> 6, threadIdx.x & 63,
+                                       scratch, c.out, c.gate, OUT, &c.tok, c.scale_log2);
 }
 
 // Kernel instance for a plan.  Raw fp16: 16-bit P; raw bf16: hi+lo P (bf16's
@@ -573,9 +641,9 @@ void attention_combine(CombineArgs c) {
 template <int D, int NQT>
 const void *pick(bool stream, Dtype dtype, bool precise) {
     if (stream) {
-        if (precise) return (const void *)&attention_stream<D, true, true, _Float16>;
-        if (dtype == Dtype::BF16) return (const void *)&attention_stream<D, false, true, __bf16>;
-        return (const void *)&attention_stream<D, false, false, _Float16>;
+        if (precise) return (const void *)&attention_stream<D, true, true, _Float16, false>;
+        if (dtype == Dtype::BF16) return (const void *)&attention_stream<D, false, true, __bf16, false>;
+        return (const void *)&attention_stream<D, false, false, _Float16, false>;
     }
     if (precise) return (const void *)&attention_coop<D, NQT, true, true, _Float16, kCoopWaves>;
     if (dtype == Dtype::BF16) return (const void *)&attention_coop<D, NQT, false, true, __bf16, kCoopWaves>;
@@ -584,10 +652,10 @@ const void *pick(bool stream, Dtype dtype, bool precise) {
 
 template <int D, typename PT, bool NT>
 const void *combine_kernel(Dtype dtype, bool out_f32, bool gated) {
-    if (gated) return (const void *)&attention_combine<D, _Float16, kOutGated, PT, NT>;
-    if (out_f32) return (const void *)&attention_combine<D, _Float16, kOutF32, PT, NT>;
-    return dtype == Dtype::BF16 ? (const void *)&attention_combine<D, __bf16, kOutSame, PT, NT>
-                                : (const void *)&attention_combine<D, _Float16, kOutSame, PT, NT>;
+    if (gated) return (const void *)&attention_combine<D, _Float16, kOutGated, PT, NT, false>;
+    if (out_f32) return (const void *)&attention_combine<D, _Float16, kOutF32, PT, NT, false>;
+    return dtype == Dtype::BF16 ? (const void *)&attention_combine<D, __bf16, kOutSame, PT, NT, false>
+                                : (const void *)&attention_combine<D, _Float16, kOutSame, PT, NT, false>;
 }
 
 // fp16 partial rows come only from the ring kernel, which stores them
@@ -790,6 +858,64 @@ void launch_combine(const Shape &s, const SplitPlan &plan, Dtype dtype,
     require(kernel != nullptr, "unsupported head_dim for the combine kernel");
     void *args[] = {&c};
     check(hipLaunchKernel(kernel, grid, dim3(kWaves * kWave), args, 0, stream));
+}
+
+namespace {
+// The cached keys 0 .. position-1 as seen by the fused decode's one token
+// (its row sees every one of them), for the model's geometry.
+Shape fused_decode_shape(int position, int capacity) {
+    return Shape{kModelQHeads, kModelKvHeads, kModelHeadDim, 1, position - 1, capacity};
+}
+}  // namespace
+
+size_t fused_decode_workspace_bytes(int position) {
+    const Shape s = fused_decode_shape(position, 0);
+    return plan_bytes(s, plan_split(s, 1, Dtype::F16, true));
+}
+
+void launch_fused_decode(const FusedToken &tok, int capacity, void *workspace, float *out, hipStream_t stream) {
+    constexpr int D = kModelHeadDim;
+    require(tok.position >= 1, "the fused decode needs at least one cached key");
+    const Shape s = fused_decode_shape(tok.position, capacity);
+    const SplitPlan plan = plan_split(s, 1, Dtype::F16, true);
+    require(plan.kind == SplitKind::Stream && plan.rows <= 8 && !plan.half_parts && plan.splits >= 1,
+            "the fused decode runs the stream kernel on at most 8 rows");
+    constexpr float kScaleLog2 = (1.0f / 16.0f) * 1.4426950408889634f;
+
+    SplitArgs a = {};
+    a.k_pages = tok.k_pages;
+    a.v_pages = tok.v_pages;
+    a.part_o = static_cast<float *>(workspace);
+    a.part_ml = a.part_o + (size_t)s.kv_heads * plan.splits * plan.rows * D;
+    a.head_stride = tok.head_stride;
+    a.q_heads = s.q_heads;
+    a.kv_heads = s.kv_heads;
+    a.group = s.group();
+    a.rows = plan.rows;
+    a.position = s.position;
+    a.n_keys = tok.position;
+    a.n_pages = plan.n_pages;
+    a.splits = plan.splits;
+    a.scale_log2 = kScaleLog2;
+    a.tok = tok;
+    void *split_args[] = {&a};
+    check(hipLaunchKernel((const void *)&attention_stream<D, true, true, _Float16, true>,
+                          dim3(plan.splits * s.kv_heads), dim3(kWaves * kWave), split_args, 0, stream));
+
+    CombineArgs c = {};
+    c.part_o = workspace;
+    c.part_ml = a.part_ml;
+    c.out = out;
+    c.gate = tok.q_gate;
+    c.q_heads = s.q_heads;
+    c.group = s.group();
+    c.rows = plan.rows;
+    c.splits = plan.splits;
+    c.scale_log2 = kScaleLog2;
+    c.tok = tok;
+    void *combine_args[] = {&c};
+    check(hipLaunchKernel((const void *)&attention_combine<D, _Float16, kOutGated, float, false, true>,
+                          dim3(plan.rows, s.kv_heads), dim3(kWaves * kWave), combine_args, 0, stream));
 }
 
 }  // namespace rs

@@ -2,6 +2,7 @@
 // kernel).
 #pragma once
 #include "kernels.hpp"
+#include "prep.hpp"
 
 #include <cmath>
 #include <type_traits>
@@ -24,11 +25,19 @@ enum { kOutSame = 0, kOutF32 = 1, kOutGated = 2 };
 // non-temporally, matching partials that were stored that way (the load
 // policy of the combine follows the store policy of the split kernel: the
 // mixed pairs measured slower).
-template <int D, typename KV, typename PT, bool NT>
+//
+// NEWKEY (fused decode, one token): the splits cover the cached keys only.
+// Wave 0 prepares the new token's query row and its KV head's key (RMSNorm,
+// gamma, RoPE: the prepare kernel's functions, so the same bits) and value,
+// and folds that key in as one more split: score q . fp16(k), weight 1 at
+// its own max, value fp16(v), the cache's rounding.  Row 0 of the head also
+// appends fp16(k) and fp16(v) to the pages at tok->position.
+template <int D, typename KV, typename PT, bool NT, bool NEWKEY = false>
 __device__ __forceinline__ void combine_row(const PT *part_o, const float *part_ml, int splits,
                                             int rows, int group, int q_heads, int row, int h,
                                             bool valid, int w4, int lane, float *scratch,
-                                            void *out, const float *gate, int out_mode) {
+                                            void *out, const float *gate, int out_mode,
+                                            const FusedToken *tok = nullptr, float scale_log2 = 0.f) {
     constexpr int DV = D / kWave;
     constexpr int kBatch = 16;
     float *part = scratch;                   // [4][D + 1]
@@ -49,6 +58,27 @@ __device__ __forceinline__ void combine_row(const PT *part_o, const float *part_
         gv = gate[((size_t)t * q_heads + hq) * 2 * D + D + jd];
 
     float M = -INFINITY, L = 0.f, acc[DV] = {};
+    // NEWKEY: the new token's inputs, requested with the partials (wave 0).
+    float xq[1][4], xk[1][4], gq[4], gk[4], vn[DV], m_new = -INFINITY;
+    _Float16 kh[4], vh[DV];
+    if constexpr (NEWKEY) {
+        static_assert(D == 4 * kWave && DV == 4, "the fused model's 256-dim heads");
+        if (w4 == 0) {
+            const float *qsrc = tok->q_gate + ((size_t)t * q_heads + hq) * 2 * D;
+            const float *ksrc = tok->key + (size_t)h * D;
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                xq[0][i] = qsrc[64 * i + lane];
+                xk[0][i] = ksrc[64 * i + lane];
+                gq[i] = tok->q_norm[64 * i + lane];
+                gk[i] = tok->k_norm[64 * i + lane];
+            }
+            // Scalar loads: the fused entry does not require `value` to be
+            // 16-byte aligned.
+#pragma unroll
+            for (int d = 0; d < DV; ++d) vn[d] = tok->value[(size_t)h * D + lane * DV + d];
+        }
+    }
     // Rounds of 4*kBatch splits (one round for up to 64 splits).
     for (int s0 = 0; s0 < splits; s0 += 4 * kBatch) {
         // Every load is issued unconditionally (splits past the end re-read
@@ -67,6 +97,26 @@ __device__ __forceinline__ void combine_row(const PT *part_o, const float *part_
                 ov[i] = __builtin_nontemporal_load(src);
             else
                 ov[i] = *src;
+        }
+        if constexpr (NEWKEY) {
+            // Round 0, wave 0: the new key is prepared while this round's
+            // partial loads are in flight (its inputs were requested first).
+            if (s0 == 0 && w4 == 0) {
+                float c = 1.f, sn = 0.f;
+                if (lane < 32) rope_cos_sin(tok->position, rope_freq(lane), c, sn);
+                const float cr[1] = {c}, sr[1] = {sn};
+                norm_rope_rows<1>(xq, gq, cr, sr, tok->epsilon, lane);
+                norm_rope_rows<1>(xk, gk, cr, sr, tok->epsilon, lane);
+                float dot = 0.f;
+#pragma unroll
+                for (int i = 0; i < 4; ++i) {
+                    kh[i] = (_Float16)xk[0][i];
+                    dot += xq[0][i] * (float)kh[i];
+                }
+                m_new = wave_sum_dpp(dot) * scale_log2;
+#pragma unroll
+                for (int d = 0; d < DV; ++d) vh[d] = (_Float16)vn[d];
+            }
         }
 #pragma unroll
         for (int i = 0; i < kBatch; ++i) {
@@ -94,6 +144,25 @@ __device__ __forceinline__ void combine_row(const PT *part_o, const float *part_
             for (int d = 0; d < DV; ++d) acc[d] += wo * (float)ov[i][d];
         }
         M = rm;
+    }
+    if constexpr (NEWKEY) {
+        if (w4 == 0) {
+            // The new key as one more split: weight 1 at its own max.
+            const float rm = fmaxf(M, m_new);
+            const float f = __builtin_amdgcn_exp2f(M - rm), e = __builtin_amdgcn_exp2f(m_new - rm);
+            L = L * f + e;
+#pragma unroll
+            for (int d = 0; d < DV; ++d) acc[d] = acc[d] * f + e * (float)vh[d];
+            M = rm;
+            if (valid && row == 0) {
+                _Float16 *kp = static_cast<_Float16 *>(tok->k_pages) + (size_t)h * tok->head_stride;
+                _Float16 *vp = static_cast<_Float16 *>(tok->v_pages) + (size_t)h * tok->head_stride;
+#pragma unroll
+                for (int i = 0; i < 4; ++i) kp[k_page_offset(tok->position, 64 * i + lane, D)] = kh[i];
+#pragma unroll
+                for (int d = 0; d < DV; ++d) vp[v_page_offset(tok->position, lane * DV + d, D)] = vh[d];
+            }
+        }
     }
     // One barrier: every wave leaves its (M, L) and its unscaled
     // accumulators in its slot; then thread j of the workgroup merges head

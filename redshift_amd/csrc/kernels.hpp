@@ -17,6 +17,23 @@ struct Shape {
 
 enum class SplitKind { Stream, Coop, Ring };
 
+// The new token of a fused decode call (the reference's attn_prepare inputs
+// for one token of the 24/4/256 model): the split kernel prepares the query
+// from it, and the combine kernel prepares its key and value, attends to
+// them as the last key and appends them to the pages.
+struct FusedToken {
+    const float *q_gate;   // [q_heads][2D]: q, then the gate
+    const float *key;      // [kv_heads][D]
+    const float *value;    // [kv_heads][D]
+    const float *q_norm;   // [D]
+    const float *k_norm;   // [D]
+    void *k_pages;
+    void *v_pages;
+    size_t head_stride;
+    float epsilon;
+    int position;          // the token's position: RoPE angle and page slot
+};
+
 // Arguments of every split-K partial kernel.
 struct SplitArgs {
     const void *q;        // [tokens][q_heads][D] 16-bit (hi part when QSPLIT)
@@ -28,6 +45,7 @@ struct SplitArgs {
     size_t head_stride;
     int q_heads, kv_heads, group, rows, position, n_keys, n_pages, splits;
     float scale_log2;
+    FusedToken tok;       // the fused decode instance's query source
 };
 
 // attention_ring instance (ring.hip) for head_dim D and nqt query tiles
@@ -75,6 +93,15 @@ void launch_split(const Shape &s, const SplitPlan &plan, Dtype dtype, bool preci
 void launch_combine(const Shape &s, const SplitPlan &plan, Dtype dtype,
                     const void *workspace, void *out, bool out_f32, const float *gate,
                     hipStream_t stream);
+
+// Fused decode of one new token at tok.position >= 1 (24/4/256, fp16 pages):
+// the split kernel prepares the query itself and attends to the cached keys
+// 0 .. position-1; the combine prepares the new key and value, adds them as
+// the last key, appends them to the pages and applies the gate.  No prepare
+// launch.  The workspace holds the partials of plan_split for the shape with
+// position-1 and one token.
+void launch_fused_decode(const FusedToken &tok, int capacity, void *workspace, float *out, hipStream_t stream);
+size_t fused_decode_workspace_bytes(int position);
 
 // Chunked prefill: all group*tokens query rows against the pages in one
 // launch (no workspace); `dtype` q and out, [tokens][q_heads][D].  A precise

@@ -101,6 +101,44 @@ def test_attention_long_context_against_closed_form(lib, gpu, position, batch):
     np.testing.assert_array_equal(vc[:n].view(np.uint16), c['value_cache'].reshape(-1).view(np.uint16))
 
 
+@pytest.mark.parametrize('position', [0, 1, 31, 32, 33, 1000])
+def test_fused_decode_matches_oracle(gpu, position):
+    """One token through the device fused entry: from position 1 on, the
+    split kernel prepares the query itself and the combine adds, and
+    appends, the new key (no prepare launch); position 0 has no cached key
+    and takes the prepared path.  Against the oracle on the reference's
+    sine-wave fixture and tolerances; the appended rows must equal the
+    prepare kernel's bit for bit (same functions), checked through a batch
+    of two that ends at the same token."""
+    torch = gpu
+    c = kat.sine_wave_case(batch=2, position=position)
+    one = {k: (c[k][:1] if k in ('q_gate', 'key', 'value') else c[k]) for k in c}
+    expected = ref.fused_attention(one['key_cache'], one['value_cache'], one['q_gate'], one['key'], one['value'],
+                                   one['q_norm'], one['k_norm'], 1, position, c['epsilon'])
+    capacity = A.round_capacity(position + 2)
+    cache = A.PagedKV(4, 256, capacity, torch.float16)
+    if position:
+        cache.pack(torch.from_numpy(c['key_cache']).cuda(), torch.from_numpy(c['value_cache']).cuda())
+    dev = [torch.from_numpy(f32(one[name])).cuda() for name in ('q_gate', 'key', 'value', 'q_norm', 'k_norm')]
+    out = A.attention_fused(*dev, cache, position, c['epsilon'])
+    kc, vc = cache.unpack(0, position + 1)
+    torch.cuda.synchronize()
+    assert_close(out.cpu().numpy(), expected[0], 3e-4)
+    assert_close(kc.float().cpu().numpy(), expected[1], 2e-3)
+    assert_close(vc.float().cpu().numpy(), expected[2], 0)
+    # The prepared path (a batch of two) appends the same bits for token 0.
+    cache2 = A.PagedKV(4, 256, capacity, torch.float16)
+    if position:
+        cache2.pack(torch.from_numpy(c['key_cache']).cuda(), torch.from_numpy(c['value_cache']).cuda())
+    dev2 = [torch.from_numpy(f32(c[name])).cuda() for name in ('q_gate', 'key', 'value', 'q_norm', 'k_norm')]
+    out2 = A.attention_fused(*dev2, cache2, position, c['epsilon'])
+    kc2, vc2 = cache2.unpack(0, position + 1)
+    torch.cuda.synchronize()
+    np.testing.assert_array_equal(kc.cpu().numpy().view(np.uint16), kc2.cpu().numpy().view(np.uint16))
+    np.testing.assert_array_equal(vc.cpu().numpy().view(np.uint16), vc2.cpu().numpy().view(np.uint16))
+    assert_close(out.cpu().numpy(), out2[:1].cpu().numpy(), 3e-5)
+
+
 @pytest.mark.parametrize('batch,position', [(3, 5), (8, 40)])
 def test_drop_in_matches_reference_vectors(lib, gpu, batch, position):
     """qv_test_attention against the output of the reference's own CPU
