@@ -142,18 +142,34 @@ void run_attention(const rs::Shape &s, rs::Dtype dtype, bool precise, float scal
     }
 }
 
-// The reference's k_attention on device buffers of the 24/4/256 model.  One
-// token after at least one cached key (decode): two launches, the split
-// kernel preparing the query itself and the combine adding and appending
-// the new key.  Otherwise the prepare kernel writes the query's hi + lo
-// parts to q_hilo (2 * batch * 24 * 256 fp16) and appends the new K/V to
-// the pages, then attention (with the sigmoid gate) runs on them.
+// Partials bytes of a fused call: those of the prepared path (attention over
+// keys 0 .. position+batch-1) or of the fused split (the cached keys only),
+// whichever is larger.  The ring kernel's split count is not monotonic in
+// the page count (65 pages take 33 splits of two pages, 64 pages 64 splits
+// of one), so neither bounds the other.
+size_t fused_partials_bytes(int batch, int position) {
+    constexpr int H = rs::kModelQHeads, HKV = rs::kModelKvHeads, D = rs::kModelHeadDim;
+    const rs::Shape s{H, HKV, D, batch, position, 0};
+    size_t parts = rs::attention_workspace_bytes(s, rs::Dtype::F16, true);
+    if (batch <= rs::kMaxFusedSplitTokens && position >= 1)
+        parts = std::max(parts, rs::fused_tokens_workspace_bytes(batch, position));
+    return parts;
+}
+
+// The reference's k_attention on device buffers of the 24/4/256 model.  Up
+// to 8 tokens after at least one cached key (decode, verification): two
+// launches, the split kernel preparing the queries itself and the combine
+// adding and appending the new keys.  Otherwise (a first token, or a
+// prefill chunk) the prepare kernel writes the query's hi + lo parts to
+// q_hilo (2 * batch * 24 * 256 fp16) and appends the new K/V to the pages,
+// then attention (with the sigmoid gate) runs on them.
 void fused_attention(float *out, void *k_pages, void *v_pages, const float *q_gate, const float *key,
                      const float *value, const float *q_norm, const float *k_norm, int batch,
                      int position, int capacity, float epsilon, uint16_t *q_hilo, void *partials,
-                     hipStream_t stream) {
+                     size_t partials_bytes, hipStream_t stream) {
+    require(partials_bytes >= fused_partials_bytes(batch, position), "workspace too small");
     constexpr int H = rs::kModelQHeads, HKV = rs::kModelKvHeads, D = rs::kModelHeadDim;
-    if (batch == 1 && position >= 1) {
+    if (batch <= rs::kMaxFusedSplitTokens && position >= 1) {
         rs::FusedToken tok;
         tok.q_gate = q_gate;
         tok.key = key;
@@ -165,7 +181,8 @@ void fused_attention(float *out, void *k_pages, void *v_pages, const float *q_ga
         tok.head_stride = (size_t)capacity * D;
         tok.epsilon = epsilon;
         tok.position = position;
-        rs::launch_fused_decode(tok, capacity, partials, out, stream);
+        tok.tokens = batch;
+        rs::launch_fused_tokens(tok, capacity, partials, out, stream);
         return;
     }
     const rs::Shape s{H, HKV, D, batch, position, capacity};
@@ -226,7 +243,8 @@ extern "C" int qv_test_attention(float *out, void *key_cache, void *value_cache,
         DeviceBuffer qg(2 * out_bytes), k(kv_bytes), v(kv_bytes);
         DeviceBuffer qn(D * sizeof(float)), kn(D * sizeof(float));
         DeviceBuffer q(out_bytes), output(out_bytes);   // q: hi and lo fp16 parts
-        DeviceBuffer workspace(rs::attention_workspace_bytes(shape, rs::Dtype::F16, true));
+        const size_t partials_bytes = fused_partials_bytes(batch, position);
+        DeviceBuffer workspace(partials_bytes);
         hipStream_t stream = nullptr;
         // Host -> device: only the prefix [0, position) of each cache.
         upload(k_rows.data(), key_cache, (size_t)position * row_bytes);
@@ -240,7 +258,7 @@ extern "C" int qv_test_attention(float *out, void *key_cache, void *value_cache,
                         capacity, 0, position, stream);
         fused_attention(output.floats(), k_pages.data(), v_pages.data(), qg.floats(), k.floats(),
                         v.floats(), qn.floats(), kn.floats(), batch, position, capacity, epsilon,
-                        static_cast<uint16_t *>(q.data()), workspace.data(), stream);
+                        static_cast<uint16_t *>(q.data()), workspace.data(), partials_bytes, stream);
         rs::launch_unpack(k_rows.data(), v_rows.data(), k_pages.data(), v_pages.data(), HKV, D,
                           capacity, 0, n, stream);
         check(hipGetLastError());
@@ -416,14 +434,12 @@ extern "C" int qv_attention_combine(void *out, int dtype, int out_dtype, int q_h
     });
 }
 
-// The query's hi + lo parts, then the partials; a fused decode uses only the
-// partials region (no larger than the prepared path's).
+// The query's hi + lo parts, then the partials.
+static size_t fused_query_bytes(int batch) {
+    return align256((size_t)batch * rs::kModelQHeads * rs::kModelHeadDim * sizeof(float));
+}
 static size_t fused_workspace(int batch, int position) {
-    constexpr int H = rs::kModelQHeads, HKV = rs::kModelKvHeads, D = rs::kModelHeadDim;
-    const rs::Shape s{H, HKV, D, batch, position, 0};
-    size_t parts = rs::attention_workspace_bytes(s, rs::Dtype::F16, true);
-    if (batch == 1 && position >= 1) parts = std::max(parts, rs::fused_decode_workspace_bytes(position));
-    return align256((size_t)batch * H * D * sizeof(float)) + parts;
+    return fused_query_bytes(batch) + fused_partials_bytes(batch, position);
 }
 
 extern "C" int qv_attention_fused_workspace(uint64_t *bytes, int batch, int position) {
@@ -456,8 +472,8 @@ extern "C" int qv_attention_fused(float *out, void *k_pages, void *v_pages,
         require(workspace_bytes >= fused_workspace(batch, position), "workspace too small");
         hipStream_t st = static_cast<hipStream_t>(stream);
         uint16_t *q = static_cast<uint16_t *>(workspace);   // hi then lo fp16 parts
-        void *partials = static_cast<char *>(workspace) + align256((size_t)batch * H * D * sizeof(float));
+        void *partials = static_cast<char *>(workspace) + fused_query_bytes(batch);
         fused_attention(out, k_pages, v_pages, q_gate, key, value, q_norm, k_norm, batch, position,
-                        capacity, epsilon, q, partials, st);
+                        capacity, epsilon, q, partials, workspace_bytes - fused_query_bytes(batch), st);
     });
 }

@@ -124,18 +124,19 @@ __device__ __forceinline__ int v_slot_token(int g, int j) {
 // stores and loads.
 // ---------------------------------------------------------------------------
 //
-// PREP (the fused decode of one new token): the query is not read from q but
-// prepared here from a.tok (RMSNorm, gamma, RoPE at a.tok.position, hi + lo
-// fp16 parts; the same functions as the prepare kernel, so the same bits).
-// Wave w prepares the group's rows w and w + 4 while the first K page is in
-// flight, and writes them into the fragment slots of the LDS hand-over.
-template <int D, bool QSPLIT, bool PSPLIT, typename KV, bool PREP>
+// PREP > 0 (the fused path's new tokens): the query is not read from q but
+// prepared here from a.tok (RMSNorm, gamma, RoPE at the row's position, hi +
+// lo fp16 parts; the same functions as the prepare kernel, so the same bits).
+// Wave w prepares rows w, w + 4, ... (PREP of them) while the first K page is
+// in flight.  Every row sees the cached keys 0 .. a.position only: the new
+// tokens' own keys are added by the combine.
+template <int D, bool QSPLIT, bool PSPLIT, typename KV, int PREP>
 __global__ __launch_bounds__(kWaves * kWave)
 void attention_stream(SplitArgs a) {
     using V8 = typename Vec8<KV>::type;
     using QS = QueryStage<D, 1, QSPLIT, KV>;
     constexpr int KS = D / 32, DT = D / 16, NQ = QSPLIT ? 2 : 1;
-    static_assert(!PREP || (D == 4 * kWave && QSPLIT && std::is_same<KV, _Float16>::value),
+    static_assert(PREP == 0 || (D == 4 * kWave && QSPLIT && std::is_same<KV, _Float16>::value),
                   "the prepared query is the fp32 query of the 256-dim fp16 model, as hi + lo parts");
     __shared__ f32x4 so[kWaves][DT * kWave];   // merge slots, one per wave
     __shared__ V8 sq[QS::N * kWave];       // query fragments
@@ -144,12 +145,14 @@ void attention_stream(SplitArgs a) {
     const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
     const int split = blockIdx.x % a.splits, h = blockIdx.x / a.splits;
     QS qs;
-    float xq[2][4], gq[4];   // PREP: rows w and w + 4, lane l holding dims 64i + l
-    if constexpr (PREP) {
+    constexpr int PR = PREP > 0 ? PREP : 1;
+    float xq[PR][4], gq[4];   // PREP: rows w + 4r, lane l holding dims 64i + l
+    if constexpr (PREP > 0) {
 #pragma unroll
-        for (int r = 0; r < 2; ++r) {
+        for (int r = 0; r < PR; ++r) {
             const int row = min(w + 4 * r, a.rows - 1);
-            const float *src = a.tok.q_gate + (size_t)(h * a.group + row) * 2 * D;
+            const int t = row / a.group;
+            const float *src = a.tok.q_gate + ((size_t)t * a.q_heads + h * a.group + row - t * a.group) * 2 * D;
 #pragma unroll
             for (int i = 0; i < 4; ++i) xq[r][i] = src[64 * i + lane];
         }
@@ -167,7 +170,7 @@ void attention_stream(SplitArgs a) {
     const int n_steps = wi < a.n_pages ? (a.n_pages - 1 - wi) / waves_total + 1 : 0;
     const KV *kh = static_cast<const KV *>(a.k_pages) + (size_t)h * a.head_stride + lane * 8;
     const KV *vh = static_cast<const KV *>(a.v_pages) + (size_t)h * a.head_stride + lane * 8;
-    const int limit = a.position + min(lane & 15, a.rows - 1) / a.group;   // last visible key
+    const int limit = a.position + (PREP > 0 ? 0 : min(lane & 15, a.rows - 1) / a.group);   // last visible key
 
     f32x4 acc[DT];
 #pragma unroll
@@ -266,20 +269,25 @@ void attention_stream(SplitArgs a) {
     // head's last page), so every wave issues it before waiting on the query.
     load_k(min(wi, a.n_pages - 1));
     // PREP: the prepared rows are staged in LDS as fp32, row-major with a
-    // stride of D + 4 floats (the fragment slots' LDS, unused here), so the
-    // writes (lane l: dims 64i + l) and the fragment reads (16 rows, 32 bytes
-    // each) are both free of bank conflicts; hi and lo parts are split while
-    // gathering.
+    // stride of D + 4 floats (in the merge slots, which the page loop does
+    // not use), so the writes (lane l: dims 64i + l) and the fragment reads
+    // (16 rows, 32 bytes each) are both free of bank conflicts; hi and lo
+    // parts are split while gathering.
     constexpr int kStage = D + 4;
-    static_assert(!PREP || 8 * kStage * sizeof(float) <= sizeof(sq), "the staged rows fit the fragment slots");
-    float *stage = reinterpret_cast<float *>(sq);
-    if constexpr (PREP) {
-        float c = 1.f, sn = 0.f;
-        if (lane < 32) rope_cos_sin(a.tok.position, rope_freq(lane), c, sn);
-        const float cr[2] = {c, c}, sr[2] = {sn, sn};
-        norm_rope_rows<2>(xq, gq, cr, sr, a.tok.epsilon, lane);
+    static_assert(PREP == 0 || 16 * kStage * sizeof(float) <= sizeof(so), "the staged rows fit the merge slots");
+    float *stage = reinterpret_cast<float *>(so);
+    if constexpr (PREP > 0) {
+        const double freq = rope_freq(lane);
+        float cr[PR], sr[PR];
 #pragma unroll
-        for (int r = 0; r < 2; ++r) {
+        for (int r = 0; r < PR; ++r) {
+            cr[r] = 1.f;
+            sr[r] = 0.f;
+            if (lane < 32) rope_cos_sin(a.tok.position + min(w + 4 * r, a.rows - 1) / a.group, freq, cr[r], sr[r]);
+        }
+        norm_rope_rows<PR>(xq, gq, cr, sr, a.tok.epsilon, lane);
+#pragma unroll
+        for (int r = 0; r < PR; ++r) {
             const int row = w + 4 * r;
             if (row < a.rows) {
 #pragma unroll
@@ -290,7 +298,7 @@ void attention_stream(SplitArgs a) {
         qs.publish(sq, lane, w);
     }
     lds_barrier();
-    if constexpr (PREP) {
+    if constexpr (PREP > 0) {
         // Fragment ks of lane l: row l%16, dims 32ks + 8(l/16) .. +7, as
         // hi = fp16(q) and lo = fp16(q - hi).  Rows past the group are zero
         // (their results are never stored).
@@ -641,9 +649,9 @@ void attention_combine(CombineArgs c) {
 template <int D, int NQT>
 const void *pick(bool stream, Dtype dtype, bool precise) {
     if (stream) {
-        if (precise) return (const void *)&attention_stream<D, true, true, _Float16, false>;
-        if (dtype == Dtype::BF16) return (const void *)&attention_stream<D, false, true, __bf16, false>;
-        return (const void *)&attention_stream<D, false, false, _Float16, false>;
+        if (precise) return (const void *)&attention_stream<D, true, true, _Float16, 0>;
+        if (dtype == Dtype::BF16) return (const void *)&attention_stream<D, false, true, __bf16, 0>;
+        return (const void *)&attention_stream<D, false, false, _Float16, 0>;
     }
     if (precise) return (const void *)&attention_coop<D, NQT, true, true, _Float16, kCoopWaves>;
     if (dtype == Dtype::BF16) return (const void *)&attention_coop<D, NQT, false, true, __bf16, kCoopWaves>;
@@ -861,61 +869,81 @@ void launch_combine(const Shape &s, const SplitPlan &plan, Dtype dtype,
 }
 
 namespace {
-// The cached keys 0 .. position-1 as seen by the fused decode's one token
-// (its row sees every one of them), for the model's geometry.
-Shape fused_decode_shape(int position, int capacity) {
-    return Shape{kModelQHeads, kModelKvHeads, kModelHeadDim, 1, position - 1, capacity};
+// The split plan of a fused call: rows = 6 * tokens query rows per KV head
+// over the cached keys 0 .. position-1 (the shape's position is chosen so
+// that position + tokens is the cached key count).
+SplitPlan fused_plan(int tokens, int position) {
+    const Shape s{kModelQHeads, kModelKvHeads, kModelHeadDim, tokens, position - tokens, 0};
+    return plan_split(s, tokens, Dtype::F16, true);
 }
 }  // namespace
 
-size_t fused_decode_workspace_bytes(int position) {
-    const Shape s = fused_decode_shape(position, 0);
-    return plan_bytes(s, plan_split(s, 1, Dtype::F16, true));
+size_t fused_tokens_workspace_bytes(int tokens, int position) {
+    const Shape s{kModelQHeads, kModelKvHeads, kModelHeadDim, tokens, position - tokens, 0};
+    return plan_bytes(s, fused_plan(tokens, position));
 }
 
-void launch_fused_decode(const FusedToken &tok, int capacity, void *workspace, float *out, hipStream_t stream) {
+void launch_fused_tokens(const FusedToken &tok, int capacity, void *workspace, float *out, hipStream_t stream) {
     constexpr int D = kModelHeadDim;
-    require(tok.position >= 1, "the fused decode needs at least one cached key");
-    const Shape s = fused_decode_shape(tok.position, capacity);
-    const SplitPlan plan = plan_split(s, 1, Dtype::F16, true);
-    require(plan.kind == SplitKind::Stream && plan.rows <= 8 && !plan.half_parts && plan.splits >= 1,
-            "the fused decode runs the stream kernel on at most 8 rows");
+    const int T = tok.tokens;
+    require(tok.position >= 1, "the fused split needs at least one cached key");
+    require(T >= 1 && T <= kMaxFusedSplitTokens, "the fused split takes 1 to 8 tokens");
+    const SplitPlan plan = fused_plan(T, tok.position);
+    require((plan.kind == SplitKind::Stream || plan.kind == SplitKind::Ring) && !plan.half_parts &&
+            plan.splits >= 1, "the fused split runs the stream or ring kernel");
     constexpr float kScaleLog2 = (1.0f / 16.0f) * 1.4426950408889634f;
+    const int kv_heads = kModelKvHeads, group = kModelQHeads / kModelKvHeads;
+
+    const void *split = nullptr;
+    int threads = kWaves * kWave;
+    if (plan.kind == SplitKind::Stream) {
+        // Rows w + 4r per wave: two rows for one token (6 rows), four for two.
+        split = plan.rows <= 8 ? (const void *)&attention_stream<D, true, true, _Float16, 2>
+                               : (const void *)&attention_stream<D, true, true, _Float16, 4>;
+        require(plan.rows <= 16, "the stream kernel holds 16 rows");
+    } else {
+        split = ring_prep_kernel(plan.nqt);
+        threads = kRingThreads;
+    }
+    require(split != nullptr, "no prepared-query split kernel for this row count");
 
     SplitArgs a = {};
     a.k_pages = tok.k_pages;
     a.v_pages = tok.v_pages;
     a.part_o = static_cast<float *>(workspace);
-    a.part_ml = a.part_o + (size_t)s.kv_heads * plan.splits * plan.rows * D;
+    a.part_ml = a.part_o + (size_t)kv_heads * plan.splits * plan.rows * D;
     a.head_stride = tok.head_stride;
-    a.q_heads = s.q_heads;
-    a.kv_heads = s.kv_heads;
-    a.group = s.group();
+    a.q_heads = kModelQHeads;
+    a.kv_heads = kv_heads;
+    a.group = group;
     a.rows = plan.rows;
-    a.position = s.position;
+    a.position = tok.position - 1;   // every row sees keys 0 .. position-1
     a.n_keys = tok.position;
     a.n_pages = plan.n_pages;
     a.splits = plan.splits;
     a.scale_log2 = kScaleLog2;
     a.tok = tok;
     void *split_args[] = {&a};
-    check(hipLaunchKernel((const void *)&attention_stream<D, true, true, _Float16, true>,
-                          dim3(plan.splits * s.kv_heads), dim3(kWaves * kWave), split_args, 0, stream));
+    check(hipLaunchKernel(split, dim3(plan.splits * kv_heads), dim3(threads), split_args, 0, stream));
 
     CombineArgs c = {};
     c.part_o = workspace;
     c.part_ml = a.part_ml;
     c.out = out;
     c.gate = tok.q_gate;
-    c.q_heads = s.q_heads;
-    c.group = s.group();
+    c.q_heads = kModelQHeads;
+    c.group = group;
     c.rows = plan.rows;
     c.splits = plan.splits;
     c.scale_log2 = kScaleLog2;
     c.tok = tok;
+    // The stream kernel stores its partials with the default policy, the
+    // ring kernel non-temporally; the combine loads them the same way.
+    const void *combine = plan.kind == SplitKind::Stream
+        ? (const void *)&attention_combine<D, _Float16, kOutGated, float, false, true>
+        : (const void *)&attention_combine<D, _Float16, kOutGated, float, true, true>;
     void *combine_args[] = {&c};
-    check(hipLaunchKernel((const void *)&attention_combine<D, _Float16, kOutGated, float, false, true>,
-                          dim3(plan.rows, s.kv_heads), dim3(kWaves * kWave), combine_args, 0, stream));
+    check(hipLaunchKernel(combine, dim3(plan.rows, kv_heads), dim3(kWaves * kWave), combine_args, 0, stream));
 }
 
 }  // namespace rs

@@ -17,21 +17,23 @@ struct Shape {
 
 enum class SplitKind { Stream, Coop, Ring };
 
-// The new token of a fused decode call (the reference's attn_prepare inputs
-// for one token of the 24/4/256 model): the split kernel prepares the query
-// from it, and the combine kernel prepares its key and value, attends to
-// them as the last key and appends them to the pages.
+// The new tokens of a fused call of 1..8 tokens (the reference's
+// attn_prepare inputs for the 24/4/256 model): the split kernel prepares the
+// queries from them and attends to the cached keys; the combine kernel
+// prepares their keys and values, attends to them causally (token t sees
+// new keys 0..t) and appends them to the pages.
 struct FusedToken {
-    const float *q_gate;   // [q_heads][2D]: q, then the gate
-    const float *key;      // [kv_heads][D]
-    const float *value;    // [kv_heads][D]
+    const float *q_gate;   // [tokens][q_heads][2D]: q, then the gate
+    const float *key;      // [tokens][kv_heads][D]
+    const float *value;    // [tokens][kv_heads][D]
     const float *q_norm;   // [D]
     const float *k_norm;   // [D]
     void *k_pages;
     void *v_pages;
     size_t head_stride;
     float epsilon;
-    int position;          // the token's position: RoPE angle and page slot
+    int position;          // token 0's position: RoPE angles and page slots
+    int tokens;
 };
 
 // Arguments of every split-K partial kernel.
@@ -53,6 +55,9 @@ struct SplitArgs {
 // (nullptr otherwise).  It takes kRingThreads threads and SplitArgs.
 constexpr int kRingThreads = 512;
 const void *ring_kernel(int D, int nqt, Dtype dtype, bool precise);
+// The precise D=256 instance that prepares its query from SplitArgs::tok
+// (the fused split of 3..8 tokens; nqt 2 or 3), or nullptr.
+const void *ring_prep_kernel(int nqt);
 
 // The split-K decomposition chosen for one launch of the partial kernel.
 struct SplitPlan {
@@ -94,14 +99,15 @@ void launch_combine(const Shape &s, const SplitPlan &plan, Dtype dtype,
                     const void *workspace, void *out, bool out_f32, const float *gate,
                     hipStream_t stream);
 
-// Fused decode of one new token at tok.position >= 1 (24/4/256, fp16 pages):
-// the split kernel prepares the query itself and attends to the cached keys
-// 0 .. position-1; the combine prepares the new key and value, adds them as
-// the last key, appends them to the pages and applies the gate.  No prepare
-// launch.  The workspace holds the partials of plan_split for the shape with
-// position-1 and one token.
-void launch_fused_decode(const FusedToken &tok, int capacity, void *workspace, float *out, hipStream_t stream);
-size_t fused_decode_workspace_bytes(int position);
+// Fused attention of tok.tokens (1..8) new tokens at tok.position >= 1
+// (24/4/256, fp16 pages) in two launches: the split kernel prepares the
+// queries itself and attends to the cached keys 0 .. position-1; the combine
+// prepares the new keys and values, adds them causally, appends them to the
+// pages and applies the gate.  No prepare launch.  The workspace holds the
+// split's partials (fused_tokens_workspace_bytes).
+void launch_fused_tokens(const FusedToken &tok, int capacity, void *workspace, float *out, hipStream_t stream);
+size_t fused_tokens_workspace_bytes(int tokens, int position);
+constexpr int kMaxFusedSplitTokens = 8;
 
 // Chunked prefill: all group*tokens query rows against the pages in one
 // launch (no workspace); `dtype` q and out, [tokens][q_heads][D].  A precise

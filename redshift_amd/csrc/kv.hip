@@ -86,8 +86,8 @@ void prepare_kernel(_Float16 *q_hilo, _Float16 *k_pages, _Float16 *v_pages, cons
             q_hilo[(size_t)gridDim.y * H * D + idx] = (_Float16)(x[0][w] - (float)hi);
         } else {
             const int token = position + t;
-            k_pages[(size_t)kh * head_stride + k_page_offset(token, d, D)] = (_Float16)x[0][w];
-            v_pages[(size_t)kh * head_stride + v_page_offset(token, d, D)] = (_Float16)v[w];
+            k_pages[(size_t)kh * head_stride + k_page_offset(token, d, D)] = cache_half(x[0][w]);
+            v_pages[(size_t)kh * head_stride + v_page_offset(token, d, D)] = cache_half(v[w]);
         }
     }
 }

@@ -29,6 +29,15 @@ __device__ __forceinline__ void rope_cos_sin(int pos, double freq, float &c, flo
     sincosf((float)r, &s, &c);
 }
 
+// The fp16 cache entry of an fp32 value, rounded as the reference rounds
+// one (__float2half_rn of a float): the value is first held as fp32, so the
+// compiler cannot fold the product that made it and the conversion into one
+// mixed-precision FMA, which rounds once and differs in rare cases.
+__device__ __forceinline__ _Float16 cache_half(float x) {
+    asm volatile("" : "+v"(x));
+    return (_Float16)x;
+}
+
 // Sum over the 64 lanes of a wave, the same in every lane: xor-1 and xor-2
 // quad permutes, the half-row and row mirrors (within 16 lanes, all on
 // DPP), then the 16-lane row groups exchanged with lane swaps.

@@ -317,11 +317,15 @@ def test_fused_device_path_matches_oracle(gpu):
     assert_close(vc.float().cpu().numpy(), expected[2], 0)
 
 
-@pytest.mark.parametrize('batch,position', [(5, 5000), (8, 20000), (3, 40)])
+@pytest.mark.parametrize('batch,position', [(5, 5000), (8, 20000), (3, 40), (2, 100), (4, 31), (6, 33),
+                                            (7, 1)])
 def test_fused_verify_matches_oracle(gpu, batch, position):
-    """Fused verify batches of 3-8 tokens (the ring kernel's precise
-    instance: fp32 query as hi + lo parts) at split lengths of 1 to ~11
-    pages, on the reference's sine-wave fixture and tolerances."""
+    """Fused batches of 2-8 tokens: the split kernel prepares the queries
+    itself (stream kernel up to 16 rows, the ring kernel's precise instance
+    beyond) over the cached keys, and the combine adds the new keys
+    causally.  Split lengths of 1 to ~11 pages, a first cached page that is
+    full (31 + 1) or holds one key, on the reference's sine-wave fixture and
+    tolerances."""
     torch = gpu
     c = kat.sine_wave_case(batch=batch, position=position)
     expected = ref.fused_attention(c['key_cache'], c['value_cache'], c['q_gate'], c['key'], c['value'],
@@ -330,8 +334,11 @@ def test_fused_verify_matches_oracle(gpu, batch, position):
     cache.pack(torch.from_numpy(c['key_cache']).cuda(), torch.from_numpy(c['value_cache']).cuda())
     dev = [torch.from_numpy(f32(c[name])).cuda() for name in ('q_gate', 'key', 'value', 'q_norm', 'k_norm')]
     out = A.attention_fused(*dev, cache, position, c['epsilon'])
+    kc, vc = cache.unpack(0, position + batch)
     torch.cuda.synchronize()
     assert_close(out.cpu().numpy(), expected[0], 3e-4)
+    assert_close(kc.float().cpu().numpy(), expected[1], 2e-3)
+    assert_close(vc.float().cpu().numpy(), expected[2], 0)
 
 
 @pytest.mark.parametrize('batch,position', [(100, 300), (57, 1)])
