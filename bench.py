@@ -428,8 +428,8 @@ def main():
                            'GB/s': round(wf.kv_bytes() / (us * 1e-6) / 1e9, 1),
                            'frac_hbm': round(wf.kv_bytes() / (us * 1e-6) / 1e9 / HBM_PEAK_GBS, 4),
                            'what': 'qv_attention_fused per layer: prepare + append + attention + gate'
-                                   + (' (one token: query prepared in the split kernel, key and value '
-                                      'prepared, attended and appended in the combine; two launches)'
+                                   + (' (one token: query prepared and key and value appended in the '
+                                      'split kernel, the new key added in the combine; two launches)'
                                       if wf.tokens == 1 else '')}
         if 'fused_prefill_2k' in chosen:
             # The fused drop-in on a 2048-token prefill chunk at position 6144

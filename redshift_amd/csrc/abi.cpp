@@ -156,10 +156,10 @@ size_t fused_partials_bytes(int batch, int position) {
     return parts;
 }
 
-// The reference's k_attention on device buffers of the 24/4/256 model.  Up
-// to 8 tokens after at least one cached key (decode, verification): two
-// launches, the split kernel preparing the queries itself and the combine
-// adding and appending the new keys.  Otherwise (a first token, or a
+// The reference's k_attention on device buffers of the 24/4/256 model.  One
+// token after at least one cached key (decode): two launches, the split
+// kernel preparing the query and appending the new key and value, the
+// combine adding that key.  Otherwise (verification, a first token, a
 // prefill chunk) the prepare kernel writes the query's hi + lo parts to
 // q_hilo (2 * batch * 24 * 256 fp16) and appends the new K/V to the pages,
 // then attention (with the sigmoid gate) runs on them.

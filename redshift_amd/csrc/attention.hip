@@ -124,19 +124,21 @@ __device__ __forceinline__ int v_slot_token(int g, int j) {
 // stores and loads.
 // ---------------------------------------------------------------------------
 //
-// PREP > 0 (the fused path's new tokens): the query is not read from q but
-// prepared here from a.tok (RMSNorm, gamma, RoPE at the row's position, hi +
-// lo fp16 parts; the same functions as the prepare kernel, so the same bits).
-// Wave w prepares rows w, w + 4, ... (PREP of them) while the first K page is
-// in flight.  Every row sees the cached keys 0 .. a.position only: the new
-// tokens' own keys are added by the combine.
-template <int D, bool QSPLIT, bool PSPLIT, typename KV, int PREP>
+// PREP (the fused path's new tokens, 1 or 2 of them, group 6): the query is
+// not read from q but prepared here from a.tok (RMSNorm, gamma, RoPE, hi +
+// lo fp16 parts; the same functions as the prepare kernel, so the same bits)
+// while the first K page is in flight: wave w prepares rows 3w .. 3w+2, three
+// query heads of token w/2.  Every row sees the cached keys 0 .. a.position
+// only.  The first split's workgroups also store the prepared rows in
+// a.tok.q_prep and prepare and append the new keys (wave j: token j), which
+// the combine adds.
+template <int D, bool QSPLIT, bool PSPLIT, typename KV, bool PREP>
 __global__ __launch_bounds__(kWaves * kWave)
 void attention_stream(SplitArgs a) {
     using V8 = typename Vec8<KV>::type;
     using QS = QueryStage<D, 1, QSPLIT, KV>;
     constexpr int KS = D / 32, DT = D / 16, NQ = QSPLIT ? 2 : 1;
-    static_assert(PREP == 0 || (D == 4 * kWave && QSPLIT && std::is_same<KV, _Float16>::value),
+    static_assert(!PREP || (D == kModelHeadDim && D == 4 * kWave && QSPLIT && std::is_same<KV, _Float16>::value),
                   "the prepared query is the fp32 query of the 256-dim fp16 model, as hi + lo parts");
     __shared__ f32x4 so[kWaves][DT * kWave];   // merge slots, one per wave
     __shared__ V8 sq[QS::N * kWave];       // query fragments
@@ -145,19 +147,26 @@ void attention_stream(SplitArgs a) {
     const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
     const int split = blockIdx.x % a.splits, h = blockIdx.x / a.splits;
     QS qs;
-    constexpr int PR = PREP > 0 ? PREP : 1;
-    float xq[PR][4], gq[4];   // PREP: rows w + 4r, lane l holding dims 64i + l
-    if constexpr (PREP > 0) {
+    // PREP: rows 3w + r of token w/2 (lane l holding dims 64i + l), and the
+    // new key of token w in the first split.
+    constexpr int PR = 3;
+    float xq[PR][4], gq[4];
+    NewKeyRow nk;
+    const int ptok = w >> 1;
+    const bool prows = PREP && ptok < a.tok.tokens;               // wave-uniform
+    const bool pkey = PREP && split == 0 && w < a.tok.tokens;     // wave-uniform
+    if constexpr (PREP) {
+        if (prows) {
 #pragma unroll
-        for (int r = 0; r < PR; ++r) {
-            const int row = min(w + 4 * r, a.rows - 1);
-            const int t = row / a.group;
-            const float *src = a.tok.q_gate + ((size_t)t * a.q_heads + h * a.group + row - t * a.group) * 2 * D;
+            for (int r = 0; r < PR; ++r) {
+                const float *src = a.tok.q_gate + ((size_t)ptok * a.q_heads + h * a.group + 3 * (w & 1) + r) * 2 * D;
 #pragma unroll
-            for (int i = 0; i < 4; ++i) xq[r][i] = src[64 * i + lane];
+                for (int i = 0; i < 4; ++i) xq[r][i] = src[64 * i + lane];
+            }
+#pragma unroll
+            for (int i = 0; i < 4; ++i) gq[i] = a.tok.q_norm[64 * i + lane];
         }
-#pragma unroll
-        for (int i = 0; i < 4; ++i) gq[i] = a.tok.q_norm[64 * i + lane];
+        if (pkey) load_new_key(nk, a.tok, a.kv_heads, h, w, lane);
     } else {
         qs.issue(a, h, lane, w);
     }
@@ -170,7 +179,7 @@ void attention_stream(SplitArgs a) {
     const int n_steps = wi < a.n_pages ? (a.n_pages - 1 - wi) / waves_total + 1 : 0;
     const KV *kh = static_cast<const KV *>(a.k_pages) + (size_t)h * a.head_stride + lane * 8;
     const KV *vh = static_cast<const KV *>(a.v_pages) + (size_t)h * a.head_stride + lane * 8;
-    const int limit = a.position + (PREP > 0 ? 0 : min(lane & 15, a.rows - 1) / a.group);   // last visible key
+    const int limit = a.position + (PREP ? 0 : min(lane & 15, a.rows - 1) / a.group);   // last visible key
 
     f32x4 acc[DT];
 #pragma unroll
@@ -274,31 +283,35 @@ void attention_stream(SplitArgs a) {
     // (16 rows, 32 bytes each) are both free of bank conflicts; hi and lo
     // parts are split while gathering.
     constexpr int kStage = D + 4;
-    static_assert(PREP == 0 || 16 * kStage * sizeof(float) <= sizeof(so), "the staged rows fit the merge slots");
+    static_assert(!PREP || 16 * kStage * sizeof(float) <= sizeof(so), "the staged rows fit the merge slots");
     float *stage = reinterpret_cast<float *>(so);
-    if constexpr (PREP > 0) {
+    if constexpr (PREP) {
         const double freq = rope_freq(lane);
-        float cr[PR], sr[PR];
+        if (prows) {
+            float c = 1.f, sn = 0.f;
+            if (lane < 32) rope_cos_sin(a.tok.position + ptok, freq, c, sn);
+            const float cr[PR] = {c, c, c}, sr[PR] = {sn, sn, sn};
+            norm_rope_rows<PR>(xq, gq, cr, sr, a.tok.epsilon, lane);
 #pragma unroll
-        for (int r = 0; r < PR; ++r) {
-            cr[r] = 1.f;
-            sr[r] = 0.f;
-            if (lane < 32) rope_cos_sin(a.tok.position + min(w + 4 * r, a.rows - 1) / a.group, freq, cr[r], sr[r]);
-        }
-        norm_rope_rows<PR>(xq, gq, cr, sr, a.tok.epsilon, lane);
+            for (int r = 0; r < PR; ++r) {
+                const int row = 3 * w + r;
 #pragma unroll
-        for (int r = 0; r < PR; ++r) {
-            const int row = w + 4 * r;
-            if (row < a.rows) {
-#pragma unroll
-                for (int i = 0; i < 4; ++i) stage[row * kStage + 64 * i + lane] = xq[r][i];
+                for (int i = 0; i < 4; ++i) {
+                    stage[row * kStage + 64 * i + lane] = xq[r][i];
+                    if (split == 0) a.tok.q_prep[((size_t)h * a.rows + row) * D + 64 * i + lane] = xq[r][i];
+                }
             }
+        }
+        if (pkey) {
+            float c = 1.f, sn = 0.f;
+            if (lane < 32) rope_cos_sin(a.tok.position + w, freq, c, sn);
+            append_new_key(nk, a.tok, h, w, c, sn, lane);
         }
     } else {
         qs.publish(sq, lane, w);
     }
     lds_barrier();
-    if constexpr (PREP > 0) {
+    if constexpr (PREP) {
         // Fragment ks of lane l: row l%16, dims 32ks + 8(l/16) .. +7, as
         // hi = fp16(q) and lo = fp16(q - hi).  Rows past the group are zero
         // (their results are never stored).
@@ -649,9 +662,9 @@ void attention_combine(CombineArgs c) {
 template <int D, int NQT>
 const void *pick(bool stream, Dtype dtype, bool precise) {
     if (stream) {
-        if (precise) return (const void *)&attention_stream<D, true, true, _Float16, 0>;
-        if (dtype == Dtype::BF16) return (const void *)&attention_stream<D, false, true, __bf16, 0>;
-        return (const void *)&attention_stream<D, false, false, _Float16, 0>;
+        if (precise) return (const void *)&attention_stream<D, true, true, _Float16, false>;
+        if (dtype == Dtype::BF16) return (const void *)&attention_stream<D, false, true, __bf16, false>;
+        return (const void *)&attention_stream<D, false, false, _Float16, false>;
     }
     if (precise) return (const void *)&attention_coop<D, NQT, true, true, _Float16, kCoopWaves>;
     if (dtype == Dtype::BF16) return (const void *)&attention_coop<D, NQT, false, true, __bf16, kCoopWaves>;
@@ -878,34 +891,31 @@ SplitPlan fused_plan(int tokens, int position) {
 }
 }  // namespace
 
-size_t fused_tokens_workspace_bytes(int tokens, int position) {
+// The partials, then the prepared queries (fp32 [kv_heads][rows][D]).
+size_t fused_prep_offset(int tokens, int position) {
     const Shape s{kModelQHeads, kModelKvHeads, kModelHeadDim, tokens, position - tokens, 0};
-    return plan_bytes(s, fused_plan(tokens, position));
+    return (plan_bytes(s, fused_plan(tokens, position)) + 255) & ~size_t(255);
+}
+
+size_t fused_tokens_workspace_bytes(int tokens, int position) {
+    return fused_prep_offset(tokens, position) + (size_t)kModelQHeads * tokens * kModelHeadDim * sizeof(float);
 }
 
 void launch_fused_tokens(const FusedToken &tok, int capacity, void *workspace, float *out, hipStream_t stream) {
     constexpr int D = kModelHeadDim;
     const int T = tok.tokens;
     require(tok.position >= 1, "the fused split needs at least one cached key");
-    require(T >= 1 && T <= kMaxFusedSplitTokens, "the fused split takes 1 to 8 tokens");
+    require(T >= 1 && T <= kMaxFusedSplitTokens, "too many tokens for the fused split");
     const SplitPlan plan = fused_plan(T, tok.position);
-    require((plan.kind == SplitKind::Stream || plan.kind == SplitKind::Ring) && !plan.half_parts &&
-            plan.splits >= 1, "the fused split runs the stream or ring kernel");
+    require(!plan.half_parts && plan.splits >= 1, "the fused split stores fp32 partials");
     constexpr float kScaleLog2 = (1.0f / 16.0f) * 1.4426950408889634f;
     const int kv_heads = kModelKvHeads, group = kModelQHeads / kModelKvHeads;
+    require(plan.rows == group * T, "the fused split serves every query head of every token");
+    FusedToken ft = tok;
+    ft.q_prep = reinterpret_cast<float *>(static_cast<char *>(workspace) + fused_prep_offset(T, tok.position));
 
-    const void *split = nullptr;
-    int threads = kWaves * kWave;
-    if (plan.kind == SplitKind::Stream) {
-        // Rows w + 4r per wave: two rows for one token (6 rows), four for two.
-        split = plan.rows <= 8 ? (const void *)&attention_stream<D, true, true, _Float16, 2>
-                               : (const void *)&attention_stream<D, true, true, _Float16, 4>;
-        require(plan.rows <= 16, "the stream kernel holds 16 rows");
-    } else {
-        split = ring_prep_kernel(plan.nqt);
-        threads = kRingThreads;
-    }
-    require(split != nullptr, "no prepared-query split kernel for this row count");
+    require(plan.kind == SplitKind::Stream && plan.rows <= 12, "the prepared-query stream kernel takes one or two tokens");
+    const void *split = (const void *)&attention_stream<D, true, true, _Float16, true>;
 
     SplitArgs a = {};
     a.k_pages = tok.k_pages;
@@ -922,9 +932,9 @@ void launch_fused_tokens(const FusedToken &tok, int capacity, void *workspace, f
     a.n_pages = plan.n_pages;
     a.splits = plan.splits;
     a.scale_log2 = kScaleLog2;
-    a.tok = tok;
+    a.tok = ft;
     void *split_args[] = {&a};
-    check(hipLaunchKernel(split, dim3(plan.splits * kv_heads), dim3(threads), split_args, 0, stream));
+    check(hipLaunchKernel(split, dim3(plan.splits * kv_heads), dim3(kWaves * kWave), split_args, 0, stream));
 
     CombineArgs c = {};
     c.part_o = workspace;
@@ -936,12 +946,10 @@ void launch_fused_tokens(const FusedToken &tok, int capacity, void *workspace, f
     c.rows = plan.rows;
     c.splits = plan.splits;
     c.scale_log2 = kScaleLog2;
-    c.tok = tok;
-    // The stream kernel stores its partials with the default policy, the
-    // ring kernel non-temporally; the combine loads them the same way.
-    const void *combine = plan.kind == SplitKind::Stream
-        ? (const void *)&attention_combine<D, _Float16, kOutGated, float, false, true>
-        : (const void *)&attention_combine<D, _Float16, kOutGated, float, true, true>;
+    c.tok = ft;
+    // The stream kernel stores its partials with the default policy; the
+    // combine loads them the same way.
+    const void *combine = (const void *)&attention_combine<D, _Float16, kOutGated, float, false, true>;
     void *combine_args[] = {&c};
     check(hipLaunchKernel(combine, dim3(plan.rows, kv_heads), dim3(kWaves * kWave), combine_args, 0, stream));
 }

@@ -26,14 +26,13 @@ enum { kOutSame = 0, kOutF32 = 1, kOutGated = 2 };
 // policy of the combine follows the store policy of the split kernel: the
 // mixed pairs measured slower).
 //
-// NEWKEY (the fused path's new tokens, 1..8): the splits cover the cached
-// keys only.  Wave w4 takes the new keys j = w4 and w4 + 4 that this row
-// sees (j <= its token t): it prepares the row's query and those keys
-// (RMSNorm, gamma, RoPE at position + token: the prepare kernel's functions,
-// so the same bits) and folds each in as one more split: score q . fp16(k),
-// weight 1 at its own max, value fp16(v), the cache's rounding.  The row of
-// token j's first query head also appends fp16(k_j) and fp16(v_j) to the
-// pages at position + j.
+// NEWKEY (the fused decode's new token; the code takes up to 8 tokens): the
+// splits cover the cached keys only.  Wave w4 takes the new keys j = w4 and
+// w4 + 4 that this row sees (j <= its token t) and folds each in as one
+// more split: score
+// q . k_j with the prepared fp32 query (tok->q_prep) and the fp16 key the
+// split kernel appended at position + j, weight 1 at its own max, value the
+// appended fp16 v_j.
 template <int D, typename KV, typename PT, bool NT, bool NEWKEY = false>
 __device__ __forceinline__ void combine_row(const PT *part_o, const float *part_ml, int splits,
                                             int rows, int group, int q_heads, int row, int h,
@@ -60,36 +59,30 @@ __device__ __forceinline__ void combine_row(const PT *part_o, const float *part_
         gv = gate[((size_t)t * q_heads + hq) * 2 * D + D + jd];
 
     float M = -INFINITY, L = 0.f, acc[DV] = {};
-    // NEWKEY: this wave's new keys; their inputs are requested with the
-    // partials.
+    // NEWKEY: this wave's new keys (lane l: dims DV*l .. +DV-1 of the query
+    // and of each key and value), requested with the partials.
     constexpr int NK = 2;
-    float xq[1][4], gq[4], gk[4], xk[NK][1][4], vn[NK][DV], m_new[NK] = {-INFINITY, -INFINITY};
-    _Float16 kh[NK][4], vh[NK][DV];
+    typedef _Float16 H4 __attribute__((ext_vector_type(4)));
+    f32x4 qn = {};
+    H4 kn[NK] = {};
+    _Float16 vh[NK][DV] = {};
+    float m_new[NK] = {-INFINITY, -INFINITY};
     bool has[NK] = {};
     if constexpr (NEWKEY) {
         static_assert(D == 4 * kWave && DV == 4, "the fused model's 256-dim heads");
-        const int kv_heads = q_heads / group;
 #pragma unroll
         for (int k = 0; k < NK; ++k) has[k] = w4 + 4 * k < tok->tokens && w4 + 4 * k <= t;
-        if (has[0]) {
-            const float *qsrc = tok->q_gate + ((size_t)t * q_heads + hq) * 2 * D;
-#pragma unroll
-            for (int i = 0; i < 4; ++i) {
-                xq[0][i] = qsrc[64 * i + lane];
-                gq[i] = tok->q_norm[64 * i + lane];
-                gk[i] = tok->k_norm[64 * i + lane];
-            }
-        }
+        if (has[0]) qn = *reinterpret_cast<const f32x4 *>(tok->q_prep + ((size_t)h * rows + rc) * D + lane * DV);
+        const _Float16 *kp = static_cast<const _Float16 *>(tok->k_pages) + (size_t)h * tok->head_stride;
+        const _Float16 *vp = static_cast<const _Float16 *>(tok->v_pages) + (size_t)h * tok->head_stride;
 #pragma unroll
         for (int k = 0; k < NK; ++k) {
             if (has[k]) {
-                const size_t kv_row = ((size_t)(w4 + 4 * k) * kv_heads + h) * D;
+                const int pos = tok->position + w4 + 4 * k;
+                // Dims DV*l .. +3 of a key are contiguous in its page.
+                kn[k] = *reinterpret_cast<const H4 *>(kp + k_page_offset(pos, lane * DV, D));
 #pragma unroll
-                for (int i = 0; i < 4; ++i) xk[k][0][i] = tok->key[kv_row + 64 * i + lane];
-                // Scalar loads: the fused entry does not require `value` to
-                // be 16-byte aligned.
-#pragma unroll
-                for (int d = 0; d < DV; ++d) vn[k][d] = tok->value[kv_row + lane * DV + d];
+                for (int d = 0; d < DV; ++d) vh[k][d] = vp[v_page_offset(pos, lane * DV + d, D)];
             }
         }
     }
@@ -113,30 +106,16 @@ __device__ __forceinline__ void combine_row(const PT *part_o, const float *part_
                 ov[i] = *src;
         }
         if constexpr (NEWKEY) {
-            // Round 0: the new keys are prepared while this round's partial
-            // loads are in flight (their inputs were requested first).
-            if (s0 == 0 && has[0]) {
-                const double freq = rope_freq(lane);
-                float c = 1.f, sn = 0.f;
-                if (lane < 32) rope_cos_sin(tok->position + t, freq, c, sn);
-                const float cq[1] = {c}, sq[1] = {sn};
-                norm_rope_rows<1>(xq, gq, cq, sq, tok->epsilon, lane);
+            // Round 0: the new keys' scores, while this round's partial loads
+            // are in flight (their inputs were requested first).
+            if (s0 == 0) {
 #pragma unroll
                 for (int k = 0; k < NK; ++k) {
                     if (has[k]) {
-                        float ck = 1.f, sk = 0.f;
-                        if (lane < 32) rope_cos_sin(tok->position + w4 + 4 * k, freq, ck, sk);
-                        const float cr[1] = {ck}, sr[1] = {sk};
-                        norm_rope_rows<1>(xk[k], gk, cr, sr, tok->epsilon, lane);
                         float dot = 0.f;
 #pragma unroll
-                        for (int i = 0; i < 4; ++i) {
-                            kh[k][i] = cache_half(xk[k][0][i]);
-                            dot += xq[0][i] * (float)kh[k][i];
-                        }
+                        for (int d = 0; d < DV; ++d) dot += qn[d] * (float)kn[k][d];
                         m_new[k] = wave_sum_dpp(dot) * scale_log2;
-#pragma unroll
-                        for (int d = 0; d < DV; ++d) vh[k][d] = cache_half(vn[k][d]);
                     }
                 }
             }
@@ -179,16 +158,6 @@ __device__ __forceinline__ void combine_row(const PT *part_o, const float *part_
 #pragma unroll
                 for (int d = 0; d < DV; ++d) acc[d] = acc[d] * f + e * (float)vh[k][d];
                 M = rm;
-                const int j = w4 + 4 * k;
-                if (valid && row == j * group) {
-                    const int pos = tok->position + j;
-                    _Float16 *kp = static_cast<_Float16 *>(tok->k_pages) + (size_t)h * tok->head_stride;
-                    _Float16 *vp = static_cast<_Float16 *>(tok->v_pages) + (size_t)h * tok->head_stride;
-#pragma unroll
-                    for (int i = 0; i < 4; ++i) kp[k_page_offset(pos, 64 * i + lane, D)] = kh[k][i];
-#pragma unroll
-                    for (int d = 0; d < DV; ++d) vp[v_page_offset(pos, lane * DV + d, D)] = vh[k][d];
-                }
             }
         }
     }

@@ -17,11 +17,12 @@ struct Shape {
 
 enum class SplitKind { Stream, Coop, Ring };
 
-// The new tokens of a fused call of 1..8 tokens (the reference's
-// attn_prepare inputs for the 24/4/256 model): the split kernel prepares the
-// queries from them and attends to the cached keys; the combine kernel
-// prepares their keys and values, attends to them causally (token t sees
-// new keys 0..t) and appends them to the pages.
+// The new token of a fused decode (the reference's attn_prepare inputs for
+// the 24/4/256 model).  The split kernel prepares the query and attends to
+// the cached keys; its first split's workgroups also prepare the new key and
+// value, append them to the pages and publish the prepared query rows in
+// q_prep.  The combine kernel adds the new key from the pages and q_prep.
+// (The kernels take up to two tokens, token t seeing new keys 0..t.)
 struct FusedToken {
     const float *q_gate;   // [tokens][q_heads][2D]: q, then the gate
     const float *key;      // [tokens][kv_heads][D]
@@ -34,6 +35,7 @@ struct FusedToken {
     float epsilon;
     int position;          // token 0's position: RoPE angles and page slots
     int tokens;
+    float *q_prep;         // [kv_heads][tokens * group][D] prepared fp32 queries
 };
 
 // Arguments of every split-K partial kernel.
@@ -55,9 +57,6 @@ struct SplitArgs {
 // (nullptr otherwise).  It takes kRingThreads threads and SplitArgs.
 constexpr int kRingThreads = 512;
 const void *ring_kernel(int D, int nqt, Dtype dtype, bool precise);
-// The precise D=256 instance that prepares its query from SplitArgs::tok
-// (the fused split of 3..8 tokens; nqt 2 or 3), or nullptr.
-const void *ring_prep_kernel(int nqt);
 
 // The split-K decomposition chosen for one launch of the partial kernel.
 struct SplitPlan {
@@ -99,15 +98,19 @@ void launch_combine(const Shape &s, const SplitPlan &plan, Dtype dtype,
                     const void *workspace, void *out, bool out_f32, const float *gate,
                     hipStream_t stream);
 
-// Fused attention of tok.tokens (1..8) new tokens at tok.position >= 1
-// (24/4/256, fp16 pages) in two launches: the split kernel prepares the
-// queries itself and attends to the cached keys 0 .. position-1; the combine
-// prepares the new keys and values, adds them causally, appends them to the
-// pages and applies the gate.  No prepare launch.  The workspace holds the
-// split's partials (fused_tokens_workspace_bytes).
+// Fused decode of tok.tokens new tokens (up to kMaxFusedSplitTokens) at
+// tok.position >= 1 (24/4/256, fp16 pages) in two launches: the split kernel
+// prepares the query itself, attends to the cached keys 0 .. position-1 and
+// (first split) appends the new key and value; the combine adds the new key
+// and applies the gate.  No prepare launch.  The workspace holds the split's
+// partials and the prepared query rows (fused_tokens_workspace_bytes).
 void launch_fused_tokens(const FusedToken &tok, int capacity, void *workspace, float *out, hipStream_t stream);
 size_t fused_tokens_workspace_bytes(int tokens, int position);
-constexpr int kMaxFusedSplitTokens = 8;
+// One token (decode).  Verification batches of 2..8 tokens take the
+// prepare kernel instead: for 8 tokens at 16K, preparing 48 query rows in
+// the ring kernel's prologue and the new keys in the combine cost more than
+// the launch they save (28.3-32.2 against 28.8 us per layer).
+constexpr int kMaxFusedSplitTokens = 1;
 
 // Chunked prefill: all group*tokens query rows against the pages in one
 // launch (no workspace); `dtype` q and out, [tokens][q_heads][D].  A precise

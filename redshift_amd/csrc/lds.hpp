@@ -16,13 +16,6 @@ __device__ __forceinline__ void wait_vmcnt() {
     __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | (7 << 4) | (15 << 8));
 }
 
-// s_waitcnt lgkmcnt(0) leaving the other counters alone: this wave's LDS
-// stores have completed (ring_barrier does not wait for them).
-__device__ __forceinline__ void wait_lds_stores() {
-    asm volatile("" ::: "memory");
-    __builtin_amdgcn_s_waitcnt(15 | (3 << 14) | (7 << 4));
-}
-
 // LDS byte address of a __shared__ object.
 __device__ __forceinline__ uint32_t lds_addr(const void *p) {
     return (uint32_t)(uintptr_t)(__attribute__((address_space(3))) const void *)p;

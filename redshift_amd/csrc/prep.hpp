@@ -3,7 +3,7 @@
 // pairs (i, i+32), i < 32, by the angle (position+t) * 1e7^(-i/32).  One
 // wave prepares a row.
 #pragma once
-#include "common.hpp"
+#include "kernels.hpp"
 
 #include <cmath>
 
@@ -95,6 +95,39 @@ __device__ __forceinline__ void norm_rope_rows(float (&x)[R][4], const float (&g
         const float cp = lane_xor32(c[r]), sp = lane_xor32(s[r]);
         x[r][0] = lane < 32 ? ((x[r][0] * c[r]) - (other * s[r]))    // a c - b s
                             : ((other * sp) + (x[r][0] * cp));    // a s + b c
+    }
+}
+
+// The fused split kernels' new keys: the inputs of new token j's key for
+// KV head h (its K row, the K gamma, its V row), lane l holding dims
+// 64i + l like the prepare kernel; prepared (RMSNorm, gamma, RoPE with the
+// angle's cosine and sine c, s on lanes < 32) and appended to the pages at
+// position + j with the prepare kernel's functions and rounding, so the same
+// bits.
+struct NewKeyRow {
+    float k[1][4], g[4], v[4];
+};
+__device__ __forceinline__ void load_new_key(NewKeyRow &r, const FusedToken &tok, int kv_heads, int h, int j,
+                                             int lane) {
+    const size_t row = ((size_t)j * kv_heads + h) * kModelHeadDim;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        r.k[0][i] = tok.key[row + 64 * i + lane];
+        r.g[i] = tok.k_norm[64 * i + lane];
+        r.v[i] = tok.value[row + 64 * i + lane];
+    }
+}
+__device__ __forceinline__ void append_new_key(NewKeyRow &r, const FusedToken &tok, int h, int j, float c,
+                                               float s, int lane) {
+    constexpr int D = kModelHeadDim;
+    const float cr[1] = {c}, sr[1] = {s};
+    norm_rope_rows<1>(r.k, r.g, cr, sr, tok.epsilon, lane);
+    _Float16 *kp = static_cast<_Float16 *>(tok.k_pages) + (size_t)h * tok.head_stride;
+    _Float16 *vp = static_cast<_Float16 *>(tok.v_pages) + (size_t)h * tok.head_stride;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        kp[k_page_offset(tok.position + j, 64 * i + lane, D)] = cache_half(r.k[0][i]);
+        vp[v_page_offset(tok.position + j, 64 * i + lane, D)] = cache_half(r.v[i]);
     }
 }
 

@@ -23,7 +23,6 @@
 // more MFMA per fragment and P is split into hi + lo parts as well.
 #include "kernels.hpp"
 #include "lds.hpp"
-#include "prep.hpp"
 
 #include <cmath>
 #include <cstdint>
@@ -68,14 +67,7 @@ constexpr int kRingBuffers = 4;   // NBUF-1 pages in flight while one is consume
 constexpr int kStreamLoad = 2;
 constexpr float kLazy = 8.f;   // lazy row-max threshold, log2 units
 
-// PREP (the fused path's new tokens, precise instance only): the query is
-// prepared here from a.tok instead of read from q: wave w prepares rows
-// w, w + 8, ... (RMSNorm, gamma, RoPE at the row's position: the prepare
-// kernel's functions) while the first pages are in flight and stages them as
-// fp32 in the buffers that otherwise carry the query fragments.  Every row
-// sees the cached keys 0 .. a.position only; the new tokens' own keys are
-// added by the combine.
-template <int D, int NQT, bool PSPLIT, typename KV, bool QSPLIT = false, bool PREP = false>
+template <int D, int NQT, bool PSPLIT, typename KV, bool QSPLIT = false>
 __global__ __launch_bounds__(kRingWaves * kWave, 1)
 void attention_ring(SplitArgs a) {
     using V8 = typename Vec8<KV>::type;
@@ -127,30 +119,10 @@ void attention_ring(SplitArgs a) {
     // is then requested after the fragments have moved to registers.
     const int row = min(16 * qt + (lane & 15), a.rows - 1);
     const int t = row / a.group;
-    const int limit = a.position + (PREP ? 0 : t);                 // last key of this row
-    const int tile_limit = a.position + (PREP ? 0 : min(16 * qt, a.rows - 1) / a.group);
+    const int limit = a.position + t;                            // last key of this row
+    const int tile_limit = a.position + min(16 * qt, a.rows - 1) / a.group;
     static_assert(4 * KS * kWave * 8 <= 2 * PAGE, "query fragments fit one ring buffer");
-    static_assert(!PREP || (QSPLIT && D == 4 * kWave && std::is_same<KV, _Float16>::value),
-                  "the prepared query is the fp32 query of the 256-dim fp16 model");
-    // PREP: rows w + 8r of this wave (lane l holding dims 64i + l), staged
-    // as fp32 rows of D + 4 floats (conflict-free writes and fragment reads)
-    // over buffers NBUF-2 and NBUF-1.
-    constexpr int RPW = PREP ? 2 * NQT : 1;
-    constexpr int kStage = D + 4;
-    static_assert(!PREP || 16 * NQT * kStage * 4 <= 2 * 2 * PAGE * (int)sizeof(KV), "staged rows fit two buffers");
-    float xq[RPW][4], gq[4];
-    if constexpr (PREP) {
-#pragma unroll
-        for (int r = 0; r < RPW; ++r) {
-            const int pr = min(w + kRingWaves * r, a.rows - 1);
-            const int pt = pr / a.group;
-            const float *src = a.tok.q_gate + ((size_t)pt * a.q_heads + h * a.group + pr - pt * a.group) * 2 * D;
-#pragma unroll
-            for (int i = 0; i < 4; ++i) xq[r][i] = src[64 * i + lane];
-        }
-#pragma unroll
-        for (int i = 0; i < 4; ++i) gq[i] = a.tok.q_norm[64 * i + lane];
-    } else if (computes && (kt == 0 || QSPLIT)) {
+    if (computes && (kt == 0 || QSPLIT)) {
         const KV *src = static_cast<const KV *>(kt == 0 ? a.q : a.q_lo) +
                         ((size_t)t * a.q_heads + (size_t)h * a.group + (row - t * a.group)) * D + 8 * g;
         KV *dst = kt == 0 ? ring[NBUF - 1] : ring[NBUF - 2];
@@ -288,28 +260,6 @@ void attention_ring(SplitArgs a) {
         static_for<0, FIRST>([&](auto k) {
             if (decltype(k)::value < n) stage(p0 + decltype(k)::value, ring[decltype(k)::value]);
         });
-        float *staged = reinterpret_cast<float *>(ring[NBUF - 2]);
-        if constexpr (PREP) {
-            const double freq = rope_freq(lane);
-            float cr[RPW], sr[RPW];
-#pragma unroll
-            for (int r = 0; r < RPW; ++r) {
-                cr[r] = 1.f;
-                sr[r] = 0.f;
-                if (lane < 32)
-                    rope_cos_sin(a.tok.position + min(w + kRingWaves * r, a.rows - 1) / a.group, freq, cr[r], sr[r]);
-            }
-            norm_rope_rows<RPW>(xq, gq, cr, sr, a.tok.epsilon, lane);
-#pragma unroll
-            for (int r = 0; r < RPW; ++r) {
-                const int pr = w + kRingWaves * r;
-                if (pr < a.rows) {
-#pragma unroll
-                    for (int i = 0; i < 4; ++i) staged[pr * kStage + 64 * i + lane] = xq[r][i];
-                }
-            }
-            wait_lds_stores();
-        }
         // Step 0: page 0 and the query fragments (loaded first) have landed;
         // the fragments move to registers before the last buffers are
         // refilled with pages.
@@ -320,26 +270,7 @@ void attention_ring(SplitArgs a) {
             });
         }
         ring_barrier();
-        if (PREP && computes) {
-            // Fragment ks of lane l: row 16qt + l%16, dims 32ks + 8(l/16) ..
-            // +7, as hi = fp16(q) and lo = fp16(q - hi); rows past the group
-            // are zero (never stored).
-            const int fr = 16 * qt + (lane & 15);
-            const bool live = fr < a.rows;
-#pragma unroll
-            for (int ks = 0; ks < KS; ++ks) {
-                const float *src = staged + fr * kStage + 32 * ks + 8 * g;
-                const f32x4 q0 = live ? *reinterpret_cast<const f32x4 *>(src) : f32x4{0.f, 0.f, 0.f, 0.f};
-                const f32x4 q1 = live ? *reinterpret_cast<const f32x4 *>(src + 4) : f32x4{0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-                for (int j = 0; j < 8; ++j) {
-                    const float x = j < 4 ? q0[j] : q1[j - 4];
-                    const KV hi = (KV)x;
-                    qf[ks][j] = hi;
-                    qlo[ks][j] = (KV)(x - (float)hi);
-                }
-            }
-        } else if (computes) {
+        if (computes) {
             const uint32_t qbase = lds_addr(ring[NBUF - 1]) + qt * KS * 1024 + lane * 16;
             static_for<0, KS>([&](auto ks) {
                 lds_read<decltype(ks)::value * 1024>(qf[decltype(ks)::value], qbase);
@@ -465,14 +396,6 @@ const void *pick_precise(int nqt) {
         case 2: return (const void *)&attention_ring<D, 2, true, _Float16, true>;
         case 3: return (const void *)&attention_ring<D, 3, true, _Float16, true>;
         case 4: return (const void *)&attention_ring<D, 4, true, _Float16, true>;
-    }
-    return nullptr;
-}
-
-const void *ring_prep_kernel(int nqt) {
-    switch (nqt) {
-        case 2: return (const void *)&attention_ring<256, 2, true, _Float16, true, true>;
-        case 3: return (const void *)&attention_ring<256, 3, true, _Float16, true, true>;
     }
     return nullptr;
 }

@@ -320,12 +320,11 @@ def test_fused_device_path_matches_oracle(gpu):
 @pytest.mark.parametrize('batch,position', [(5, 5000), (8, 20000), (3, 40), (2, 100), (4, 31), (6, 33),
                                             (7, 1)])
 def test_fused_verify_matches_oracle(gpu, batch, position):
-    """Fused batches of 2-8 tokens: the split kernel prepares the queries
-    itself (stream kernel up to 16 rows, the ring kernel's precise instance
-    beyond) over the cached keys, and the combine adds the new keys
-    causally.  Split lengths of 1 to ~11 pages, a first cached page that is
-    full (31 + 1) or holds one key, on the reference's sine-wave fixture and
-    tolerances."""
+    """Fused verification batches of 2-8 tokens (prepare kernel, then the
+    precise split kernels: fp32 query as hi + lo parts) at split lengths of
+    1 to ~11 pages, a first cached page that is full (31 + 1) or holds one
+    key, on the reference's sine-wave fixture and tolerances, with the
+    appended cache rows."""
     torch = gpu
     c = kat.sine_wave_case(batch=batch, position=position)
     expected = ref.fused_attention(c['key_cache'], c['value_cache'], c['q_gate'], c['key'], c['value'],
