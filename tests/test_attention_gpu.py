@@ -117,6 +117,10 @@ def test_fused_decode_matches_oracle(gpu, position):
                                    one['q_norm'], one['k_norm'], 1, position, c['epsilon'])
     capacity = A.round_capacity(position + 2)
     cache = A.PagedKV(4, 256, capacity, torch.float16)
+    # Slots past the prefix hold NaN: the split kernel reads the new token's
+    # slot (masked) while the first split writes it.
+    cache.k.fill_(float('nan'))
+    cache.v.fill_(float('nan'))
     if position:
         cache.pack(torch.from_numpy(c['key_cache']).cuda(), torch.from_numpy(c['value_cache']).cuda())
     dev = [torch.from_numpy(f32(one[name])).cuda() for name in ('q_gate', 'key', 'value', 'q_norm', 'k_norm')]
@@ -128,6 +132,8 @@ def test_fused_decode_matches_oracle(gpu, position):
     assert_close(vc.float().cpu().numpy(), expected[2], 0)
     # The prepared path (a batch of two) appends the same bits for token 0.
     cache2 = A.PagedKV(4, 256, capacity, torch.float16)
+    cache2.k.fill_(float('nan'))
+    cache2.v.fill_(float('nan'))
     if position:
         cache2.pack(torch.from_numpy(c['key_cache']).cuda(), torch.from_numpy(c['value_cache']).cuda())
     dev2 = [torch.from_numpy(f32(c[name])).cuda() for name in ('q_gate', 'key', 'value', 'q_norm', 'k_norm')]
