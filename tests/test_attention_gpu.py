@@ -574,3 +574,31 @@ def test_session_verify_commit_checkpoint_restore(gpu):
     kv.reset()
     with pytest.raises(SessionError, match='no valid checkpoint'):
         kv.restore()
+
+
+def random_shapes(n, seed=2024):
+    """Seeded shapes across both kernels' ranges: KV heads 1-8, groups 1-8,
+    head_dim 128/256, fp16/bf16, 1-24 tokens (split-K up to 48 rows per KV
+    head, the prefill kernel beyond), positions 0-3000, with and without
+    outlier keys."""
+    rng = np.random.default_rng(seed)
+    shapes = []
+    for i in range(n):
+        kv = int(rng.choice([1, 2, 4, 8]))
+        group = int(rng.integers(1, 9))
+        tokens = int(rng.choice([1, 2, 3, 5, 8, 9, 13, 24]))
+        shapes.append((kv * group, kv, int(rng.choice([128, 256])), tokens, int(rng.integers(0, 3001)),
+                       str(rng.choice(['f16', 'bf16'])), int(rng.choice([0, 16])), 900 + i))
+    return shapes
+
+
+@pytest.mark.parametrize('q_heads,kv_heads,head_dim,T,position,dtype,outliers,seed', random_shapes(24))
+def test_random_shapes_against_oracle(gpu, q_heads, kv_heads, head_dim, T, position, dtype, outliers, seed):
+    """qv_attention with float32 output on seeded random shapes, pages past
+    the last key filled with NaN, against the oracle to the full bounds."""
+    outliers = min(outliers, position + T)
+    w = Workload('random', q_heads, kv_heads, head_dim, T, position, 1 / head_dim ** .5, dtype, seed, 1.0, 0.5,
+                 outliers, 8.0)
+    q, k, v, _ = make_inputs(w)
+    want = ref.gqa_attention(to_float(q, dtype), to_float(k, dtype), to_float(v, dtype), position, w.scale)
+    assert_parity(gpu_attention(w, q, k, v, gpu, fill_nan=True, out_dtype=gpu.float32), want)
