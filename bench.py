@@ -281,10 +281,14 @@ def time_kv_copy(torch, A, w, layers, steps, warmup, seed):
     return 1000 * start.elapsed_time(end) / (steps * layers)
 
 
-def cpu_baseline(w, target_s=8.0):
+def cpu_baseline(torch, A, w, target_s=8.0):
     """The numpy fp32 restatement of the reference's CPU attention (oracle),
     one layer's decode, timed single-threaded and on all host cores (capped
-    at 16 threads): median of at least 5 calls, about target_s each."""
+    at 16 threads): median of at least 5 calls, about target_s each.
+
+    The same layer also runs once through the HIP path, and its output is
+    checked against the oracle's within max-abs 2e-3 and relative L2 1e-3
+    (`check`); a result outside them ends the bench with an error."""
     import numpy as np
     from threadpoolctl import threadpool_info, threadpool_limits
 
@@ -293,10 +297,12 @@ def cpu_baseline(w, target_s=8.0):
 
     q, k, v, _ = make_inputs(w)
     k32, v32 = k.astype(np.float32), v.astype(np.float32)
+    expected = None
 
     def run(threads):
+        nonlocal expected
         with threadpool_limits(limits=threads):
-            gqa_attention_fp32(q, k32, v32, w.position, w.scale)   # warm-up
+            expected = gqa_attention_fp32(q, k32, v32, w.position, w.scale)   # warm-up
             times = []
             t_end = time.perf_counter() + target_s
             while len(times) < 5 or time.perf_counter() < t_end:
@@ -318,6 +324,7 @@ def cpu_baseline(w, target_s=8.0):
     blas = next((f"{i['internal_api']} {i['version']}" for i in threadpool_info()
                  if i.get('user_api') == 'blas'), 'unknown')
     gbs = lambda sec: round(w.kv_bytes() / sec / 1e9, 3)
+    check = gpu_check(torch, A, w, q, k, v, expected)
     return {
         'value': gbs(many), 'unit': 'GB/s', 'cores': threads, 'kind': 'port',
         'us_per_layer': round(many * 1e6, 1),
@@ -325,7 +332,28 @@ def cpu_baseline(w, target_s=8.0):
         'sample': f'median of {n_many} ({threads} threads) and {n_one} (1 thread) single-layer {w.name} '
                   f'calls: {w.keys} keys, 24/4/256, fp16 cache widened to fp32 before timing, fp32 BLAS '
                   f'({blas}) per KV group; host {model}, {host} cores in affinity',
+        'check': check,
     }
+
+
+def gpu_check(torch, A, w, q, k, v, expected):
+    """The HIP path on the baseline's inputs (one layer, its own cache),
+    compared with the oracle's fp32 output."""
+    import numpy as np
+
+    dtype = torch.bfloat16 if w.dtype == 'bf16' else torch.float16
+    to_dev = lambda x: torch.from_numpy(np.ascontiguousarray(x)).to('cuda')
+    cache = A.PagedKV(w.kv_heads, w.head_dim, A.round_capacity(w.keys), dtype)
+    cache.pack(to_dev(k).to(dtype), to_dev(v).to(dtype))
+    got = A.attention(to_dev(q).to(dtype), cache, w.position, w.scale).float().cpu().numpy()
+    del cache
+    torch.cuda.empty_cache()
+    diff = got.astype(np.float64) - expected.astype(np.float64)
+    max_abs = float(np.abs(diff).max())
+    rel_l2 = float(np.linalg.norm(diff) / np.linalg.norm(expected.astype(np.float64)))
+    ok = bool(np.isfinite(got).all() and max_abs <= 2e-3 and rel_l2 <= 1e-3)
+    return {'against': 'oracle fp32 output on the same inputs', 'max_abs': max_abs, 'rel_l2': rel_l2,
+            'tol_max_abs': 2e-3, 'tol_rel_l2': 1e-3, 'ok': ok}
 
 
 def main():
@@ -454,8 +482,11 @@ def main():
         result['extra'] = extra
     if not args.no_cpu:
         log('cpu baseline (numpy fp32, 1 thread, one layer)')
-        result['cpu_baseline'] = cpu_baseline(w)
+        result['cpu_baseline'] = cpu_baseline(torch, A, w)
     print(json.dumps(result), flush=True)
+    if 'cpu_baseline' in result and not result['cpu_baseline']['check']['ok']:
+        sys.exit('bench: the HIP output differs from the oracle beyond tolerance: '
+                 + json.dumps(result['cpu_baseline']['check']))
 
 
 if __name__ == '__main__':
