@@ -149,6 +149,23 @@ int qv_attention_combine(void *out, int dtype, int out_dtype, int q_heads, int k
                          int tokens, int position, const void *workspace,
                          uint64_t workspace_bytes, void *stream);
 
+/* Workspace bytes of qv_attention_precise for this shape. */
+int qv_attention_precise_workspace(uint64_t *bytes, int q_heads, int kv_heads, int head_dim,
+                                   int tokens, int position);
+/* The raw core at the reference's own precision: an fp32 query on fp16
+ * pages, fp32 output.  The reference's attention kernels read q as fp32
+ * (written by attn_prepare, src/kernels.cu:416-434, read at :435-503) from
+ * fp16 caches.  The library splits q into fp16 parts hi = fp16(q) and
+ * lo = fp16(q - hi), staged at the start of the workspace, and multiplies
+ * both by K; P multiplies V as hi + lo parts too.  The parts hold q to
+ * about 22 significant bits: |q| < 65504, error at most
+ * 2^-25 + 2^-22 |q|.  q and out: [tokens][q_heads][head_dim] float32;
+ * shapes, limits and kernels otherwise as qv_attention. */
+int qv_attention_precise(float *out, const float *q, const void *k_pages, const void *v_pages,
+                         int q_heads, int kv_heads, int head_dim, int tokens, int position,
+                         int capacity, float scale, void *workspace, uint64_t workspace_bytes,
+                         void *stream);
+
 /* Workspace bytes of qv_attention_fused for this batch/position. */
 int qv_attention_fused_workspace(uint64_t *bytes, int batch, int position);
 /* Device-side drop-in for the reference's k_attention (src/kernels.cu:575-580)

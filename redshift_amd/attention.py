@@ -123,6 +123,39 @@ def attention(q, cache, position, scale, out=None, ws=None, out_dtype=None):
     return out
 
 
+def precise_workspace_bytes(q_heads, kv_heads, head_dim, tokens, position):
+    lib = library()
+    size = ct.c_uint64()
+    check(lib, lib.qv_attention_precise_workspace(ct.byref(size), q_heads, kv_heads, head_dim, tokens, position))
+    return size.value
+
+
+def attention_precise(q, cache, position, scale, out=None, ws=None):
+    """Raw causal GQA attention at the reference's precision: a float32
+    query [tokens][q_heads][head_dim] on an fp16 cache, float32 output
+    (qv_attention_precise; the library splits q into fp16 hi + lo parts)."""
+    lib = library()
+    _require(q.dim() == 3, 'q must be [tokens, q_heads, head_dim]')
+    _require(q.dtype == torch.float32, f'q must be float32, not {q.dtype}')
+    _require(cache.dtype == torch.float16, 'the precise path runs on an fp16 cache')
+    _require(q.shape[2] == cache.head_dim, f'q has head_dim {q.shape[2]}, the cache {cache.head_dim}')
+    _same_device([('q', q)], cache.k.device)
+    q = q.contiguous()
+    tokens, q_heads, head_dim = q.shape
+    if out is None:
+        out = torch.empty(q.shape, dtype=torch.float32, device=q.device)
+    _require(tuple(out.shape) == tuple(q.shape) and out.dtype == torch.float32 and out.is_contiguous(),
+             f'out must be a contiguous float32 tensor of shape {tuple(q.shape)}')
+    _same_device([('out', out)], q.device)
+    if ws is None:
+        ws = workspace(precise_workspace_bytes(q_heads, cache.kv_heads, head_dim, tokens, position), q.device)
+    _same_device([('workspace', ws)], cache.k.device)
+    check(lib, lib.qv_attention_precise(_ptr(out), _ptr(q), _ptr(cache.k), _ptr(cache.v), q_heads,
+                                        cache.kv_heads, head_dim, tokens, position, cache.capacity,
+                                        float(scale), _ptr(ws), _nbytes(ws), _stream()))
+    return out
+
+
 def _check_query(q, cache):
     """The query must be [tokens, q_heads, head_dim] of the cache's 16-bit
     type on the cache's device (the library sees untyped pointers)."""
@@ -171,11 +204,10 @@ def fused_workspace_bytes(batch, position):
     return size.value
 
 
-def attention_fused(q_gate, key, value, q_norm, k_norm, cache, position, epsilon, out=None, ws=None):
-    """Device-side fused attention of the fixed 24/4/256 model (the reference's
-    k_attention): prepares q/k, appends k/v at position.., attends and gates.
-    All inputs float32 device tensors; `cache` is an fp16 PagedKV(4, 256, ...)."""
-    lib = library()
+def check_fused_inputs(q_gate, key, value, q_norm, k_norm, cache):
+    """The fused entry's tensors: float32 q_gate [batch][24][512], key and
+    value [batch][4][256], q_norm and k_norm [256] on the device of `cache`,
+    an fp16 PagedKV(4, 256, ...).  Returns the named tensors."""
     _require((cache.dtype, cache.kv_heads, cache.head_dim) == (torch.float16, 4, 256),
              'the fused path runs on an fp16 PagedKV(4, 256, ...)')
     batch = q_gate.shape[0]
@@ -187,6 +219,16 @@ def attention_fused(q_gate, key, value, q_norm, k_norm, cache, position, epsilon
         _require(t.numel() == torch.Size(shapes[name]).numel(),
                  f'{name} must hold {shapes[name]} values, not {tuple(t.shape)}')
     _same_device(named, cache.k.device)
+    return named
+
+
+def attention_fused(q_gate, key, value, q_norm, k_norm, cache, position, epsilon, out=None, ws=None):
+    """Device-side fused attention of the fixed 24/4/256 model (the reference's
+    k_attention): prepares q/k, appends k/v at position.., attends and gates.
+    All inputs float32 device tensors; `cache` is an fp16 PagedKV(4, 256, ...)."""
+    lib = library()
+    named = check_fused_inputs(q_gate, key, value, q_norm, k_norm, cache)
+    batch = q_gate.shape[0]
     if out is None:
         out = torch.empty((batch, 24, 256), dtype=torch.float32, device=q_gate.device)
     _require(out.dtype == torch.float32 and out.numel() == batch * 24 * 256 and out.is_contiguous(),

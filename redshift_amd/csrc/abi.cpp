@@ -434,6 +434,44 @@ extern "C" int qv_attention_combine(void *out, int dtype, int out_dtype, int q_h
     });
 }
 
+// qv_attention_precise: the query's fp16 hi and lo parts (2 * tokens *
+// q_heads * head_dim halves, rounded up to 256 bytes), then the partials of
+// the precise kernel instances.
+static size_t precise_query_bytes(const rs::Shape &s) {
+    return align256((size_t)2 * s.tokens * s.q_heads * s.head_dim * sizeof(uint16_t));
+}
+static size_t precise_workspace(const rs::Shape &s) {
+    return precise_query_bytes(s) + rs::attention_workspace_bytes(s, rs::Dtype::F16, true);
+}
+
+extern "C" int qv_attention_precise_workspace(uint64_t *bytes, int q_heads, int kv_heads, int head_dim,
+                                              int tokens, int position) {
+    return call([&] {
+        require(bytes != nullptr, "null bytes output");
+        *bytes = precise_workspace(attention_shape(q_heads, kv_heads, head_dim, tokens, position, 0));
+    });
+}
+
+extern "C" int qv_attention_precise(float *out, const float *q, const void *k_pages, const void *v_pages,
+                                    int q_heads, int kv_heads, int head_dim, int tokens, int position,
+                                    int capacity, float scale, void *workspace, uint64_t workspace_bytes,
+                                    void *stream) {
+    return call([&] {
+        const rs::Shape s = attention_shape(q_heads, kv_heads, head_dim, tokens, position, capacity);
+        fits_cache(s);
+        require(std::isfinite(scale), "scale must be finite");
+        require(workspace != nullptr, "null attention buffer");
+        raw_buffers(out, q, k_pages, v_pages, workspace);
+        require(workspace_bytes >= precise_workspace(s), "workspace too small");
+        hipStream_t st = static_cast<hipStream_t>(stream);
+        const size_t n = (size_t)s.tokens * s.q_heads * s.head_dim;
+        uint16_t *q_hilo = static_cast<uint16_t *>(workspace);
+        rs::launch_split_query(q_hilo, q, n, st);
+        run_attention(s, rs::Dtype::F16, true, scale, q_hilo, q_hilo + n, k_pages, v_pages,
+                      static_cast<char *>(workspace) + precise_query_bytes(s), out, true, nullptr, st);
+    });
+}
+
 // The query's hi + lo parts, then the partials.
 static size_t fused_query_bytes(int batch) {
     return align256((size_t)batch * rs::kModelQHeads * rs::kModelHeadDim * sizeof(float));
@@ -467,8 +505,8 @@ extern "C" int qv_attention_fused(float *out, void *k_pages, void *v_pages,
         constexpr int H = rs::kModelQHeads, HKV = rs::kModelKvHeads, D = rs::kModelHeadDim;
         const rs::Shape s{H, HKV, D, batch, position, capacity};
         fits_cache(s);
-        require(aligned16(q_gate) && aligned16(workspace) && aligned16(k_pages) && aligned16(v_pages),
-                "attention buffers must be 16-byte aligned");
+        require(aligned16(out) && aligned16(q_gate) && aligned16(workspace) && aligned16(k_pages) &&
+                aligned16(v_pages), "attention buffers must be 16-byte aligned");
         require(workspace_bytes >= fused_workspace(batch, position), "workspace too small");
         hipStream_t st = static_cast<hipStream_t>(stream);
         uint16_t *q = static_cast<uint16_t *>(workspace);   // hi then lo fp16 parts

@@ -19,20 +19,15 @@
 //                     its own run of pages with a private softmax state; the
 //                     four waves merge through LDS once at the end (one
 //                     barrier: each wave's state in its own slot).
-//   attention_coop    up to three query tiles (<= 48 rows, verification).
-//                     Eight waves split each 128-key block (four pages) by
-//                     keys for Q.K^T and by head dims for P.V, exchanging the
-//                     block max and the P fragments through LDS, so the 48-row
-//                     accumulators are spread over the waves instead of
-//                     replicated.
+//   attention_ring    (ring.hip) 17..48 rows (verification): eight waves
+//                     share a ring of LDS page buffers filled by direct
+//                     global->LDS loads.
 #include "combine.hpp"
 #include "kernels.hpp"
 #include "prep.hpp"
 
 #include <algorithm>
 #include <cmath>
-#include <cstdlib>
-#include <cstring>
 #include <mutex>
 #include <type_traits>
 #include <vector>
@@ -44,12 +39,6 @@ template <typename T> struct Vec8;
 template <> struct Vec8<_Float16> { using type = f16x8; };
 template <> struct Vec8<__bf16> { using type = bf16x8; };
 
-typedef _Float16 f16x4 __attribute__((ext_vector_type(4)));
-typedef __bf16 bf16x4 __attribute__((ext_vector_type(4)));
-template <typename T> struct Vec4;
-template <> struct Vec4<_Float16> { using type = f16x4; };
-template <> struct Vec4<__bf16> { using type = bf16x4; };
-
 __device__ __forceinline__ f32x4 mfma(f16x8 a, f16x8 b, f32x4 c) {
     return __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, c, 0, 0, 0);
 }
@@ -59,7 +48,6 @@ __device__ __forceinline__ f32x4 mfma(bf16x8 a, bf16x8 b, f32x4 c) {
 
 constexpr int kWaves = 4;          // waves per workgroup of the partial kernels
 constexpr int kMaxSplits = 1024;   // bound on workgroups per KV head
-constexpr int kCoopWaves = 8;      // waves per workgroup of attention_coop
 
 // Query fragments (B operand of S^T): fragment (i, qt, ks) of lane l holds
 // row 16*qt + l%16, dims 32*ks + 8*(l/16) .. +7 of the hi (i = 0) or lo (i = 1,
@@ -226,6 +214,15 @@ void attention_stream(SplitArgs a) {
             x[r] = s0[r] * a.scale_log2;
             x[4 + r] = s1[r] * a.scale_log2;
         }
+        // Keys past a row's last visible key score -inf.  The fused decode
+        // (PREP) relies on this mask and on the value zeroing below: the
+        // first split appends the new key and value at key `position + 1`
+        // of the page it streams while other workgroups read that page,
+        // and every PREP row's limit is `position` (the last cached key,
+        // n_keys = position + 1), so whatever such a read returns for that
+        // slot is masked here and its value zeroed.  A change to either
+        // mask (or to which keys the split covers) must keep that slot
+        // invisible.
         if (b * 32 + 31 > a.position) {
 #pragma unroll
             for (int j = 0; j < 8; ++j)
@@ -259,6 +256,7 @@ void attention_stream(SplitArgs a) {
         for (int dt = 0; dt < DT; ++dt) acc[dt] *= alpha;
         if (b * 32 + 32 > a.n_keys) {
             // Zero V slots past the last key: 0 * (stale NaN) would poison O.
+            // (The fused decode's appended value sits in such a slot.)
 #pragma unroll
             for (int j = 0; j < 8; ++j) {
                 if (b * 32 + v_slot_token(lane >> 4, j) >= a.n_keys) {
@@ -278,13 +276,14 @@ void attention_stream(SplitArgs a) {
     // head's last page), so every wave issues it before waiting on the query.
     load_k(min(wi, a.n_pages - 1));
     // PREP: the prepared rows are staged in LDS as fp32, row-major with a
-    // stride of D + 4 floats (in the merge slots, which the page loop does
-    // not use), so the writes (lane l: dims 64i + l) and the fragment reads
-    // (16 rows, 32 bytes each) are both free of bank conflicts; hi and lo
-    // parts are split while gathering.
+    // stride of D + 4 floats, in the query-fragment buffer (which PREP does
+    // not otherwise use, and which nothing writes after the gather), so the
+    // writes (lane l: dims 64i + l) and the fragment reads (16 rows, 32
+    // bytes each) are both free of bank conflicts; hi and lo parts are split
+    // while gathering.
     constexpr int kStage = D + 4;
-    static_assert(!PREP || 16 * kStage * sizeof(float) <= sizeof(so), "the staged rows fit the merge slots");
-    float *stage = reinterpret_cast<float *>(so);
+    static_assert(!PREP || kWaves * PR * kStage * sizeof(float) <= sizeof(sq), "the staged rows fit the query buffer");
+    float *stage = reinterpret_cast<float *>(sq);
     if constexpr (PREP) {
         const double freq = rope_freq(lane);
         if (prows) {
@@ -380,262 +379,6 @@ void attention_stream(SplitArgs a) {
     }
 }
 
-// ---------------------------------------------------------------------------
-// attention_coop: NQT query tiles (up to 48 rows), WAVES waves per workgroup.
-// A split owns a contiguous run of pages, walked WAVES/2 pages (a block of
-// 16*WAVES keys) per step:
-//   * wave w computes S^T for the 16 keys of tile w of the block, all rows;
-//   * the block max per row is exchanged through LDS; every wave derives the
-//     same running max, so all waves scale their P values alike;
-//   * wave w writes its P values into the shared P^T operands (LDS) and then
-//     computes O^T for head dims w*D/WAVES .. +D/WAVES-1, all rows.
-// Row sums add across waves without rescaling; no O merge is needed.
-//
-// Register budget (two waves per SIMD): the query fragments live in LDS and
-// are read per use; each wave holds its own accumulators (NQT * D/WAVES dims)
-// and two register sets of KV operands, so the next block's loads stay in
-// flight across both barriers of the current block.  All loads are issued
-// unconditionally (pages past the split are clamped and masked), so every path
-// through the loop issues the same loads.
-//
-// The running max moves lazily: only when a block max exceeds it by more than
-// kLazy (log2 units).  P = exp2(s - m) then stays below 2^kLazy, exact in fp16
-// and bf16, and the accumulator rescale is skipped (wave-uniform branch) for
-// most blocks.
-// ---------------------------------------------------------------------------
-constexpr float kLazy = 8.f;
-
-template <int D, int NQT, bool QSPLIT, bool PSPLIT, typename KV, int WAVES>
-__global__ __launch_bounds__(WAVES * kWave, 2)
-void attention_coop(SplitArgs a) {
-    using V8 = typename Vec8<KV>::type;
-    using V4 = typename Vec4<KV>::type;
-    constexpr int KS = D / 32, NQ = QSPLIT ? 2 : 1, NP = PSPLIT ? 2 : 1;
-    constexpr int PAGES = WAVES / 2;              // pages per block
-    constexpr int DTW = D / (16 * WAVES);         // head-dim tiles per wave in P.V
-    constexpr int NQF = NQ * NQT * KS;            // query fragments
-    constexpr int QPW = (NQF + WAVES - 1) / WAVES;   // query fragments per wave
-    static_assert(DTW >= 1, "each wave owns at least one 16-dim tile");
-    __shared__ V8 sq[NQF * kWave];                // query fragments
-    __shared__ V8 sp[NP][PAGES][NQT][kWave];      // P^T operands of the block's pages
-    __shared__ float smax[WAVES][16 * NQT];       // per-wave block max per row
-    __shared__ float sl[WAVES][16 * NQT];         // row sums, exchanged once at the end
-
-    const int lane = threadIdx.x & 63, w = threadIdx.x >> 6, g = lane >> 4;
-    const int split = blockIdx.x % a.splits, h = blockIdx.x / a.splits;
-
-    // Query fragments: wave w fetches fragments w, w+WAVES, ... and the
-    // workgroup shares them through LDS.  This happens before any KV load:
-    // once the KV loads of every workgroup are queued in the memory system, a
-    // query line requested behind them waits for the whole flood.
-#pragma unroll
-    for (int i = 0; i < QPW; ++i) {
-        const int e = min(w + WAVES * i, NQF - 1);
-        const int ks = e % KS, qt = (e / KS) % NQT, lo = e / (KS * NQT);
-        const int row = min(16 * qt + (lane & 15), a.rows - 1);   // padded rows repeat the last
-        const int t = row / a.group, gg = row - t * a.group;
-        const V8 frag = *reinterpret_cast<const V8 *>(static_cast<const KV *>(lo ? a.q_lo : a.q) +
-                                                      ((size_t)t * a.q_heads + (size_t)h * a.group + gg) * D +
-                                                      32 * ks + 8 * g);
-        if (w + WAVES * i < NQF) sq[(w + WAVES * i) * kWave + lane] = frag;
-    }
-
-    const int p0 = (int)((long long)split * a.n_pages / a.splits);
-    const int p1 = (int)((long long)(split + 1) * a.n_pages / a.splits);
-    const int n_steps = (p1 - p0 + PAGES - 1) / PAGES;
-    const KV *kh = static_cast<const KV *>(a.k_pages) + (size_t)h * a.head_stride + lane * 8;
-    const KV *vh = static_cast<const KV *>(a.v_pages) + (size_t)h * a.head_stride + lane * 8;
-
-    int limit[NQT];   // last visible key of row 16*qt + lane%16
-#pragma unroll
-    for (int qt = 0; qt < NQT; ++qt)
-        limit[qt] = a.position + min(16 * qt + (lane & 15), a.rows - 1) / a.group;
-
-    f32x4 acc[NQT][DTW];
-    float m[NQT], l[NQT];
-#pragma unroll
-    for (int qt = 0; qt < NQT; ++qt) {
-        m[qt] = -INFINITY;
-        l[qt] = 0.f;
-#pragma unroll
-        for (int d = 0; d < DTW; ++d) acc[qt][d] = f32x4{0.f, 0.f, 0.f, 0.f};
-    }
-
-    struct Block {
-        V8 k[KS];             // this wave's 16-key tile (A operand of S^T)
-        V8 v[PAGES][DTW];     // this wave's head dims of every page (A operand of O^T)
-    };
-    auto load_block = [&](int step, Block &B) {
-        step = min(step, n_steps - 1);
-        const int page = min(p0 + step * PAGES + (w >> 1), p1 - 1);
-        const KV *kp = kh + (size_t)page * 32 * D + (w & 1) * 16 * D;
-#pragma unroll
-        for (int ks = 0; ks < KS; ++ks) B.k[ks] = *reinterpret_cast<const V8 *>(kp + ks * 512);
-#pragma unroll
-        for (int kk = 0; kk < PAGES; ++kk) {
-            const int pg = min(p0 + step * PAGES + kk, p1 - 1);
-            const KV *vp = vh + (size_t)pg * 32 * D + w * DTW * 512;
-#pragma unroll
-            for (int d = 0; d < DTW; ++d) B.v[kk][d] = *reinterpret_cast<const V8 *>(vp + d * 512);
-        }
-    };
-
-    auto process = [&](int step, Block &cur) {
-        const int pb = p0 + step * PAGES;                         // first page of the block
-        // ---- S^T for this wave's 16 keys, all rows ----
-        f32x4 s[NQT];
-#pragma unroll
-        for (int qt = 0; qt < NQT; ++qt) s[qt] = f32x4{0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-        for (int ks = 0; ks < KS; ++ks) {
-#pragma unroll
-            for (int qt = 0; qt < NQT; ++qt) {
-                s[qt] = mfma(cur.k[ks], sq[(qt * KS + ks) * kWave + lane], s[qt]);
-                if constexpr (QSPLIT) s[qt] = mfma(cur.k[ks], sq[((NQT + qt) * KS + ks) * kWave + lane], s[qt]);
-            }
-        }
-        // Keys of register r: key0 + r.  Edge blocks (past the split, or
-        // holding keys past some row's limit) are masked; others only scaled.
-        const int page = pb + (w >> 1);
-        const int key0 = page * 32 + 16 * (w & 1) + 4 * g;
-        const bool edge = pb + PAGES > p1 || (pb + PAGES) * 32 - 1 > a.position;
-        float x[NQT][4];
-#pragma unroll
-        for (int qt = 0; qt < NQT; ++qt) {
-#pragma unroll
-            for (int r = 0; r < 4; ++r) x[qt][r] = s[qt][r] * a.scale_log2;
-            if (edge) {
-#pragma unroll
-                for (int r = 0; r < 4; ++r)
-                    if (page >= p1 || key0 + r > limit[qt]) x[qt][r] = -INFINITY;
-            }
-            float wm = fmaxf(fmaxf(x[qt][0], x[qt][1]), fmaxf(x[qt][2], x[qt][3]));
-            wm = fmaxf(wm, __shfl_xor(wm, 16, kWave));
-            wm = fmaxf(wm, __shfl_xor(wm, 32, kWave));
-            if (lane < 16) smax[w][16 * qt + lane] = wm;
-        }
-        lds_barrier();   // (1) block maxima visible
-
-        float alpha[NQT];
-        bool rescale = false;
-#pragma unroll
-        for (int qt = 0; qt < NQT; ++qt) {
-            const int row = 16 * qt + (lane & 15);
-            float bm = smax[0][row];
-#pragma unroll
-            for (int ww = 1; ww < WAVES; ++ww) bm = fmaxf(bm, smax[ww][row]);
-            alpha[qt] = 1.f;
-            if (bm > m[qt] + kLazy) {   // also the first finite block max of a row
-                alpha[qt] = __builtin_amdgcn_exp2f(m[qt] - bm);
-                m[qt] = bm;
-                rescale = true;
-            }
-            const float mu = m[qt] == -INFINITY ? 0.f : m[qt];   // fully masked so far
-            V4 ph, pl;
-            float ps = 0.f;
-#pragma unroll
-            for (int r = 0; r < 4; ++r) {
-                const float e = __builtin_amdgcn_exp2f(x[qt][r] - mu);
-                const KV eh = (KV)e;
-                ph[r] = eh;
-                if constexpr (PSPLIT) {
-                    pl[r] = (KV)(e - (float)eh);
-                    ps += e;
-                } else {
-                    ps += (float)eh;   // normalise by the weights actually applied
-                }
-            }
-            l[qt] = l[qt] * alpha[qt] + ps;
-            // Slots 4*(w%2) .. +3 of the P^T operand of page w/2 hold these keys.
-            *reinterpret_cast<V4 *>(reinterpret_cast<KV *>(&sp[0][w >> 1][qt][lane]) + 4 * (w & 1)) = ph;
-            if constexpr (PSPLIT)
-                *reinterpret_cast<V4 *>(reinterpret_cast<KV *>(&sp[NP - 1][w >> 1][qt][lane]) + 4 * (w & 1)) = pl;
-        }
-        lds_barrier();   // (2) P^T operands visible
-
-        // ---- O^T for this wave's head dims, all rows ----
-        if (__any(rescale)) {
-#pragma unroll
-            for (int qt = 0; qt < NQT; ++qt)
-#pragma unroll
-                for (int d = 0; d < DTW; ++d) acc[qt][d] *= alpha[qt];
-        }
-        if ((pb + PAGES) * 32 > a.n_keys || pb + PAGES > p1) {
-            // Zero V slots of keys past the last key or pages past the split
-            // (stale or re-read data): 0 * (stale NaN) would poison O.
-#pragma unroll
-            for (int kk = 0; kk < PAGES; ++kk)
-#pragma unroll
-                for (int j = 0; j < 8; ++j)
-                    if (pb + kk >= p1 || (pb + kk) * 32 + v_slot_token(g, j) >= a.n_keys) {
-#pragma unroll
-                        for (int d = 0; d < DTW; ++d) cur.v[kk][d][j] = (KV)0.f;
-                    }
-        }
-#pragma unroll
-        for (int kk = 0; kk < PAGES; ++kk) {
-#pragma unroll
-            for (int qt = 0; qt < NQT; ++qt) {
-                const V8 pf = sp[0][kk][qt][lane];
-#pragma unroll
-                for (int d = 0; d < DTW; ++d) acc[qt][d] = mfma(cur.v[kk][d], pf, acc[qt][d]);
-                if constexpr (PSPLIT) {
-                    const V8 pfl = sp[NP - 1][kk][qt][lane];
-#pragma unroll
-                    for (int d = 0; d < DTW; ++d) acc[qt][d] = mfma(cur.v[kk][d], pfl, acc[qt][d]);
-                }
-            }
-        }
-    };
-
-    // The first two blocks are requested together; afterwards a register set
-    // is refilled as soon as its block has been consumed, so the memory system
-    // always holds the next block of every workgroup.  The step count is the
-    // same for every wave of the workgroup, so the (uniform) breaks keep all
-    // waves at the same barriers.
-    lds_barrier();   // query fragments visible
-    if (n_steps > 0) {
-        Block S0, S1;
-        load_block(0, S0);
-        load_block(1, S1);
-        for (int j = 0;; j += 2) {
-            process(j, S0);
-            if (j + 1 >= n_steps) break;
-            load_block(j + 2, S0);
-            process(j + 1, S1);
-            if (j + 2 >= n_steps) break;
-            load_block(j + 3, S1);
-        }
-    }
-
-    // ---- partial results: O rows (this wave's dims), m and l ----
-#pragma unroll
-    for (int qt = 0; qt < NQT; ++qt) {
-        l[qt] += __shfl_xor(l[qt], 16, kWave);
-        l[qt] += __shfl_xor(l[qt], 32, kWave);
-        if (lane < 16) sl[w][16 * qt + lane] = l[qt];
-    }
-    lds_barrier();
-    float *pml = a.part_ml + ((size_t)h * a.splits + split) * 2 * a.rows;
-    float *po = a.part_o + ((size_t)h * a.splits + split) * a.rows * D;
-#pragma unroll
-    for (int qt = 0; qt < NQT; ++qt) {
-        const int row = 16 * qt + (lane & 15);
-        if (row < a.rows) {
-            if (w == 0 && lane < 16) {
-                float L = 0.f;
-#pragma unroll
-                for (int ww = 0; ww < WAVES; ++ww) L += sl[ww][row];
-                pml[row] = m[qt];
-                pml[a.rows + row] = L;
-            }
-#pragma unroll
-            for (int d = 0; d < DTW; ++d)
-                __builtin_nontemporal_store(acc[qt][d], reinterpret_cast<f32x4 *>(po + (size_t)row * D + (w * DTW + d) * 16 + 4 * g));
-        }
-    }
-}
-
 struct CombineArgs {
     const void *part_o;   // float or _Float16 rows (SplitPlan::half_parts)
     const float *part_ml;
@@ -656,19 +399,14 @@ void attention_combine(CombineArgs c) {
                                        scratch, c.out, c.gate, OUT, &c.tok, c.scale_log2);
 }
 
-// Kernel instance for a plan.  Raw fp16: 16-bit P; raw bf16: hi+lo P (bf16's
-// 8-bit significand would otherwise dominate the error); fused (fp32 q):
-// hi+lo q and hi+lo P.
-template <int D, int NQT>
-const void *pick(bool stream, Dtype dtype, bool precise) {
-    if (stream) {
-        if (precise) return (const void *)&attention_stream<D, true, true, _Float16, false>;
-        if (dtype == Dtype::BF16) return (const void *)&attention_stream<D, false, true, __bf16, false>;
-        return (const void *)&attention_stream<D, false, false, _Float16, false>;
-    }
-    if (precise) return (const void *)&attention_coop<D, NQT, true, true, _Float16, kCoopWaves>;
-    if (dtype == Dtype::BF16) return (const void *)&attention_coop<D, NQT, false, true, __bf16, kCoopWaves>;
-    return (const void *)&attention_coop<D, NQT, false, false, _Float16, kCoopWaves>;
+// attention_stream instance: raw fp16 multiplies V by a 16-bit P; raw bf16
+// by hi + lo P (bf16's 8-bit significand alone would dominate the error); a
+// precise query (fp32 as fp16 hi + lo parts) takes hi + lo P as well.
+template <int D>
+const void *stream_kernel(Dtype dtype, bool precise) {
+    if (precise) return (const void *)&attention_stream<D, true, true, _Float16, false>;
+    if (dtype == Dtype::BF16) return (const void *)&attention_stream<D, false, true, __bf16, false>;
+    return (const void *)&attention_stream<D, false, false, _Float16, false>;
 }
 
 template <int D, typename PT, bool NT>
@@ -680,8 +418,8 @@ const void *combine_kernel(Dtype dtype, bool out_f32, bool gated) {
 }
 
 // fp16 partial rows come only from the ring kernel, which stores them
-// non-temporally; fp32 ones are non-temporal from the ring and coop kernels
-// and default-policy from attention_stream.
+// non-temporally; fp32 ones are non-temporal from the ring kernel and
+// default-policy from attention_stream.
 template <int D>
 const void *combine_kernel(Dtype dtype, bool out_f32, bool gated, bool half_parts, bool nt_parts) {
     if (half_parts) return combine_kernel<D, _Float16, true>(dtype, out_f32, gated);
@@ -695,45 +433,9 @@ const void *split_kernel(const SplitPlan &p, int D, Dtype dtype, bool precise) {
         require(k != nullptr, "unsupported head_dim / query rows for the ring kernel");
         return k;
     }
-    const bool stream = p.kind == SplitKind::Stream;
-    if (D == 256) {
-        switch (p.nqt) {
-            case 1: return pick<256, 1>(stream, dtype, precise);
-            case 2: return pick<256, 2>(false, dtype, precise);
-            case 3: return pick<256, 3>(false, dtype, precise);
-        }
-    } else if (D == 128) {
-        switch (p.nqt) {
-            case 1: return pick<128, 1>(stream, dtype, precise);
-            case 2: return pick<128, 2>(false, dtype, precise);
-            case 3: return pick<128, 3>(false, dtype, precise);
-        }
-    }
-    throw std::invalid_argument("unsupported head_dim / query rows for the split kernel");
-}
-
-// Kernel of a plan: one query tile (decode) runs attention_stream, more run
-// attention_ring (16-bit queries, and fp32 ones as hi + lo parts).
-// RS_DECODE_KERNEL=coop|ring and RS_VERIFY_KERNEL=coop pick the alternatives
-// (for measurement).
-SplitKind env_kind(const char *name, SplitKind fallback) {
-    const char *v = std::getenv(name);
-    if (v && std::strcmp(v, "coop") == 0) return SplitKind::Coop;
-    if (v && std::strcmp(v, "ring") == 0) return SplitKind::Ring;
-    if (v && std::strcmp(v, "stream") == 0) return SplitKind::Stream;
-    return fallback;
-}
-
-SplitKind kind_for(int nqt, bool precise) {
-    static const SplitKind decode = env_kind("RS_DECODE_KERNEL", SplitKind::Stream);
-    static const SplitKind verify = [] {
-        const SplitKind k = env_kind("RS_VERIFY_KERNEL", SplitKind::Ring);
-        return k == SplitKind::Stream ? SplitKind::Ring : k;
-    }();
-    const SplitKind k = nqt == 1 ? decode : verify;
-    // One query tile of fp32 (hi + lo) queries streams; several use the
-    // ring kernel's precise instance (the fused model path, fp16, D=256).
-    return precise && k == SplitKind::Ring && nqt == 1 ? SplitKind::Stream : k;
+    if (D == 256) return stream_kernel<256>(dtype, precise);
+    if (D == 128) return stream_kernel<128>(dtype, precise);
+    throw std::invalid_argument("unsupported head_dim for the split kernel");
 }
 
 }  // namespace
@@ -756,9 +458,7 @@ int device_cu_count() {
 int chunk_tokens(const Shape &s) { return std::max(1, kMaxRows / s.group()); }
 
 int block_threads(const SplitPlan &p) {
-    return p.kind == SplitKind::Stream ? kWaves * kWave
-         : p.kind == SplitKind::Coop   ? kCoopWaves * kWave
-                                       : kRingThreads;
+    return p.kind == SplitKind::Stream ? kWaves * kWave : kRingThreads;
 }
 
 // Resident workgroups per CU of a kernel instance (cached per device).
@@ -781,7 +481,8 @@ SplitPlan plan_split(const Shape &s, int tokens, Dtype dtype, bool precise) {
     SplitPlan p;
     p.rows = s.group() * tokens;
     p.nqt = (p.rows + 15) / 16;
-    p.kind = kind_for(p.nqt, precise);
+    // One query tile (decode) streams; several (verification) use the ring.
+    p.kind = p.nqt == 1 ? SplitKind::Stream : SplitKind::Ring;
     const long long n_keys = (long long)s.position + tokens;
     p.n_pages = (int)((n_keys + kPageTokens - 1) / kPageTokens);
     p.splits = 1;
@@ -790,18 +491,12 @@ SplitPlan plan_split(const Shape &s, int tokens, Dtype dtype, bool precise) {
     const int resident = device_cu_count() *
                          blocks_per_cu(split_kernel(p, s.head_dim, dtype, precise), block_threads(p));
     int per_head = std::max(1, std::min(resident / s.kv_heads, kMaxSplits));
-    // RS_SPLITS_PER_HEAD caps the split count (for measurement).
-    static const int cap = [] {
-        const char *v = std::getenv("RS_SPLITS_PER_HEAD");
-        return v ? std::max(1, std::atoi(v)) : 0;
-    }();
-    if (cap) per_head = std::min(per_head, cap);
     if (p.kind == SplitKind::Stream) {
         // Decode streams fastest from three quarters of the CUs: on the
         // 139,264-key decode (4 KV heads) 48 splits per head (192
         // workgroups) take 95.5 us against 97.6 us for 64, and the combine
         // has fewer partials to merge.
-        if (!cap) per_head = std::max(1, std::min(per_head, device_cu_count() * 3 / (4 * s.kv_heads)));
+        per_head = std::max(1, std::min(per_head, device_cu_count() * 3 / (4 * s.kv_heads)));
         // Every wave gets at least one page on average.
         p.splits = std::max(1, std::min(per_head, (p.n_pages + kWaves - 1) / kWaves));
     } else {

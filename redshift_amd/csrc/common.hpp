@@ -78,13 +78,5 @@ __device__ __forceinline__ void lds_barrier() {
     __builtin_amdgcn_s_barrier();
     __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
 }
-__device__ __forceinline__ float wave_max(float x) {
-    for (int d = 32; d; d >>= 1) x = fmaxf(x, __shfl_xor(x, d, kWave));
-    return x;
-}
-__device__ __forceinline__ float wave_sum(float x) {
-    for (int d = 32; d; d >>= 1) x += __shfl_xor(x, d, kWave);
-    return x;
-}
 
 }  // namespace rs

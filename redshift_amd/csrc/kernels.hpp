@@ -15,7 +15,7 @@ struct Shape {
     int n_keys() const { return position + tokens; }
 };
 
-enum class SplitKind { Stream, Coop, Ring };
+enum class SplitKind { Stream, Ring };
 
 // The new token of a fused decode (the reference's attn_prepare inputs for
 // the 24/4/256 model).  The split kernel prepares the query and attends to
@@ -52,15 +52,15 @@ struct SplitArgs {
     FusedToken tok;       // the fused decode instance's query source
 };
 
-// attention_ring instance (ring.hip) for head_dim D and nqt query tiles
-// (1..4); precise (fp32 hi + lo) queries have an fp16, D=256 instance only
+// attention_ring instance (ring.hip) for head_dim D (128 or 256) and nqt
+// query tiles (1..4); precise (fp32 hi + lo) queries run on fp16 pages only
 // (nullptr otherwise).  It takes kRingThreads threads and SplitArgs.
 constexpr int kRingThreads = 512;
 const void *ring_kernel(int D, int nqt, Dtype dtype, bool precise);
 
 // The split-K decomposition chosen for one launch of the partial kernel.
 struct SplitPlan {
-    SplitKind kind;  // attention_stream (one query tile), attention_coop or attention_ring
+    SplitKind kind;  // attention_stream (one query tile) or attention_ring
     int nqt;         // 16-row query tiles per KV head (rows = group * tokens)
     int rows;        // valid query rows per KV head
     int n_pages;     // 32-key pages per KV head holding keys 0..n_keys-1
@@ -133,6 +133,10 @@ void launch_pack(void *k_pages, void *v_pages, const void *k_rows, const void *v
 void launch_unpack(void *k_rows, void *v_rows, const void *k_pages, const void *v_pages,
                    int kv_heads, int head_dim, int capacity, int first, int count,
                    hipStream_t stream);
+
+// An fp32 query [n] as two fp16 arrays [2][n]: hi = fp16(q), lo = fp16(q -
+// hi) (the B operands of the precise kernel instances).
+void launch_split_query(void *q_hilo, const float *q, size_t n, hipStream_t stream);
 
 // RMSNorm + RoPE of q and k, fp16 append of k and v into the pages at
 // position..position+batch-1 (the reference's attn_prepare semantics for the

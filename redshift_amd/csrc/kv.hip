@@ -92,6 +92,19 @@ void prepare_kernel(_Float16 *q_hilo, _Float16 *k_pages, _Float16 *v_pages, cons
     }
 }
 
+// hi = fp16(q), lo = fp16(q - hi): q - hi is exact in fp32, so the two
+// parts hold q to about 22 significant bits (|q| < 65504, error at most
+// 2^-25 + 2^-22 |q| once lo falls into fp16's subnormal range).
+__global__ __launch_bounds__(256)
+void split_query(_Float16 *hi, _Float16 *lo, const float *q, size_t n) {
+    for (size_t e = (size_t)blockIdx.x * blockDim.x + threadIdx.x; e < n; e += (size_t)gridDim.x * blockDim.x) {
+        const float x = q[e];
+        const _Float16 h = (_Float16)x;
+        hi[e] = h;
+        lo[e] = (_Float16)(x - (float)h);
+    }
+}
+
 // Copy of whole pages: for every KV head, elements [0, n) of its run (the
 // pages of tokens 0 .. n/D-1) from a cache of stride src_stride to one of
 // stride dst_stride.  Each thread moves kCopyUnroll 16-byte pieces of one
@@ -149,6 +162,14 @@ void launch_unpack(void *k_rows, void *v_rows, const void *k_pages, const void *
                    hipStream_t stream) {
     convert<false>(const_cast<void *>(k_pages), const_cast<void *>(v_pages), k_rows, v_rows,
                    kv_heads, head_dim, capacity, first, count, stream);
+}
+
+void launch_split_query(void *q_hilo, const float *q, size_t n, hipStream_t stream) {
+    if (!n) return;
+    const unsigned blocks = (unsigned)std::min<size_t>((n + 255) / 256, 65536);
+    _Float16 *hi = static_cast<_Float16 *>(q_hilo);
+    hipLaunchKernelGGL(split_query, dim3(blocks), dim3(256), 0, stream, hi, hi + n, q, n);
+    check(hipGetLastError());
 }
 
 void launch_prepare(void *q_hilo, void *k_pages, void *v_pages, const float *q_gate,

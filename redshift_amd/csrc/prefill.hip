@@ -25,8 +25,9 @@
 // halves are interleaved chunk by chunk, so every wave keeps both units busy
 // instead of alternating between them in step with the other waves of its
 // SIMD.  Online softmax in base 2 with a lazily moved row max (see ring.hip);
-// the max is taken over raw scores and the scale is folded into the
-// exponent's fused multiply-add.  bf16 caches multiply by P split into hi +
+// scores are scaled before they are masked and their max is taken, so any
+// finite scale (zero and negative ones included) gives the softmax of the
+// scaled scores.  bf16 caches multiply by P split into hi +
 // lo bf16 parts, fp16 caches by a single fp16 P.
 //
 // Scheduling: workgroup i serves KV head i % kv_heads (with 4 KV heads the
@@ -38,7 +39,6 @@
 
 #include <algorithm>
 #include <cmath>
-#include <cstdlib>
 #include <type_traits>
 
 namespace rs {
@@ -247,7 +247,7 @@ void attention_prefill(PrefillArgs a) {
         // Scores of page i; keys past a row's limit are masked.
         float x[8];
 #pragma unroll
-        for (int j = 0; j < 8; ++j) x[j] = s[j >> 2][j & 3];
+        for (int j = 0; j < 8; ++j) x[j] = s[j >> 2][j & 3] * a.scale_log2;
         if (i * 32 + 31 > wave_first_limit) {
             keep_branch();
 #pragma unroll
@@ -263,7 +263,7 @@ void attention_prefill(PrefillArgs a) {
         pin(mx);
         qk_chunk(std::integral_constant<int, 1>{}, kb, sn);
         // Every row sees key 0, so the max is finite from the first page on.
-        const float bm = mx * a.scale_log2;
+        const float bm = mx;
         float alpha = 1.f;
         const bool moved = bm > m + kLazy;
         if (moved) alpha = __builtin_amdgcn_exp2f(m - bm);
@@ -272,11 +272,11 @@ void attention_prefill(PrefillArgs a) {
         pin(alpha, m);
         qk_chunk(std::integral_constant<int, 2>{}, kb, sn);
 #pragma unroll
-        for (int j = 0; j < 4; ++j) e[j] = __builtin_amdgcn_exp2f(__builtin_fmaf(x[j], a.scale_log2, -m));
+        for (int j = 0; j < 4; ++j) e[j] = __builtin_amdgcn_exp2f(x[j] - m);
         pin(e[0], e[1], e[2], e[3]);
         qk_chunk(std::integral_constant<int, 3>{}, kb, sn);
 #pragma unroll
-        for (int j = 4; j < 8; ++j) e[j] = __builtin_amdgcn_exp2f(__builtin_fmaf(x[j], a.scale_log2, -m));
+        for (int j = 4; j < 8; ++j) e[j] = __builtin_amdgcn_exp2f(x[j] - m);
         pin(e[4], e[5], e[6], e[7]);
         qk_chunk(std::integral_constant<int, 4>{}, kb, sn);
         // P^T as B operands: hi parts (and lo parts, bf16).
@@ -415,37 +415,26 @@ void attention_prefill(PrefillArgs a) {
 
 // Rows per workgroup: 192 (twelve waves, three per SIMD; 2048 tokens of six
 // query heads per KV head make 64 workgroups per KV head, one round on 256
-// CUs) or 128 (RS_PREFILL_ROWS=128, for measurement).  A precise query (hi +
-// lo parts) needs twice the query registers: 128 rows (eight waves, two per
-// SIMD).
-int prefill_rows() {
-    static const int rows = [] {
-        const char *v = std::getenv("RS_PREFILL_ROWS");
-        return v && std::atoi(v) == 128 ? 128 : 192;
-    }();
-    return rows;
-}
-
-template <int D, int ROWS>
-const void *prefill_kernel(Dtype dtype, bool out_f32) {
-    if (dtype == Dtype::BF16)
-        return out_f32 ? (const void *)&attention_prefill<D, __bf16, true, false, kOutF32, ROWS>
-                       : (const void *)&attention_prefill<D, __bf16, true, false, kOutSame, ROWS>;
-    return out_f32 ? (const void *)&attention_prefill<D, _Float16, false, false, kOutF32, ROWS>
-                   : (const void *)&attention_prefill<D, _Float16, false, false, kOutSame, ROWS>;
-}
+// CUs).  A precise query (hi + lo parts) needs twice the query registers:
+// 128 rows (eight waves, two per SIMD).
+constexpr int kPrefillRows = 192, kPreciseRows = 128;
 
 template <int D>
-const void *prefill_kernel(Dtype dtype, bool out_f32, int rows) {
-    return rows == 128 ? prefill_kernel<D, 128>(dtype, out_f32) : prefill_kernel<D, 192>(dtype, out_f32);
+const void *prefill_kernel(Dtype dtype, bool out_f32) {
+    constexpr int R = kPrefillRows;
+    if (dtype == Dtype::BF16)
+        return out_f32 ? (const void *)&attention_prefill<D, __bf16, true, false, kOutF32, R>
+                       : (const void *)&attention_prefill<D, __bf16, true, false, kOutSame, R>;
+    return out_f32 ? (const void *)&attention_prefill<D, _Float16, false, false, kOutF32, R>
+                   : (const void *)&attention_prefill<D, _Float16, false, false, kOutSame, R>;
 }
 
 // The fused model path: fp16 pages, fp32 query as hi + lo parts, hi + lo P
 // (the same precision as the split kernels' precise instance).
 template <int D>
 const void *precise_prefill_kernel(bool gated) {
-    return gated ? (const void *)&attention_prefill<D, _Float16, true, true, kOutGated, 128>
-                 : (const void *)&attention_prefill<D, _Float16, true, true, kOutF32, 128>;
+    return gated ? (const void *)&attention_prefill<D, _Float16, true, true, kOutGated, kPreciseRows>
+                 : (const void *)&attention_prefill<D, _Float16, true, true, kOutF32, kPreciseRows>;
 }
 
 }  // namespace
@@ -468,12 +457,14 @@ void launch_prefill(const Shape &s, Dtype dtype, bool precise, float scale, cons
     a.group = s.group();
     a.rows = s.group() * s.tokens;
     a.position = s.position;
-    const int rows = precise ? 128 : prefill_rows();
+    const int rows = precise ? kPreciseRows : kPrefillRows;
     a.n_tiles = (a.rows + rows - 1) / rows;
     a.scale_log2 = scale * 1.4426950408889634f;
-    const void *kernel = precise ? (s.head_dim == 256 ? precise_prefill_kernel<256>(gate != nullptr) : nullptr)
-                       : s.head_dim == 256 ? prefill_kernel<256>(dtype, out_f32, rows)
-                       : s.head_dim == 128 ? prefill_kernel<128>(dtype, out_f32, rows) : nullptr;
+    const void *kernel = precise ? (s.head_dim == 256   ? precise_prefill_kernel<256>(gate != nullptr)
+                                    : s.head_dim == 128 ? precise_prefill_kernel<128>(gate != nullptr)
+                                                        : nullptr)
+                       : s.head_dim == 256 ? prefill_kernel<256>(dtype, out_f32)
+                       : s.head_dim == 128 ? prefill_kernel<128>(dtype, out_f32) : nullptr;
     require(kernel != nullptr, "unsupported head_dim for the prefill kernel");
     void *args[] = {&a};
     const int threads = (rows / 16) * kWave;

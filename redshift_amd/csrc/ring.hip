@@ -407,7 +407,10 @@ const void *pick_precise(int nqt) {
 }
 
 const void *ring_kernel(int D, int nqt, Dtype dtype, bool precise) {
-    if (precise) return dtype == Dtype::F16 && D == 256 ? pick_precise<256>(nqt) : nullptr;
+    if (precise) {
+        if (dtype != Dtype::F16) return nullptr;
+        return D == 256 ? pick_precise<256>(nqt) : D == 128 ? pick_precise<128>(nqt) : nullptr;
+    }
     if (D == 256) return pick_tiles<256>(nqt, dtype);
     if (D == 128) return pick_tiles<128>(nqt, dtype);
     return nullptr;

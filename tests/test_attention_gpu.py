@@ -522,60 +522,6 @@ def test_kv_copy_prefix_bitwise(gpu, head_dim, kv_heads):
         np.testing.assert_array_equal(v.cpu().numpy().view(np.uint16), (-rows[:1000]).cpu().numpy().view(np.uint16))
 
 
-def test_session_verify_commit_checkpoint_restore(gpu):
-    """The reference session's bookkeeping on two attention layers: prefill,
-    a recorded 8-token verification, commit(3), a decode that overwrites the
-    first rejected row, checkpoint, more tokens, restore, and a decode from
-    the restored prefix; every output against the oracle on the logical
-    (token-major) caches that the same operations produce."""
-    from redshift_amd.kvcache import AttentionKV, SessionError
-    H, HKV, D, layers, scale = 24, 4, 256, 2, 1 / 16
-    rng = np.random.default_rng(5)
-    kv = AttentionKV(layers, HKV, D, context=1024)
-    logical = [[np.zeros((0, HKV, D)), np.zeros((0, HKV, D))] for _ in range(layers)]
-
-    def run(T, recording=False):
-        kv.begin(T, recording)
-        for layer in range(layers):
-            q = rng.standard_normal((T, H, D)).astype(np.float16)
-            k = (rng.standard_normal((T, HKV, D)) * .5).astype(np.float16)
-            v = (rng.standard_normal((T, HKV, D)) * .5).astype(np.float16)
-            pos = kv.position
-            lk, lv = logical[layer]
-            logical[layer] = [np.concatenate([lk[:pos], k]), np.concatenate([lv[:pos], v])]
-            got = kv.attend(layer, gpu.from_numpy(q).cuda(), gpu.from_numpy(k).cuda(), gpu.from_numpy(v).cuda(), scale)
-            gpu.cuda.synchronize()
-            want = ref.gqa_attention(q, logical[layer][0], logical[layer][1], pos, scale)
-            assert_parity(got.cpu().numpy().astype(np.float64), want)
-        kv.end()
-
-    for _ in range(12):              # prefill 96 tokens, 8 at a time (the server's chunks)
-        run(8)
-    assert kv.position == 96
-    run(8, recording=True)
-    assert (kv.position, kv.pending) == (104, 8)
-    with pytest.raises(SessionError, match='commit or abort'):
-        kv.begin(1)
-    with pytest.raises(SessionError, match='acceptance outside'):
-        kv.commit(9)
-    kv.commit(3)
-    assert (kv.position, kv.pending) == (99, 0)
-    with pytest.raises(SessionError, match='no pending'):
-        kv.commit(1)
-    run(1)                           # overwrites the first rejected row (99)
-    kv.checkpoint()
-    saved = [[a.copy() for a in pair] for pair in logical]
-    run(8)
-    run(5)
-    kv.restore()
-    assert kv.position == 100
-    logical = saved
-    run(4)                           # from the restored prefix
-    kv.reset()
-    with pytest.raises(SessionError, match='no valid checkpoint'):
-        kv.restore()
-
-
 def random_shapes(n, seed=2024):
     """Seeded shapes across both kernels' ranges: KV heads 1-8, groups 1-8,
     head_dim 128/256, fp16/bf16, 1-24 tokens (split-K up to 48 rows per KV

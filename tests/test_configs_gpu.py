@@ -1,0 +1,139 @@
+"""The workload shapes at full size and at their stated precision, the
+precise (fp32-query) entry, and scores under any finite scale.
+
+Every check holds the float32 output to max-abs 2e-3 and relative-L2 1e-3
+against the float64 oracle (oracle/attention_ref.py, the restatement of the
+reference's tests/cpu_reference.py:55-89) on the same seeded inputs.
+"""
+import numpy as np
+import pytest
+
+from oracle import attention_ref as ref
+from redshift_amd import attention as A
+from redshift_amd.workloads import WORKLOADS, Workload, f32_to_bf16_bits, make_inputs, to_float
+from tests.test_attention_gpu import MAX_ABS, assert_parity, gpu_attention, make_cache
+
+pytestmark = pytest.mark.gpu
+
+# The fp32 query travels as fp16 hi + lo parts (about 22 significant bits)
+# and P as hi + lo parts: far inside the parity bounds.
+PRECISE_REL_L2 = 5e-5
+
+
+def rel_l2(got, want):
+    return float(np.linalg.norm(got - want) / np.linalg.norm(want))
+
+
+def precise_attention(w, q32, k16, v16, torch, fill_nan=True):
+    """qv_attention_precise of an fp32 query on an fp16 cache."""
+    wf16 = Workload(**{**w.__dict__, 'dtype': 'f16'})
+    cache = make_cache(k16, v16, wf16, torch, fill_nan=fill_nan)
+    out = A.attention_precise(torch.from_numpy(np.ascontiguousarray(q32, np.float32)).cuda(), cache,
+                              w.position, w.scale)
+    torch.cuda.synchronize()
+    return out.cpu().numpy().astype(np.float64)
+
+
+def test_cpu_plumbing_at_its_stated_precision(gpu):
+    """8/2/128, one query on 128 keys, fp32 Q/K/V from N(0,1) with seed 0,
+    scale 1/sqrt(128): the fp32 query through qv_attention_precise; K and V
+    are the fp16 cache entries (the reference's caches are fp16 and its CPU
+    oracle rounds them with half(), tests/cpu_reference.py:57,75-76).  The
+    oracle runs on exactly the fp32 query and those fp16 keys and values."""
+    w = WORKLOADS['cpu_plumbing']
+    q, k, v, _ = make_inputs(w)
+    assert q.dtype == np.float32
+    k16, v16 = k.astype(np.float16), v.astype(np.float16)
+    got = precise_attention(w, q, k16, v16, gpu)
+    want = ref.gqa_attention(q, k16, v16, w.position, w.scale)
+    assert_parity(got, want)
+    assert rel_l2(got, want) <= PRECISE_REL_L2
+    # The same keys with the query rounded to fp16 (the raw 16-bit entry)
+    # carry the query's own rounding: the precise entry is the closer one.
+    q16 = q.astype(np.float16)
+    got16 = gpu_attention(Workload(**{**w.__dict__, 'dtype': 'f16'}), q16, k16, v16, gpu, out_dtype=gpu.float32)
+    assert rel_l2(got, want) < rel_l2(got16, want)
+
+
+SAMPLE = np.unique(np.concatenate([[0, 1, 2, 5, 2047], np.linspace(3, 2046, 27).astype(int)]))
+
+
+@pytest.mark.parametrize('kv_dtype', ['bf16', 'f16'])
+def test_prefill_chunk_full_size_float32_output(gpu, kv_dtype):
+    """2048 query tokens appended to a 6144-token cache (8192 keys), causal,
+    24/4/256, inputs N(0,1) from seed 2, float32 output: every head of 32
+    sampled token rows to both bounds (bf16 caches as stated, and fp16
+    caches of the same shape).  The 16-bit output of the same call must
+    equal that float32 value up to its own rounding (half an ulp)."""
+    w = Workload(**{**WORKLOADS['prefill_2k'].__dict__, 'dtype': kv_dtype})
+    q, k, v, _ = make_inputs(w)
+    print(f'prefill 2048 at 6144, {kv_dtype}', flush=True)
+    got32 = gpu_attention(w, q, k, v, gpu, fill_nan=True, out_dtype=gpu.float32)
+    want = ref.gqa_attention(to_float(q, kv_dtype), to_float(k, kv_dtype), to_float(v, kv_dtype),
+                             w.position, w.scale, rows=SAMPLE)
+    assert_parity(got32[SAMPLE], want)
+    got16 = gpu_attention(w, q, k, v, gpu, fill_nan=True)
+    half_ulp = np.abs(want) * (2.0 ** -8 if kv_dtype == 'bf16' else 2.0 ** -11)
+    assert np.all(np.abs(got16[SAMPLE] - want) <= MAX_ABS + half_ulp)
+    if kv_dtype == 'bf16':
+        want16 = to_float(f32_to_bf16_bits(want.astype(np.float32)), 'bf16')
+        assert rel_l2(got16[SAMPLE], want16) <= 1e-3
+
+
+def test_prefill_chunk_full_size_precise(gpu):
+    """The same chunk with an fp32 query on fp16 caches through the precise
+    entry (the reference's precision: fp32 q, fp16 cache)."""
+    w = WORKLOADS['prefill_2k']
+    rng = np.random.default_rng(w.seed)
+    q = rng.standard_normal((w.tokens, w.q_heads, w.head_dim), dtype=np.float32)
+    k = rng.standard_normal((w.keys, w.kv_heads, w.head_dim), dtype=np.float32).astype(np.float16)
+    v = rng.standard_normal((w.keys, w.kv_heads, w.head_dim), dtype=np.float32).astype(np.float16)
+    got = precise_attention(w, q, k, v, gpu)
+    want = ref.gqa_attention(q, k, v, w.position, w.scale, rows=SAMPLE)
+    assert_parity(got[SAMPLE], want)
+    assert rel_l2(got[SAMPLE], want) <= PRECISE_REL_L2
+
+
+@pytest.mark.parametrize('q_heads,kv_heads,head_dim,T,position', [
+    (24, 4, 256, 1, 5000),      # decode: stream kernel
+    (24, 4, 256, 2, 31),
+    (24, 4, 256, 8, 16384),     # verify-8 at 16K: ring kernel
+    (8, 2, 128, 8, 300),        # 32 rows, head_dim 128
+    (16, 2, 128, 6, 777),       # 48 rows, head_dim 128
+    (24, 1, 256, 1, 20000),     # one KV head, many splits
+    (24, 4, 256, 100, 37),      # prefill kernel
+    (8, 2, 128, 200, 64),       # prefill kernel, head_dim 128
+])
+def test_precise_entry_against_oracle(gpu, q_heads, kv_heads, head_dim, T, position):
+    """qv_attention_precise across its kernels (fp32 query, fp16 pages,
+    pages past the last key filled with NaN)."""
+    w = Workload('precise', q_heads, kv_heads, head_dim, T, position, 1 / head_dim ** .5, 'f32', 700 + T,
+                 1.0, 0.5, min(16, position + T), 8.0)
+    q, k, v, _ = make_inputs(w)
+    k16, v16 = k.astype(np.float16), v.astype(np.float16)
+    got = precise_attention(w, q, k16, v16, gpu)
+    want = ref.gqa_attention(q, k16, v16, position, w.scale)
+    assert_parity(got, want)
+    assert rel_l2(got, want) <= PRECISE_REL_L2
+
+
+@pytest.mark.parametrize('T,scale,dtype', [
+    (100, 0.0, 'f16'), (100, -1 / 16, 'f16'), (100, -1 / 16, 'bf16'),   # prefill kernel
+    (3, 0.0, 'f16'), (8, -0.2, 'bf16'),                                 # ring kernel
+    (1, 0.0, 'bf16'), (1, -1 / 16, 'f16'),                              # stream kernel
+])
+def test_any_finite_scale(gpu, T, scale, dtype):
+    """Scores are scaled before they are masked and their maximum taken, so
+    a zero scale gives the mean of the visible values and a negative one
+    the softmax of the negated scores; NaN in the pages past the last key
+    never reaches the result."""
+    w = Workload('scale', 24, 4, 256, T, 500, scale, dtype, 800 + T, 1.0, 0.5)
+    q, k, v, _ = make_inputs(w)
+    want = ref.gqa_attention(to_float(q, dtype), to_float(k, dtype), to_float(v, dtype), w.position, scale)
+    got = gpu_attention(w, q, k, v, gpu, fill_nan=True, out_dtype=gpu.float32)
+    assert_parity(got, want)
+    if scale == 0.0:
+        vf = to_float(v, dtype)
+        t = T - 1     # the last row sees keys 0..position+T-1: their plain mean
+        mean = vf[:w.position + T].mean(axis=0)                    # [kv_heads, D]
+        np.testing.assert_allclose(got[t], np.repeat(mean, w.group, axis=0), atol=2e-3)

@@ -167,6 +167,10 @@ def test_device_entry_points_validate_before_touching_the_device(lib):
     assert b'capacity' in lib.qv_error()
     assert lib.qv_attention_fused(*([p] * 8), 100, 139200, 139264, 1e-6, p, ws, None) == -1
     assert b'139264' in lib.qv_error()
+    # Every device buffer of the fused entry is 16-byte aligned (the prefill
+    # chunk stores 16-byte vectors to out).
+    assert lib.qv_attention_fused(ct.c_void_p(4100), *([p] * 7), 100, 0, 128, 1e-6, p, ws, None) == -1
+    assert b'aligned' in lib.qv_error()
 
 
 def test_front_end_rejects_mismatched_tensors(lib):
