@@ -149,6 +149,21 @@ int qv_attention_combine(void *out, int dtype, int out_dtype, int q_heads, int k
                          int tokens, int position, const void *workspace,
                          uint64_t workspace_bytes, void *stream);
 
+/* qv_attention without a workspace argument, for callers that cannot
+ * allocate device memory (code under HIP graph capture, tight serving loops,
+ * harnesses that forbid hipMalloc).  No counterpart in the reference.  It
+ * runs the same kernels, and gives the same bits, as qv_attention; the
+ * split-K partials live in a static device array of 16 MiB per GPU, held
+ * until the process ends (the largest plan on a 256-CU MI355X takes
+ * 12.1 MiB; a shape that needs more is refused).  The call itself allocates
+ * nothing.  Every call on one GPU shares that GPU's array: calls that
+ * overlap on one GPU (concurrent streams, or threads) race on it, so
+ * serialise them.  No kernel reads a partial it has not written in the same
+ * call, so the array needs no clearing. */
+int qv_attention_noalloc(void *out, const void *q, const void *k_pages, const void *v_pages,
+                         int dtype, int out_dtype, int q_heads, int kv_heads, int head_dim,
+                         int tokens, int position, int capacity, float scale, void *stream);
+
 /* Workspace bytes of qv_attention_precise for this shape. */
 int qv_attention_precise_workspace(uint64_t *bytes, int q_heads, int kv_heads, int head_dim,
                                    int tokens, int position);

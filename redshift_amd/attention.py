@@ -156,6 +156,23 @@ def attention_precise(q, cache, position, scale, out=None, ws=None):
     return out
 
 
+def attention_noalloc(q, cache, position, scale, out=None, out_dtype=None):
+    """`attention` without a workspace: qv_attention_noalloc keeps the
+    split-K partials in the library's static device array (serialise calls
+    on one GPU)."""
+    lib = library()
+    _check_query(q, cache)
+    q = q.contiguous()
+    tokens, q_heads, head_dim = q.shape
+    if out is None:
+        out = torch.empty(q.shape, dtype=out_dtype or q.dtype, device=q.device)
+    _check_output(out, q)
+    check(lib, lib.qv_attention_noalloc(_ptr(out), _ptr(q), _ptr(cache.k), _ptr(cache.v), dtype_code(q.dtype),
+                                        out_code(out.dtype), q_heads, cache.kv_heads, head_dim, tokens,
+                                        position, cache.capacity, float(scale), _stream()))
+    return out
+
+
 def _check_query(q, cache):
     """The query must be [tokens, q_heads, head_dim] of the cache's 16-bit
     type on the cache's device (the library sees untyped pointers)."""

@@ -10,6 +10,8 @@
 #include <cstdio>
 #include <cstring>
 #include <limits>
+#include <mutex>
+#include <vector>
 
 #include "kernels.hpp"
 
@@ -395,6 +397,53 @@ extern "C" int qv_attention(void *out, const void *q, const void *k_pages, const
         require(std::isfinite(scale), "scale must be finite");
         raw_buffers(out, q, k_pages, v_pages, workspace);
         workspace_fits(workspace, workspace_bytes, rs::attention_workspace_bytes(s, dt, false));
+        run_attention(s, dt, false, scale, q, nullptr, k_pages, v_pages, workspace, out, out_f32,
+                      nullptr, static_cast<hipStream_t>(stream));
+    });
+}
+
+// ---- qv_attention_noalloc: the split-K partials in a static device array --
+// One array per GPU, loaded with the library's code object and held until the
+// process ends.  The largest plan on a 256-CU part is 256 workgroups x 48 rows
+// x (256 + 2) floats = 12.1 MiB (split counts are capped by the resident
+// workgroups, and a KV head never has fewer than one split).
+constexpr size_t kScratchBytes = size_t(16) << 20;
+static __device__ __align__(256) unsigned char scratch[kScratchBytes];
+
+namespace {
+// Device address of `scratch` on the current device.  In host code the
+// array's name is only a stand-in for the symbol, so the address is looked
+// up once per device (with that device current) and kept.
+void *scratch_address() {
+    static std::mutex mutex;
+    static std::vector<void *> addresses;
+    int device = 0;
+    check(hipGetDevice(&device));
+    std::lock_guard<std::mutex> lock(mutex);
+    if ((int)addresses.size() <= device) addresses.resize(device + 1, nullptr);
+    if (!addresses[device]) {
+        void *ptr = nullptr;
+        check(hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch)));
+        require(ptr != nullptr, "no device address for the attention scratch array");
+        addresses[device] = ptr;
+    }
+    return addresses[device];
+}
+}  // namespace
+
+extern "C" int qv_attention_noalloc(void *out, const void *q, const void *k_pages, const void *v_pages,
+                                    int dtype, int out_dtype, int q_heads, int kv_heads, int head_dim,
+                                    int tokens, int position, int capacity, float scale, void *stream) {
+    return call([&] {
+        const rs::Dtype dt = dtype_of(dtype);
+        const bool out_f32 = out_f32_of(dtype, out_dtype);
+        const rs::Shape s = attention_shape(q_heads, kv_heads, head_dim, tokens, position, capacity);
+        fits_cache(s);
+        require(std::isfinite(scale), "scale must be finite");
+        void *workspace = scratch_address();
+        raw_buffers(out, q, k_pages, v_pages, workspace);
+        require(rs::attention_workspace_bytes(s, dt, false) <= kScratchBytes,
+                "the shape needs more than the 16 MiB of split-K scratch of qv_attention_noalloc");
         run_attention(s, dt, false, scale, q, nullptr, k_pages, v_pages, workspace, out, out_f32,
                       nullptr, static_cast<hipStream_t>(stream));
     });

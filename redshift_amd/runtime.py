@@ -46,6 +46,7 @@ DEVICE_SIGNATURES = {
     'qv_attention': [_P] * 4 + [_I] * 8 + [_F, _P, _U64, _P],
     'qv_attention_split': [_P] * 3 + [_I] * 7 + [_F, _P, _U64, _P],
     'qv_attention_combine': [_P] + [_I] * 7 + [_P, _U64, _P],
+    'qv_attention_noalloc': [_P] * 4 + [_I] * 8 + [_F, _P],
     'qv_attention_precise_workspace': [ct.POINTER(_U64)] + [_I] * 5,
     'qv_attention_precise': [_P] * 4 + [_I] * 6 + [_F, _P, _U64, _P],
     'qv_attention_fused_workspace': [ct.POINTER(_U64), _I, _I],
