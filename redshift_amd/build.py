@@ -13,7 +13,7 @@ from pathlib import Path
 
 PACKAGE = Path(__file__).resolve().parent
 ROOT = PACKAGE.parent
-SOURCES = ['abi.cpp', 'attention.hip', 'kv.hip', 'prefill.hip', 'ring.hip']
+SOURCES = ['abi.cpp', 'attention.hip', 'kv.hip', 'prefill.hip', 'ring.hip', 'short.hip']
 LIBRARY = PACKAGE / 'lib' / 'libredshift_hip.so'
 ARCH = 'gfx950'
 

@@ -133,14 +133,17 @@ void run_attention(const rs::Shape &s, rs::Dtype dtype, bool precise, float scal
         rs::Shape c = s;
         c.position = s.position + t0;
         c.tokens = std::min(ct, s.tokens - t0);
-        const rs::SplitPlan plan = rs::plan_split(c, c.tokens, dtype, precise);
+        const rs::SplitPlan plan = rs::plan_split(c, c.tokens, dtype, precise, gate == nullptr);
         const size_t q_offset = t0 * row * sizeof(uint16_t);
+        void *out_chunk = static_cast<char *>(out) + t0 * row * out_elem;
+        const float *gate_chunk = gate ? gate + (size_t)t0 * 2 * row : nullptr;
+        // A short context without a gate: one split per KV head writes the
+        // rows itself.
         rs::launch_split(c, plan, dtype, precise, scale, static_cast<const char *>(q) + q_offset,
                          q_lo ? static_cast<const char *>(q_lo) + q_offset : nullptr,
-                         k_pages, v_pages, workspace, stream);
-        rs::launch_combine(c, plan, dtype, workspace,
-                           static_cast<char *>(out) + t0 * row * out_elem, out_f32,
-                           gate ? gate + (size_t)t0 * 2 * row : nullptr, stream);
+                         k_pages, v_pages, workspace, stream, out_chunk, out_f32);
+        if (!plan.direct)
+            rs::launch_combine(c, plan, dtype, workspace, out_chunk, out_f32, gate_chunk, stream);
     }
 }
 
@@ -158,10 +161,11 @@ size_t fused_partials_bytes(int batch, int position) {
     return parts;
 }
 
-// The reference's k_attention on device buffers of the 24/4/256 model.  One
-// token after at least one cached key (decode): two launches, the split
-// kernel preparing the query and appending the new key and value, the
-// combine adding that key.  Otherwise (verification, a first token, a
+// The reference's k_attention on device buffers of the 24/4/256 model.  A
+// short context (up to 8 tokens, position + batch <= 256): one launch that
+// does everything.  One token after at least one cached key (decode): two
+// launches, the split kernel preparing the query and appending the new key
+// and value, the combine adding that key.  Otherwise (verification, a
 // prefill chunk) the prepare kernel writes the query's hi + lo parts to
 // q_hilo (2 * batch * 24 * 256 fp16) and appends the new K/V to the pages,
 // then attention (with the sigmoid gate) runs on them.
@@ -171,7 +175,8 @@ void fused_attention(float *out, void *k_pages, void *v_pages, const float *q_ga
                      size_t partials_bytes, hipStream_t stream) {
     require(partials_bytes >= fused_partials_bytes(batch, position), "workspace too small");
     constexpr int H = rs::kModelQHeads, HKV = rs::kModelKvHeads, D = rs::kModelHeadDim;
-    if (batch <= rs::kMaxFusedSplitTokens && position >= 1) {
+    const bool short_context = batch <= rs::kShortMaxTokens && position + batch <= rs::kShortFusedKeys;
+    if (short_context || (batch <= rs::kMaxFusedSplitTokens && position >= 1)) {
         rs::FusedToken tok;
         tok.q_gate = q_gate;
         tok.key = key;
@@ -184,7 +189,8 @@ void fused_attention(float *out, void *k_pages, void *v_pages, const float *q_ga
         tok.epsilon = epsilon;
         tok.position = position;
         tok.tokens = batch;
-        rs::launch_fused_tokens(tok, capacity, partials, out, stream);
+        if (short_context) rs::launch_fused_short(tok, out, stream);
+        else rs::launch_fused_tokens(tok, capacity, partials, out, stream);
         return;
     }
     const rs::Shape s{H, HKV, D, batch, position, capacity};

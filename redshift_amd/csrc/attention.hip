@@ -120,7 +120,11 @@ __device__ __forceinline__ int v_slot_token(int g, int j) {
 // only.  The first split's workgroups also store the prepared rows in
 // a.tok.q_prep and prepare and append the new keys (wave j: token j), which
 // the combine adds.
-template <int D, bool QSPLIT, bool PSPLIT, typename KV, bool PREP>
+//
+// OUT: kOutPartials stores the split's partial rows; a direct output
+// (kOutSame or kOutF32: one split per KV head) stores the final rows
+// instead, and no combine runs.
+template <int D, bool QSPLIT, bool PSPLIT, typename KV, bool PREP, int OUT = kOutPartials>
 __global__ __launch_bounds__(kWaves * kWave)
 void attention_stream(SplitArgs a) {
     using V8 = typename Vec8<KV>::type;
@@ -352,7 +356,7 @@ void attention_stream(SplitArgs a) {
 #pragma unroll
     for (int dt = 0; dt < DT; ++dt) so[w][dt * kWave + lane] = acc[dt];
     lds_barrier();
-    if (w == 0 && lane < a.rows && lane < 16) {
+    if (OUT == kOutPartials && w == 0 && lane < a.rows && lane < 16) {
         float M = -INFINITY;
 #pragma unroll
         for (int ww = 0; ww < kWaves; ++ww) M = fmaxf(M, sml[ww][0][lane]);
@@ -375,7 +379,25 @@ void attention_stream(SplitArgs a) {
         f32x4 o = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
         for (int ww = 0; ww < kWaves; ++ww) o += so[ww][idx] * exp2f(sml[ww][0][r] - mu);
-        po[e] = o;
+        if constexpr (OUT == kOutPartials) {
+            po[e] = o;
+        } else {
+            // The only split of this KV head: the final row (every row sees
+            // key 0, so L > 0).
+            float L = 0.f;
+#pragma unroll
+            for (int ww = 0; ww < kWaves; ++ww) L += sml[ww][1][r] * exp2f(sml[ww][0][r] - mu);
+            o *= 1.f / L;
+            const int t = r / a.group;
+            const size_t hrow = (size_t)t * a.q_heads + h * a.group + (r - t * a.group);
+            if constexpr (OUT == kOutSame) {
+                typedef KV KV4 __attribute__((ext_vector_type(4)));
+                const KV4 v = {(KV)o[0], (KV)o[1], (KV)o[2], (KV)o[3]};
+                *reinterpret_cast<KV4 *>(static_cast<KV *>(a.out) + hrow * D + 4 * d4) = v;
+            } else {
+                *reinterpret_cast<f32x4 *>(static_cast<float *>(a.out) + hrow * D + 4 * d4) = o;
+            }
+        }
     }
 }
 
@@ -402,11 +424,24 @@ void attention_combine(CombineArgs c) {
 // attention_stream instance: raw fp16 multiplies V by a 16-bit P; raw bf16
 // by hi + lo P (bf16's 8-bit significand alone would dominate the error); a
 // precise query (fp32 as fp16 hi + lo parts) takes hi + lo P as well.
-template <int D>
+template <int D, int OUT>
 const void *stream_kernel(Dtype dtype, bool precise) {
-    if (precise) return (const void *)&attention_stream<D, true, true, _Float16, false>;
-    if (dtype == Dtype::BF16) return (const void *)&attention_stream<D, false, true, __bf16, false>;
-    return (const void *)&attention_stream<D, false, false, _Float16, false>;
+    if (precise) {
+        if constexpr (OUT == kOutSame) return nullptr;
+        else return dtype == Dtype::F16 ? (const void *)&attention_stream<D, true, true, _Float16, false, OUT> : nullptr;
+    }
+    if (dtype == Dtype::BF16) return (const void *)&attention_stream<D, false, true, __bf16, false, OUT>;
+    return (const void *)&attention_stream<D, false, false, _Float16, false, OUT>;
+}
+
+template <int D>
+const void *stream_kernel(Dtype dtype, bool precise, int out_mode) {
+    switch (out_mode) {
+        case kOutPartials: return stream_kernel<D, kOutPartials>(dtype, precise);
+        case kOutSame: return stream_kernel<D, kOutSame>(dtype, precise);
+        case kOutF32: return stream_kernel<D, kOutF32>(dtype, precise);
+    }
+    return nullptr;
 }
 
 template <int D, typename PT, bool NT>
@@ -427,15 +462,13 @@ const void *combine_kernel(Dtype dtype, bool out_f32, bool gated, bool half_part
                     : combine_kernel<D, float, false>(dtype, out_f32, gated);
 }
 
-const void *split_kernel(const SplitPlan &p, int D, Dtype dtype, bool precise) {
-    if (p.kind == SplitKind::Ring) {
-        const void *k = ring_kernel(D, p.nqt, dtype, precise);
-        require(k != nullptr, "unsupported head_dim / query rows for the ring kernel");
-        return k;
-    }
-    if (D == 256) return stream_kernel<256>(dtype, precise);
-    if (D == 128) return stream_kernel<128>(dtype, precise);
-    throw std::invalid_argument("unsupported head_dim for the split kernel");
+const void *split_kernel(const SplitPlan &p, int D, Dtype dtype, bool precise, int out_mode = kOutPartials) {
+    const void *k = p.kind == SplitKind::Ring ? ring_kernel(D, p.nqt, dtype, precise, out_mode)
+                  : D == 256                  ? stream_kernel<256>(dtype, precise, out_mode)
+                  : D == 128                  ? stream_kernel<128>(dtype, precise, out_mode)
+                                              : nullptr;
+    require(k != nullptr, "unsupported head_dim / query rows / output for the split kernel");
+    return k;
 }
 
 }  // namespace
@@ -477,7 +510,7 @@ int blocks_per_cu(const void *kernel, int threads) {
     return n;
 }
 
-SplitPlan plan_split(const Shape &s, int tokens, Dtype dtype, bool precise) {
+SplitPlan plan_split(const Shape &s, int tokens, Dtype dtype, bool precise, bool allow_direct) {
     SplitPlan p;
     p.rows = s.group() * tokens;
     p.nqt = (p.rows + 15) / 16;
@@ -487,6 +520,8 @@ SplitPlan plan_split(const Shape &s, int tokens, Dtype dtype, bool precise) {
     p.n_pages = (int)((n_keys + kPageTokens - 1) / kPageTokens);
     p.splits = 1;
     p.half_parts = false;
+    p.direct = allow_direct && p.n_pages <= (p.kind == SplitKind::Stream ? kDirectStreamPages : kDirectRingPages);
+    if (p.direct) return p;
     // Fill every CU with as many workgroups as stay resident.
     const int resident = device_cu_count() *
                          blocks_per_cu(split_kernel(p, s.head_dim, dtype, precise), block_threads(p));
@@ -512,6 +547,7 @@ SplitPlan plan_split(const Shape &s, int tokens, Dtype dtype, bool precise) {
 }
 
 size_t plan_bytes(const Shape &s, const SplitPlan &p) {
+    if (p.direct) return 0;
     return (size_t)s.kv_heads * p.splits * p.rows * ((size_t)s.head_dim + 2) * sizeof(float);
 }
 
@@ -529,14 +565,15 @@ size_t attention_workspace_bytes(const Shape &s, Dtype dtype, bool precise) {
 
 void launch_split(const Shape &s, const SplitPlan &plan, Dtype dtype, bool precise,
                   float scale, const void *q, const void *q_lo, const void *k_pages,
-                  const void *v_pages, void *workspace, hipStream_t stream) {
-    SplitArgs a;
+                  const void *v_pages, void *workspace, hipStream_t stream,
+                  void *out, bool out_f32) {
+    SplitArgs a = {};
     a.q = q;
     a.q_lo = q_lo;
     a.k_pages = k_pages;
     a.v_pages = v_pages;
     a.part_o = static_cast<float *>(workspace);
-    a.part_ml = a.part_o + (size_t)s.kv_heads * plan.splits * plan.rows * s.head_dim;
+    a.part_ml = a.part_o ? a.part_o + (size_t)s.kv_heads * plan.splits * plan.rows * s.head_dim : nullptr;
     a.head_stride = (size_t)s.capacity * s.head_dim;
     a.q_heads = s.q_heads;
     a.kv_heads = s.kv_heads;
@@ -547,7 +584,13 @@ void launch_split(const Shape &s, const SplitPlan &plan, Dtype dtype, bool preci
     a.n_pages = plan.n_pages;
     a.splits = plan.splits;
     a.scale_log2 = scale * 1.4426950408889634f;
-    const void *kernel = split_kernel(plan, s.head_dim, dtype, precise);
+    a.out = out;
+    int out_mode = kOutPartials;
+    if (plan.direct) {
+        require(out != nullptr && plan.splits == 1, "a direct split plan writes the output");
+        out_mode = out_f32 ? kOutF32 : kOutSame;
+    }
+    const void *kernel = split_kernel(plan, s.head_dim, dtype, precise, out_mode);
     void *args[] = {&a};
     // One-dimensional grid: workgroup id = KV head * splits + split.
     check(hipLaunchKernel(kernel, dim3(plan.splits * s.kv_heads), dim3(block_threads(plan)),

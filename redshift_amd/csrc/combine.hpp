@@ -9,9 +9,6 @@
 
 namespace rs {
 
-// Output of a combine: kOutSame writes the KV type, kOutF32 fp32, kOutGated
-// fp32 times sigmoid(gate), gate being q_gate[t][h][D + d] (row stride 2D).
-enum { kOutSame = 0, kOutF32 = 1, kOutGated = 2 };
 
 // One row of one KV head, combined by the four waves w4 = 0..3 of a
 // workgroup (every wave must call it, `valid` or not: it holds a workgroup

@@ -17,6 +17,11 @@ struct Shape {
 
 enum class SplitKind { Stream, Ring };
 
+// What a split kernel or the combine writes: the KV type, fp32, or fp32
+// times sigmoid(gate) (gate = q_gate[t][h][D + d], rows of 2D floats); or,
+// for a split kernel, its partial rows (the combine then writes the output).
+enum { kOutSame = 0, kOutF32 = 1, kOutGated = 2, kOutPartials = 3 };
+
 // The new token of a fused decode (the reference's attn_prepare inputs for
 // the 24/4/256 model).  The split kernel prepares the query and attends to
 // the cached keys; its first split's workgroups also prepare the new key and
@@ -50,13 +55,16 @@ struct SplitArgs {
     int q_heads, kv_heads, group, rows, position, n_keys, n_pages, splits;
     float scale_log2;
     FusedToken tok;       // the fused decode instance's query source
+    void *out;            // direct output: [tokens][q_heads][D] (one split per KV head)
 };
 
-// attention_ring instance (ring.hip) for head_dim D (128 or 256) and nqt
-// query tiles (1..4); precise (fp32 hi + lo) queries run on fp16 pages only
-// (nullptr otherwise).  It takes kRingThreads threads and SplitArgs.
+// attention_ring instance (ring.hip) for head_dim D (128 or 256), nqt query
+// tiles (1..3) and output mode (kOutPartials, or a direct output: kOutSame
+// and kOutF32 for 16-bit queries, kOutF32 for precise ones);
+// precise (fp32 hi + lo) queries run on fp16 pages only.  nullptr for other
+// combinations.  It takes kRingThreads threads and SplitArgs.
 constexpr int kRingThreads = 512;
-const void *ring_kernel(int D, int nqt, Dtype dtype, bool precise);
+const void *ring_kernel(int D, int nqt, Dtype dtype, bool precise, int out_mode);
 
 // The split-K decomposition chosen for one launch of the partial kernel.
 struct SplitPlan {
@@ -66,7 +74,17 @@ struct SplitPlan {
     int n_pages;     // 32-key pages per KV head holding keys 0..n_keys-1
     int splits;      // workgroups per KV head
     bool half_parts; // partial rows stored as fp16 O / l (the raw fp16 ring kernel)
+    bool direct;     // one split per KV head that writes the output itself (no combine)
 };
+
+// Contexts of up to kDirectStreamPages (decode) or kDirectRingPages
+// (verification) pages per KV head run in one workgroup per KV head, which
+// writes the output rows directly: a short context is bound by latency, and
+// the combine launch costs more than the split-K parallelism gains.  Measured
+// on 16 layers in a graph (fp16, 24/4/256): one token at 16..240 cached keys
+// 5.2..8.4 us against 8.7..9.8 us with split + combine; eight tokens at 16,
+// 64, 128, 240 keys 6.0, 7.9, 9.4, 12.2 us against 9.1, 9.2, 9.4, 9.5 us.
+constexpr int kDirectStreamPages = 8, kDirectRingPages = 4;
 
 // Largest number of query rows (group * tokens) per KV head that one launch of
 // the split kernel holds; longer token runs are processed in chunks.
@@ -75,10 +93,16 @@ constexpr int kMaxRows = 48;
 constexpr long long kMaxQueryRows = 1LL << 28;
 
 int device_cu_count();
-SplitPlan plan_split(const Shape &s, int chunk_tokens, Dtype dtype, bool precise);
+// allow_direct: the caller writes the output with the split kernel when the
+// plan is direct (qv_attention's ungated calls); the two-phase entry points
+// and gated outputs always combine (the combine requests the gate with the
+// partials, where a direct split would wait one more round trip for it).
+SplitPlan plan_split(const Shape &s, int chunk_tokens, Dtype dtype, bool precise, bool allow_direct = false);
 // Tokens per chunk for a shape (chunk_tokens * group <= kMaxRows).
 int chunk_tokens(const Shape &s);
-// Workspace bytes for qv_attention on this shape (largest chunk).
+// Workspace bytes for qv_attention on this shape (largest chunk, as if every
+// chunk combined its partials: an upper bound that also serves the two-phase
+// entry points).
 size_t attention_workspace_bytes(const Shape &s, Dtype dtype, bool precise);
 
 // Split-K partial kernel over the pages of every KV head.  q is 16-bit of
@@ -88,9 +112,12 @@ size_t attention_workspace_bytes(const Shape &s, Dtype dtype, bool precise);
 // (unnormalised), or fp16 O / l in the first half of that region when
 // plan.half_parts, then m and l [kv_heads][splits][2][rows] float32.
 size_t plan_bytes(const Shape &s, const SplitPlan &p);
+// A direct plan writes out (fp32 when out_f32, else `dtype`) instead of
+// the workspace.
 void launch_split(const Shape &s, const SplitPlan &plan, Dtype dtype, bool precise,
                   float scale, const void *q, const void *q_lo, const void *k_pages,
-                  const void *v_pages, void *workspace, hipStream_t stream);
+                  const void *v_pages, void *workspace, hipStream_t stream,
+                  void *out = nullptr, bool out_f32 = false);
 // Log-sum-exp combine of the partials into out.  Raw mode writes `dtype`
 // [tokens][q_heads][D]; fused mode (gate != nullptr) writes float32 and
 // multiplies by sigmoid(gate), gate being q_gate[t][h][D + d] (row stride 2D).
@@ -111,6 +138,14 @@ size_t fused_tokens_workspace_bytes(int tokens, int position);
 // the ring kernel's prologue and the new keys in the combine cost more than
 // the launch they save (28.3-32.2 against 28.8 us per layer).
 constexpr int kMaxFusedSplitTokens = 1;
+
+// The fused k_attention of up to kShortMaxTokens new tokens when position +
+// tokens <= kShortFusedKeys (short.hip): one launch, one workgroup per (token,
+// KV head) that prepares its query rows and the new keys, appends its token's
+// key and value, attends to the cached and the new keys and gates the rows.
+// No workspace.
+constexpr int kShortMaxTokens = 8, kShortFusedKeys = 256;
+void launch_fused_short(const FusedToken &tok, float *out, hipStream_t stream);
 
 // Chunked prefill: all group*tokens query rows against the pages in one
 // launch (no workspace); `dtype` q and out, [tokens][q_heads][D].  A precise

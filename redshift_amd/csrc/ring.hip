@@ -67,7 +67,10 @@ constexpr int kRingBuffers = 4;   // NBUF-1 pages in flight while one is consume
 constexpr int kStreamLoad = 2;
 constexpr float kLazy = 8.f;   // lazy row-max threshold, log2 units
 
-template <int D, int NQT, bool PSPLIT, typename KV, bool QSPLIT = false>
+// OUT: kOutPartials stores the split's partial rows; a direct output
+// (kOutSame or kOutF32: one split per KV head) stores the final rows
+// instead, and no combine runs.
+template <int D, int NQT, bool PSPLIT, typename KV, bool QSPLIT = false, int OUT = kOutPartials>
 __global__ __launch_bounds__(kRingWaves * kWave, 1)
 void attention_ring(SplitArgs a) {
     using V8 = typename Vec8<KV>::type;
@@ -75,7 +78,7 @@ void attention_ring(SplitArgs a) {
     constexpr int KS = D / 32, DT = D / 16;
     constexpr int PAGE = 32 * D;                   // elements of one K (or V) page
     // Raw fp16: partial rows stored as fp16 O / l (SplitPlan::half_parts).
-    constexpr bool HALF = !QSPLIT && std::is_same<KV, _Float16>::value;
+    constexpr bool HALF = OUT == kOutPartials && !QSPLIT && std::is_same<KV, _Float16>::value;
     constexpr int CHUNKS = 2 * PAGE * 2 / 1024;    // 1 KiB chunks of [K | V]
     constexpr int CPW = CHUNKS / kRingWaves;       // chunks (loads) per wave per page
     static_assert(CHUNKS % kRingWaves == 0, "chunks divide over the waves");
@@ -324,7 +327,26 @@ void attention_ring(SplitArgs a) {
         const float mu = M == -INFINITY ? 0.f : M;
         const float f0 = __builtin_amdgcn_exp2f(m - mu), f1 = __builtin_amdgcn_exp2f(m1 - mu);
         const int r = 16 * qt + (lane & 15);
-        if (r < a.rows) {
+        if (OUT != kOutPartials && r < a.rows) {
+            // The only split of this KV head: the final rows.  Every row sees
+            // key 0, so L > 0.  Lane group g holds dims 4g..4g+3 of every
+            // 16-dim tile.
+            const int t = r / a.group, head = h * a.group + (r - t * a.group);
+            const size_t hrow = (size_t)t * a.q_heads + head;       // [token][head] row
+            const size_t orow = hrow * D + 4 * g;                   // out: rows of D
+            const float inv = 1.f / (l * f0 + l1 * f1);
+#pragma unroll
+            for (int dt = 0; dt < DT; ++dt) {
+                const f32x4 o1 = *reinterpret_cast<const f32x4 *>(xacc + (dt * kWave + lane) * 4);
+                const f32x4 o = (acc[dt] * f0 + o1 * f1) * inv;
+                if constexpr (OUT == kOutSame) {
+                    const V4 v = {(KV)o[0], (KV)o[1], (KV)o[2], (KV)o[3]};
+                    *reinterpret_cast<V4 *>(static_cast<KV *>(a.out) + orow + dt * 16) = v;
+                } else {
+                    *reinterpret_cast<f32x4 *>(static_cast<float *>(a.out) + orow + dt * 16) = o;
+                }
+            }
+        } else if (OUT == kOutPartials && r < a.rows) {
             float *pml = a.part_ml + ((size_t)h * a.splits + split) * 2 * a.rows;
             const size_t prow = (((size_t)h * a.splits + split) * a.rows + r) * D + 4 * g;
             const float L = l * f0 + l1 * f1;
@@ -373,46 +395,44 @@ void attention_ring(SplitArgs a) {
     }
 }
 
-// Raw fp16: 16-bit P; raw bf16: hi + lo P (bf16's 8-bit significand alone
-// would dominate the error).
+// Instances: raw fp16 multiplies V by a 16-bit P, raw bf16 by hi + lo P
+// (bf16's 8-bit significand alone would dominate the error), and fp32
+// queries (hi + lo fp16 parts) by hi + lo P as well.
+template <int D, int NQT, int OUT>
+const void *pick(Dtype dtype, bool precise) {
+    if (precise) {
+        if constexpr (OUT == kOutSame) return nullptr;
+        else return dtype == Dtype::F16 ? (const void *)&attention_ring<D, NQT, true, _Float16, true, OUT> : nullptr;
+    }
+    if (dtype == Dtype::BF16) return (const void *)&attention_ring<D, NQT, true, __bf16, false, OUT>;
+    return (const void *)&attention_ring<D, NQT, false, _Float16, false, OUT>;
+}
+
 template <int D, int NQT>
-const void *pick(Dtype dtype) {
-    if (dtype == Dtype::BF16) return (const void *)&attention_ring<D, NQT, true, __bf16>;
-    return (const void *)&attention_ring<D, NQT, false, _Float16>;
+const void *pick_out(Dtype dtype, bool precise, int out_mode) {
+    switch (out_mode) {
+        case kOutPartials: return pick<D, NQT, kOutPartials>(dtype, precise);
+        case kOutSame: return pick<D, NQT, kOutSame>(dtype, precise);
+        case kOutF32: return pick<D, NQT, kOutF32>(dtype, precise);
+    }
+    return nullptr;
 }
 
 template <int D>
-const void *pick_tiles(int nqt, Dtype dtype) {
+const void *pick_tiles(int nqt, Dtype dtype, bool precise, int out_mode) {
     switch (nqt) {
-        case 1: return pick<D, 1>(dtype);
-        case 2: return pick<D, 2>(dtype);
-        case 3: return pick<D, 3>(dtype);
-        case 4: return pick<D, 4>(dtype);
+        case 1: return pick_out<D, 1>(dtype, precise, out_mode);
+        case 2: return pick_out<D, 2>(dtype, precise, out_mode);
+        case 3: return pick_out<D, 3>(dtype, precise, out_mode);
     }
     return nullptr;
 }
 
 }  // namespace
 
-// fp32 queries (hi + lo fp16 parts): hi + lo P as well.
-template <int D>
-const void *pick_precise(int nqt) {
-    switch (nqt) {
-        case 1: return (const void *)&attention_ring<D, 1, true, _Float16, true>;
-        case 2: return (const void *)&attention_ring<D, 2, true, _Float16, true>;
-        case 3: return (const void *)&attention_ring<D, 3, true, _Float16, true>;
-        case 4: return (const void *)&attention_ring<D, 4, true, _Float16, true>;
-    }
-    return nullptr;
-}
-
-const void *ring_kernel(int D, int nqt, Dtype dtype, bool precise) {
-    if (precise) {
-        if (dtype != Dtype::F16) return nullptr;
-        return D == 256 ? pick_precise<256>(nqt) : D == 128 ? pick_precise<128>(nqt) : nullptr;
-    }
-    if (D == 256) return pick_tiles<256>(nqt, dtype);
-    if (D == 128) return pick_tiles<128>(nqt, dtype);
+const void *ring_kernel(int D, int nqt, Dtype dtype, bool precise, int out_mode) {
+    if (D == 256) return pick_tiles<256>(nqt, dtype, precise, out_mode);
+    if (D == 128) return pick_tiles<128>(nqt, dtype, precise, out_mode);
     return nullptr;
 }
 

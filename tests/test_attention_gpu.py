@@ -346,6 +346,38 @@ def test_fused_verify_matches_oracle(gpu, batch, position):
     assert_close(vc.float().cpu().numpy(), expected[2], 0)
 
 
+@pytest.mark.parametrize('position', [0, 100, 247])
+def test_short_fused_appends_the_prepare_kernels_bits(gpu, position):
+    """A short context (8 tokens, position + 8 <= 256) runs in one launch
+    that prepares and appends the new keys itself; the same tokens as the
+    start of a 9-token prefill chunk go through the prepare kernel.  Both
+    append the same bits, and both outputs match the oracle."""
+    torch = gpu
+    c = kat.sine_wave_case(batch=9, position=position)
+    dev = {name: torch.from_numpy(f32(c[name])).cuda() for name in ('q_gate', 'key', 'value', 'q_norm', 'k_norm')}
+    caches = []
+    for _ in range(2):
+        cache = A.PagedKV(4, 256, A.round_capacity(position + 9), torch.float16)
+        cache.k.fill_(float('nan'))
+        cache.v.fill_(float('nan'))
+        if position:
+            cache.pack(torch.from_numpy(c['key_cache']).cuda(), torch.from_numpy(c['value_cache']).cuda())
+        caches.append(cache)
+    short = A.attention_fused(dev['q_gate'][:8], dev['key'][:8], dev['value'][:8], dev['q_norm'], dev['k_norm'],
+                              caches[0], position, c['epsilon'])
+    chunk = A.attention_fused(dev['q_gate'], dev['key'], dev['value'], dev['q_norm'], dev['k_norm'],
+                              caches[1], position, c['epsilon'])
+    kc = [cache.unpack(0, position + 8) for cache in caches]
+    torch.cuda.synchronize()
+    for a, b in zip(kc[0], kc[1]):
+        assert torch.equal(a.view(torch.int16), b.view(torch.int16))
+    expected = ref.fused_attention(c['key_cache'], c['value_cache'], c['q_gate'], c['key'], c['value'],
+                                   c['q_norm'], c['k_norm'], 9, position, c['epsilon'])
+    assert_close(short.cpu().numpy().reshape(-1), expected[0][:8 * 6144], 3e-4)
+    assert_close(chunk.cpu().numpy().reshape(-1), expected[0], 3e-4)
+    assert_close(short.cpu().numpy(), chunk[:8].cpu().numpy(), 3e-5)
+
+
 @pytest.mark.parametrize('batch,position', [(100, 300), (57, 1)])
 def test_fused_prefill_chunk_matches_oracle(gpu, batch, position):
     """A prefill chunk through the fused entry (more than 8 tokens: prepare,
@@ -390,7 +422,38 @@ def test_fused_prefill_chunk_equals_eight_token_steps(gpu):
         assert torch.equal(a.view(torch.int16), b.view(torch.int16))
 
 
-@pytest.mark.parametrize('T,position', [(1, 50000), (8, 2000)])
+@pytest.mark.parametrize('q_heads,kv_heads,head_dim,T,position,dtype', [
+    (24, 4, 256, 1, 0, 'f16'), (24, 4, 256, 1, 255, 'bf16'),       # stream kernel, 1 and 8 pages
+    (24, 4, 256, 8, 16, 'f16'), (24, 4, 256, 8, 248, 'bf16'),      # ring kernel, 1 and 8 pages
+    (16, 2, 128, 3, 100, 'f16'), (8, 8, 128, 1, 200, 'bf16'),
+])
+def test_short_context_direct_output_equals_combined(gpu, q_heads, kv_heads, head_dim, T, position, dtype):
+    """Up to 8 pages per KV head, qv_attention runs one split per KV head
+    that writes the rows itself; the two-phase entry points store partials
+    and combine them.  Both against the oracle, and against each other."""
+    torch = gpu
+    w = Workload('short', q_heads, kv_heads, head_dim, T, position, 1 / head_dim ** .5, dtype, 40 + T, 1.0, 0.5)
+    q, k, v, _ = make_inputs(w)
+    want = ref.gqa_attention(to_float(q, dtype), to_float(k, dtype), to_float(v, dtype), position, w.scale)
+    cache = make_cache(k, v, w, torch, fill_nan=True)
+    qt = to_torch(q, dtype, torch)
+    ws = A.workspace(A.attention_workspace_bytes(q_heads, kv_heads, head_dim, T, position))
+    direct = A.attention(qt, cache, position, w.scale, ws=ws, out_dtype=torch.float32)
+    combined = torch.empty_like(direct)
+    A.attention_split(qt, cache, position, w.scale, ws)
+    A.attention_combine(combined, cache, position, ws)
+    torch.cuda.synchronize()
+    direct, combined = direct.cpu().numpy().astype(np.float64), combined.cpu().numpy().astype(np.float64)
+    assert_parity(direct, want)
+    assert_parity(combined, want)
+    # The fp16 ring kernel's partial rows are fp16 O / l (2^-11 relative);
+    # every other pair differs by fp32 reassociation only.
+    half_parts = dtype == 'f16' and T * (q_heads // kv_heads) > 16
+    tolerance = 2.0 ** -10 * np.abs(want).max() if half_parts else 1e-5
+    assert np.abs(direct - combined).max() <= tolerance
+
+
+@pytest.mark.parametrize('T,position', [(1, 50000), (8, 2000), (8, 100)])
 def test_graph_replay_matches_eager(gpu, T, position):
     """The device entry points enqueue kernels only (no allocation, no
     synchronisation, no memset), so they can be captured in a HIP graph; every
