@@ -365,7 +365,8 @@ def main():
     ap.add_argument('--no-cpu', action='store_true', help='skip the CPU baseline')
     ap.add_argument('--no-extra', action='store_true', help='skip the secondary workloads')
     ap.add_argument('--extras', default='verify8_16k,decode_4k,prefill_2k,fused_verify8_16k,fused_decode_139k,'
-                                        'fused_prefill_2k,kv_checkpoint_139k',
+                                        'fused_prefill_2k,fused_verify8_prefix16,fused_verify8_prefix128,'
+                                        'kv_checkpoint_139k',
                     help='comma-separated secondary workloads to run')
     ap.add_argument('--drop-in', action='store_true',
                     help='only time the host-buffer qv_test_attention (PCIe-inclusive) and exit')
@@ -415,7 +416,10 @@ def main():
         'roofline': {'bound': 'hbm', 'kernel': 'attention_stream (decode split-K)',
                      'achieved': round(split_gbs, 1), 'peak': HBM_PEAK_GBS, 'unit': 'GB/s',
                      'frac': round(split_gbs / HBM_PEAK_GBS, 4), 'traffic': measured_traffic(),
-                     'kernel_us': round(r['split_us'], 2), 'bytes_per_launch': w.kv_bytes()},
+                     'kernel_us': round(r['split_us'], 2), 'bytes_per_launch': w.kv_bytes(),
+                     'frac_step': round(gbs / HBM_PEAK_GBS, 4),
+                     'frac_is': 'frac: the split-K kernel alone (kernel_us); frac_step: the whole layer, '
+                                'split-K + combine kernels in the graph step (us_per_layer)'},
     }
     chosen = [] if args.no_extra else [x for x in args.extras.split(',') if x]
     if chosen:
@@ -471,6 +475,22 @@ def main():
                                          'frac_mfma_peak': round(wq.flops() / (us * 1e-6) / MFMA_BF16_PEAK, 4),
                                          'what': 'qv_attention_fused on a 2048-token chunk at 6144: prepare + '
                                                  'append + precise prefill (fp32 q as fp16 hi + lo, hi + lo P) + gate'}
+        for prefix in (16, 128):
+            name = f'fused_verify8_prefix{prefix}'
+            if name not in chosen:
+                continue
+            # The reference's only published timing of this path: T=8
+            # candidates on a short prefix, qv::attention 8,642.7 ns plus
+            # qv::attn_prepare 4,088.0 ns per layer on a V100
+            # (reports/llama-v100-profile-redshift-b8.txt:14-15).
+            ws_ = Workload(name, 24, 4, 256, 8, prefix, 1 / 16, 'f16', 7, kv_std=0.5)
+            log(f'{name}: {args.layers} layers')
+            us = 1000 * time_fused(torch, A, ws_, args.layers, args.steps, args.warmup, seed=8) / args.layers
+            extra[name] = {'us_per_layer': round(us, 2),
+                           'reference_v100_us': 12.73,
+                           'what': f'qv_attention_fused per layer, 8 tokens after a {prefix}-token prefix '
+                                   '(prepare + append + attention + gate), graph step; reference: '
+                                   'V100 qv::attention 8.64 us + qv::attn_prepare 4.09 us'}
         if 'kv_checkpoint_139k' in chosen:
             log('kv_checkpoint_139k: 4 layers')
             us = time_kv_copy(torch, A, w, 4, max(5, args.steps // 2), 2, seed=5)
