@@ -16,6 +16,17 @@ ROOT = PACKAGE.parent
 SOURCES = ['abi.cpp', 'attention.hip', 'kv.hip', 'prefill.hip', 'ring.hip', 'short.hip']
 LIBRARY = PACKAGE / 'lib' / 'libredshift_hip.so'
 ARCH = 'gfx950'
+# The host-sanitizer gate: the library's sources and a driver over its C ABI,
+# with AddressSanitizer and UndefinedBehaviorSanitizer on the host code only
+# (every -fsanitize flag goes to the host pass; the device code is the
+# ordinary gfx950 build).
+SANITIZE_DRIVER = ROOT / 'tests' / 'native' / 'abi_sanitize.cpp'
+SANITIZE_BINARY = ROOT / 'tests' / 'native' / 'abi_sanitize'
+SANITIZE_FLAGS = [
+    '-Xarch_host', '-fsanitize=address', '-Xarch_host', '-fsanitize=undefined',
+    '-Xarch_host', '-fno-sanitize-recover=undefined', '-Xarch_host', '-fno-omit-frame-pointer',
+    '-Xarch_host', '-g',
+]
 
 # Packed-FP32 instructions are kept out of every code object: hipcc would
 # otherwise form v_pk_{add,mul,fma}_f32 from ordinary float code.
@@ -54,31 +65,55 @@ def _run(cmd):
     return stderr
 
 
-def build(verbose=False, jobs=None):
-    """Compile every source and link the shared library; returns its path."""
+def _compile_all(objdir, sources, extra, jobs):
+    """Compile (name, path) sources into objdir in parallel; returns the
+    objects and the compilers' messages."""
     compiler = hipcc()
-    objdir = PACKAGE / '_build'
-    objdir.mkdir(exist_ok=True)
-    LIBRARY.parent.mkdir(exist_ok=True)
-    jobs = jobs or min(len(SOURCES), os.cpu_count() or 1)
+    objdir.mkdir(parents=True, exist_ok=True)
 
-    def compile_one(name):
-        src = PACKAGE / 'csrc' / name
+    def compile_one(item):
+        name, src = item
         obj = objdir / (name + '.o')
-        cmd = [compiler, '-x', 'hip', *COMMON_FLAGS, *SOURCE_FLAGS.get(name, []), '-c', str(src), '-o', str(obj)]
+        cmd = [compiler, '-x', 'hip', *COMMON_FLAGS, *SOURCE_FLAGS.get(name, []), *extra, '-c', str(src),
+               '-o', str(obj)]
         return obj, _run(cmd)
 
+    jobs = jobs or min(len(sources), os.cpu_count() or 1)
     with ThreadPoolExecutor(jobs) as pool:
-        results = list(pool.map(compile_one, SOURCES))
-    for obj, stderr in results:
+        return list(pool.map(compile_one, sources))
+
+
+def build(verbose=False, jobs=None):
+    """Compile every source and link the shared library; returns its path."""
+    sources = [(name, PACKAGE / 'csrc' / name) for name in SOURCES]
+    results = _compile_all(PACKAGE / '_build', sources, [], jobs)
+    for _, stderr in results:
         if verbose and stderr:
             print(stderr, file=sys.stderr)
+    LIBRARY.parent.mkdir(exist_ok=True)
     tmp = LIBRARY.with_suffix('.so.tmp')
-    _run([compiler, '-shared', '-fPIC', f'--offload-arch={ARCH}', *[str(o) for o, _ in results],
+    _run([hipcc(), '-shared', '-fPIC', f'--offload-arch={ARCH}', *[str(o) for o, _ in results],
           '-o', str(tmp)])
     os.replace(tmp, LIBRARY)
     return LIBRARY
 
 
+def build_sanitizer(verbose=False, jobs=None):
+    """Link the host-sanitizer driver with a sanitized build of every source;
+    returns the executable's path."""
+    sources = [(name, PACKAGE / 'csrc' / name) for name in SOURCES]
+    sources.append((SANITIZE_DRIVER.name, SANITIZE_DRIVER))
+    results = _compile_all(PACKAGE / '_build' / 'sanitize', sources, SANITIZE_FLAGS, jobs)
+    for _, stderr in results:
+        if verbose and stderr:
+            print(stderr, file=sys.stderr)
+    tmp = SANITIZE_BINARY.with_name(SANITIZE_BINARY.name + '.tmp')
+    _run([hipcc(), f'--offload-arch={ARCH}', *SANITIZE_FLAGS[:4], *[str(o) for o, _ in results],
+          '-o', str(tmp)])
+    os.replace(tmp, SANITIZE_BINARY)
+    return SANITIZE_BINARY
+
+
 if __name__ == '__main__':
     print(build(verbose='-v' in sys.argv))
+    print(build_sanitizer(verbose='-v' in sys.argv))

@@ -241,7 +241,6 @@ extern "C" int qv_test_attention(float *out, void *key_cache, void *value_cache,
         constexpr int H = rs::kModelQHeads, HKV = rs::kModelKvHeads, D = rs::kModelHeadDim;
         const int n = position + batch;
         const int capacity = (n + rs::kPageTokens - 1) / rs::kPageTokens * rs::kPageTokens;
-        const rs::Shape shape{H, HKV, D, batch, position, capacity};
         const size_t out_bytes = (size_t)batch * H * D * sizeof(float);
         const size_t kv_bytes = (size_t)batch * HKV * D * sizeof(float);
         const size_t row_bytes = (size_t)HKV * D * sizeof(uint16_t);
@@ -356,13 +355,13 @@ extern "C" int qv_kv_copy(void *dst_k, void *dst_v, const void *src_k, const voi
         geometry(kv_heads, head_dim, dst_capacity);
         geometry(kv_heads, head_dim, src_capacity);
         require(tokens >= 0, "tokens must be non-negative");
-        const int pages = (tokens + rs::kPageTokens - 1) / rs::kPageTokens;
-        require((long long)pages * rs::kPageTokens <= std::min(dst_capacity, src_capacity),
+        const long long pages = ((long long)tokens + rs::kPageTokens - 1) / rs::kPageTokens;
+        require(pages * rs::kPageTokens <= std::min(dst_capacity, src_capacity),
                 "the pages of tokens exceed a cache capacity");
         require(dst_k && dst_v && src_k && src_v, "null KV cache");
         require(aligned16(dst_k) && aligned16(dst_v) && aligned16(src_k) && aligned16(src_v),
                 "KV caches must be 16-byte aligned");
-        rs::launch_copy(dst_k, dst_v, src_k, src_v, kv_heads, head_dim, dst_capacity, src_capacity, pages,
+        rs::launch_copy(dst_k, dst_v, src_k, src_v, kv_heads, head_dim, dst_capacity, src_capacity, (int)pages,
                         static_cast<hipStream_t>(stream));
     });
 }

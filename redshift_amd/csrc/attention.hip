@@ -510,7 +510,8 @@ int blocks_per_cu(const void *kernel, int threads) {
     return n;
 }
 
-SplitPlan plan_split(const Shape &s, int tokens, Dtype dtype, bool precise, bool allow_direct) {
+SplitPlan plan_split_for(const Shape &s, int tokens, Dtype dtype, bool precise, bool allow_direct,
+                         int cus, int (*resident_per_cu)(const SplitPlan &, int D, Dtype, bool)) {
     SplitPlan p;
     p.rows = s.group() * tokens;
     p.nqt = (p.rows + 15) / 16;
@@ -523,15 +524,14 @@ SplitPlan plan_split(const Shape &s, int tokens, Dtype dtype, bool precise, bool
     p.direct = allow_direct && p.n_pages <= (p.kind == SplitKind::Stream ? kDirectStreamPages : kDirectRingPages);
     if (p.direct) return p;
     // Fill every CU with as many workgroups as stay resident.
-    const int resident = device_cu_count() *
-                         blocks_per_cu(split_kernel(p, s.head_dim, dtype, precise), block_threads(p));
+    const int resident = cus * resident_per_cu(p, s.head_dim, dtype, precise);
     int per_head = std::max(1, std::min(resident / s.kv_heads, kMaxSplits));
     if (p.kind == SplitKind::Stream) {
         // Decode streams fastest from three quarters of the CUs: on the
         // 139,264-key decode (4 KV heads) 48 splits per head (192
         // workgroups) take 95.5 us against 97.6 us for 64, and the combine
         // has fewer partials to merge.
-        per_head = std::max(1, std::min(per_head, device_cu_count() * 3 / (4 * s.kv_heads)));
+        per_head = std::max(1, std::min(per_head, cus * 3 / (4 * s.kv_heads)));
         // Every wave gets at least one page on average.
         p.splits = std::max(1, std::min(per_head, (p.n_pages + kWaves - 1) / kWaves));
     } else {
@@ -544,6 +544,16 @@ SplitPlan plan_split(const Shape &s, int tokens, Dtype dtype, bool precise, bool
     // the partial traffic, which every workgroup writes at once at the end.
     p.half_parts = p.kind == SplitKind::Ring && dtype == Dtype::F16 && !precise;
     return p;
+}
+
+namespace {
+int resident_on_device(const SplitPlan &p, int D, Dtype dtype, bool precise) {
+    return blocks_per_cu(split_kernel(p, D, dtype, precise), block_threads(p));
+}
+}  // namespace
+
+SplitPlan plan_split(const Shape &s, int tokens, Dtype dtype, bool precise, bool allow_direct) {
+    return plan_split_for(s, tokens, dtype, precise, allow_direct, device_cu_count(), resident_on_device);
 }
 
 size_t plan_bytes(const Shape &s, const SplitPlan &p) {

@@ -98,6 +98,11 @@ int device_cu_count();
 // and gated outputs always combine (the combine requests the gate with the
 // partials, where a direct split would wait one more round trip for it).
 SplitPlan plan_split(const Shape &s, int chunk_tokens, Dtype dtype, bool precise, bool allow_direct = false);
+// plan_split on `cus` CUs of which each holds resident_per_cu(plan, D,
+// dtype, precise) workgroups of the chosen split kernel: no device query
+// (plan_split passes the current device's figures).
+SplitPlan plan_split_for(const Shape &s, int chunk_tokens, Dtype dtype, bool precise, bool allow_direct,
+                         int cus, int (*resident_per_cu)(const SplitPlan &, int D, Dtype, bool));
 // Tokens per chunk for a shape (chunk_tokens * group <= kMaxRows).
 int chunk_tokens(const Shape &s);
 // Workspace bytes for qv_attention on this shape (largest chunk, as if every
