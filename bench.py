@@ -364,7 +364,7 @@ def main():
     ap.add_argument('--layers', type=int, default=LAYERS)
     ap.add_argument('--no-cpu', action='store_true', help='skip the CPU baseline')
     ap.add_argument('--no-extra', action='store_true', help='skip the secondary workloads')
-    ap.add_argument('--extras', default='verify8_16k,decode_4k,prefill_2k,fused_verify8_16k,fused_decode_139k,'
+    ap.add_argument('--extras', default='verify8_16k,decode_16k,decode_4k,prefill_2k,fused_verify8_16k,fused_decode_139k,'
                                         'fused_prefill_2k,fused_verify8_prefix16,fused_verify8_prefix128,'
                                         'kv_checkpoint_139k',
                     help='comma-separated secondary workloads to run')
@@ -424,7 +424,7 @@ def main():
     chosen = [] if args.no_extra else [x for x in args.extras.split(',') if x]
     if chosen:
         extra = {}
-        for name in ('verify8_16k', 'decode_4k'):
+        for name in ('verify8_16k', 'decode_16k', 'decode_4k'):
             if name not in chosen:
                 continue
             wx = WORKLOADS[name]

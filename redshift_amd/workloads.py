@@ -58,6 +58,9 @@ WORKLOADS = {
         Workload('cpu_plumbing', 8, 2, 128, 1, 127, 1 / math.sqrt(128), 'f32', 0),
         Workload('decode_4k', 24, 4, 256, 1, 4095, 1 / 16, 'f16', 0, q_std=1.0, kv_std=0.5),
         Workload('verify8_16k', 24, 4, 256, 8, 16384, 1 / 16, 'f16', 1, q_std=0.5, kv_std=0.5),
+        # One token over the verify-8 workload's 16,392 keys: the same K/V
+        # bytes streamed with one query row per query head.
+        Workload('decode_16k', 24, 4, 256, 1, 16391, 1 / 16, 'f16', 1, q_std=0.5, kv_std=0.5),
         Workload('decode_139k', 24, 4, 256, 1, 139263, 1 / 16, 'f16', 3, q_std=0.5, kv_std=0.5,
                  outliers=64),
         Workload('prefill_2k', 24, 4, 256, 2048, 6144, 1 / 16, 'bf16', 2),

@@ -198,7 +198,7 @@ def gpu_attention(w, q, k, v, torch, out_dtype=None, **kw):
     return out.float().cpu().numpy().astype(np.float64)
 
 
-@pytest.mark.parametrize('name', ['decode_4k', 'verify8_16k', 'decode_139k'])
+@pytest.mark.parametrize('name', ['decode_4k', 'decode_16k', 'verify8_16k', 'decode_139k'])
 def test_raw_attention_workloads(gpu, name):
     w = WORKLOADS[name]
     q, k, v, _ = make_inputs(w)
