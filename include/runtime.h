@@ -153,9 +153,11 @@ int qv_attention_combine(void *out, int dtype, int out_dtype, int q_heads, int k
  * allocate device memory (code under HIP graph capture, tight serving loops,
  * harnesses that forbid hipMalloc).  No counterpart in the reference.  It
  * runs the same kernels, and gives the same bits, as qv_attention; the
- * split-K partials live in a static device array of 16 MiB per GPU, held
- * until the process ends (the largest plan on a 256-CU MI355X takes
- * 12.1 MiB; a shape that needs more is refused).  The call itself allocates
+ * workspace (split-K partials, or a bf16 prefill's fp16 copy of its V pages)
+ * lives in a static device array of 64 MiB per GPU, held until the process
+ * ends (the largest split-K plan on a 256-CU MI355X takes 12.1 MiB, a bf16
+ * prefill kv_heads*keys*head_dim*2 bytes; a shape that needs more is
+ * refused).  The call itself allocates
  * nothing.  Every call on one GPU shares that GPU's array: calls that
  * overlap on one GPU (concurrent streams, or threads) race on it, so
  * serialise them.  No kernel reads a partial it has not written in the same

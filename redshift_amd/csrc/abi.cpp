@@ -122,8 +122,10 @@ void run_attention(const rs::Shape &s, rs::Dtype dtype, bool precise, float scal
                    void *workspace, void *out, bool out_f32, const float *gate,
                    hipStream_t stream) {
     if (s.group() * s.tokens > rs::kMaxRows) {
-        // Long token runs (chunked prefill): one launch, no workspace.
-        rs::launch_prefill(s, dtype, precise, scale, q, q_lo, k_pages, v_pages, out, out_f32, gate, stream);
+        // Long token runs (chunked prefill): one launch (two for bf16 pages,
+        // whose workspace holds one word per workgroup).
+        rs::launch_prefill(s, dtype, precise, scale, q, q_lo, k_pages, v_pages, out, out_f32, gate, workspace,
+                           stream);
         return;
     }
     const size_t out_elem = out_f32 ? sizeof(float) : sizeof(uint16_t);
@@ -407,12 +409,14 @@ extern "C" int qv_attention(void *out, const void *q, const void *k_pages, const
     });
 }
 
-// ---- qv_attention_noalloc: the split-K partials in a static device array --
+// ---- qv_attention_noalloc: the workspace in a static device array --------
 // One array per GPU, loaded with the library's code object and held until the
-// process ends.  The largest plan on a 256-CU part is 256 workgroups x 48 rows
-// x (256 + 2) floats = 12.1 MiB (split counts are capped by the resident
-// workgroups, and a KV head never has fewer than one split).
-constexpr size_t kScratchBytes = size_t(16) << 20;
+// process ends.  The largest split-K plan on a 256-CU part is 256 workgroups
+// x 48 rows x (256 + 2) floats = 12.1 MiB (split counts are capped by the
+// resident workgroups, and a KV head never has fewer than one split); a bf16
+// prefill keeps an fp16 copy of its V pages there, kv_heads x keys x
+// head_dim x 2 bytes (32 MiB for 4 x 256 at 16,384 keys).
+constexpr size_t kScratchBytes = size_t(64) << 20;
 static __device__ __align__(256) unsigned char scratch[kScratchBytes];
 
 namespace {
@@ -448,7 +452,7 @@ extern "C" int qv_attention_noalloc(void *out, const void *q, const void *k_page
         void *workspace = scratch_address();
         raw_buffers(out, q, k_pages, v_pages, workspace);
         require(rs::attention_workspace_bytes(s, dt, false) <= kScratchBytes,
-                "the shape needs more than the 16 MiB of split-K scratch of qv_attention_noalloc");
+                "the shape needs more than the 64 MiB of workspace of qv_attention_noalloc");
         run_attention(s, dt, false, scale, q, nullptr, k_pages, v_pages, workspace, out, out_f32,
                       nullptr, static_cast<hipStream_t>(stream));
     });

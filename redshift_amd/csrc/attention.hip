@@ -562,7 +562,7 @@ size_t plan_bytes(const Shape &s, const SplitPlan &p) {
 }
 
 size_t attention_workspace_bytes(const Shape &s, Dtype dtype, bool precise) {
-    if (s.group() * s.tokens > kMaxRows) return 0;   // prefill kernel
+    if (s.group() * s.tokens > kMaxRows) return prefill_workspace_bytes(s, dtype, precise);   // prefill kernel
     const int ct = chunk_tokens(s);
     size_t best = 0;
     for (int t0 = 0; t0 < s.tokens; t0 += ct) {

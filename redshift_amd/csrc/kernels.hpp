@@ -152,14 +152,17 @@ constexpr int kMaxFusedSplitTokens = 1;
 constexpr int kShortMaxTokens = 8, kShortFusedKeys = 256;
 void launch_fused_short(const FusedToken &tok, float *out, hipStream_t stream);
 
-// Chunked prefill: all group*tokens query rows against the pages in one
-// launch (no workspace); `dtype` q and out, [tokens][q_heads][D].  A precise
-// call (fp16 pages) takes the query as hi + lo fp16 parts and writes fp32,
-// times sigmoid of the gate half of q_gate [tokens][q_heads][2D] when `gate`
-// is given.
+// Chunked prefill: all group*tokens query rows against the pages; `dtype` q
+// and out, [tokens][q_heads][D].  A precise call (fp16 pages) takes the query
+// as hi + lo fp16 parts and writes fp32, times sigmoid of the gate half of
+// q_gate [tokens][q_heads][2D] when `gate` is given.  A bf16 call runs two
+// launches (V converted to fp16, then an exact redo of the workgroups that
+// met a V value outside the fp16 range) and keeps one word per workgroup in
+// the workspace (prefill_workspace_bytes; 0 for the other calls).
+size_t prefill_workspace_bytes(const Shape &s, Dtype dtype, bool precise);
 void launch_prefill(const Shape &s, Dtype dtype, bool precise, float scale, const void *q,
                     const void *q_lo, const void *k_pages, const void *v_pages, void *out, bool out_f32,
-                    const float *gate, hipStream_t stream);
+                    const float *gate, void *workspace, hipStream_t stream);
 
 // Whole pages 0 .. pages-1 of every KV head, K and V, from caches of
 // src_capacity tokens to caches of dst_capacity tokens (checkpoint/restore).

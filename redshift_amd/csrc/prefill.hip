@@ -27,8 +27,15 @@
 // SIMD.  Online softmax in base 2 with a lazily moved row max (see ring.hip);
 // scores are scaled before they are masked and their max is taken, so any
 // finite scale (zero and negative ones included) gives the softmax of the
-// scaled scores.  bf16 caches multiply by P split into hi +
-// lo bf16 parts, fp16 caches by a single fp16 P.
+// scaled scores.  P multiplies V as one fp16 value.  On bf16 caches a
+// streaming pass (convert_v_pages) first writes the call's V pages as fp16
+// into the workspace, which is exact for every bf16 value from 2^-14 to
+// 65280 (the fp16 normal range), so bf16 runs one V product per fragment,
+// like fp16, where P split into bf16 hi + lo parts would take two.  A KV
+// head with a V value outside that range (larger, tiny but nonzero in all
+// eight keys that one operand slot holds, or not finite) is flagged by the
+// pass; the fp16 instance skips it and the exact instance (bf16 V, P as
+// bf16 hi + lo) runs it instead, returning at once for the other heads.
 //
 // Scheduling: workgroup i serves KV head i % kv_heads (with 4 KV heads the
 // round-robin dispatch over the 8 XCDs keeps every head on the same two XCDs,
@@ -93,7 +100,13 @@ struct PrefillArgs {
     const void *k_pages;
     const void *v_pages;
     void *out;
-    size_t head_stride;
+    // bf16 calls: the conversion pass's words, flag_words per KV head (a set
+    // word: a V value outside the fp16 range); run_flagged selects the heads
+    // this launch serves (0: the unflagged ones, 1: the flagged ones).
+    const uint32_t *v_flags;
+    int flag_words, run_flagged;
+    size_t head_stride;       // K (and q-side) pages
+    size_t v_head_stride;     // V pages (the converted copy is packed to the call's pages)
     int q_heads, kv_heads, group, rows, position, n_tiles;
     float scale_log2;
 };
@@ -102,15 +115,28 @@ __device__ __forceinline__ int v_slot_token(int g, int j) {
     return j < 4 ? 4 * g + j : 16 + 4 * g + j - 4;
 }
 
-// PSPLIT: P multiplies V as hi + lo 16-bit parts.  QSPLIT: the query is an
-// fp32 one given as hi + lo fp16 parts, both multiplied by K.  MODE: output
-// of the KV type, fp32, or fp32 times sigmoid(gate) (see combine.hpp).
-template <int D, typename KV, bool PSPLIT, bool QSPLIT, int MODE, int ROWS>
+// KV: the query and K page type; VT: the V page type (fp16 for a converted
+// bf16 cache), which P takes as well.  PSPLIT: P multiplies V as hi + lo
+// parts of VT (the precise instance on fp16 pages, the exact instance on
+// bf16 pages).  QSPLIT: the query is an fp32 one given as hi + lo fp16
+// parts, both multiplied by K.  MODE: output of the KV type, fp32, or fp32
+// times sigmoid(gate) (see combine.hpp).
+template <int D, typename KV, typename VT, bool PSPLIT, bool QSPLIT, int MODE, int ROWS>
 __global__ __launch_bounds__(ROWS / 16 * kWave, 1)
 void attention_prefill(PrefillArgs a) {
     using V8 = typename Vec8<KV>::type;
     using OUT = std::conditional_t<MODE == kOutSame, KV, float>;
     typedef uint32_t U4 __attribute__((ext_vector_type(4)));
+    using PT = VT;
+    using PV8 = typename Vec8<PT>::type;
+    if (a.v_flags) {
+        // This launch serves either the KV heads whose V the conversion pass
+        // flagged or the others; every wave reads the same words.
+        const uint32_t *f = a.v_flags + (size_t)(blockIdx.x % a.kv_heads) * a.flag_words;
+        uint32_t any = 0;
+        for (int i = threadIdx.x & 63; i < a.flag_words; i += 64) any |= f[i];
+        if ((__any(any != 0) != 0) != (a.run_flagged != 0)) return;
+    }
     constexpr int kPWaves = ROWS / 16;
     constexpr int KS = D / 32, DT = D / 16;
     constexpr int PAGE = 32 * D;                       // elements of one K (or V) page
@@ -121,7 +147,7 @@ void attention_prefill(PrefillArgs a) {
     constexpr int H = PAGE_BYTES / 1024 / kLoaders;
     static_assert(H >= 1 && PAGE_BYTES / 1024 % kLoaders == 0, "loads divide over the loader waves");
     __shared__ __attribute__((aligned(16))) KV kring[4 * PAGE];
-    __shared__ __attribute__((aligned(16))) KV vring[4 * PAGE];
+    __shared__ __attribute__((aligned(16))) VT vring[4 * PAGE];
 
     const int lane = threadIdx.x & 63, g = lane >> 4;
     const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);   // wave index (uniform)
@@ -180,14 +206,14 @@ void attention_prefill(PrefillArgs a) {
     const int wave_first_limit = a.position + max(row0, 0) / a.group;
 
     const KV *kh = static_cast<const KV *>(a.k_pages) + (size_t)h * a.head_stride;
-    const KV *vh = static_cast<const KV *>(a.v_pages) + (size_t)h * a.head_stride;
+    const VT *vh = static_cast<const VT *>(a.v_pages) + (size_t)h * a.v_head_stride;
     // Loader wave w copies 1 KiB chunks w*H .. w*H+H-1 of page p into the
     // ring's buffer p % 4.  Over a run the pages are requested in the order
     // K0 V0 K1 V1 K2 V2 ..., which the waits below count on.
-    auto stage = [&](const KV *src, int p, KV *ring) __attribute__((always_inline)) {
+    auto stage = [&](const auto *src, int p, auto *ring) __attribute__((always_inline)) {
         if (w >= kLoaders) return;
-        const KV *page = src + (size_t)p * PAGE + w * H * 512;       // uniform
-        KV *buf = ring + (p & 3) * PAGE + w * H * 512;
+        const auto *page = src + (size_t)p * PAGE + w * H * 512;       // uniform
+        auto *buf = ring + (p & 3) * PAGE + w * H * 512;
 #pragma unroll
         for (int c = 0; c < H; ++c)
             __builtin_amdgcn_global_load_lds(reinterpret_cast<const void *>(page + c * 512 + lane * 8),
@@ -283,9 +309,9 @@ void attention_prefill(PrefillArgs a) {
         uint32_t ph[4], pl[4] = {};
 #pragma unroll
         for (int j = 0; j < 4; j += 2) {
-            ph[j / 2] = pack2(e[j], e[j + 1], KV{});
+            ph[j / 2] = pack2(e[j], e[j + 1], PT{});
             if constexpr (PSPLIT) {
-                pl[j / 2] = pack2(e[j] - unpack_lo(ph[j / 2], KV{}), e[j + 1] - unpack_hi(ph[j / 2], KV{}), KV{});
+                pl[j / 2] = pack2(e[j] - unpack_lo(ph[j / 2], PT{}), e[j + 1] - unpack_hi(ph[j / 2], PT{}), PT{});
             }
         }
         pin(ph[0], ph[1]);
@@ -293,9 +319,9 @@ void attention_prefill(PrefillArgs a) {
         qk_chunk(std::integral_constant<int, 5>{}, kb, sn);
 #pragma unroll
         for (int j = 4; j < 8; j += 2) {
-            ph[j / 2] = pack2(e[j], e[j + 1], KV{});
+            ph[j / 2] = pack2(e[j], e[j + 1], PT{});
             if constexpr (PSPLIT) {
-                pl[j / 2] = pack2(e[j] - unpack_lo(ph[j / 2], KV{}), e[j + 1] - unpack_hi(ph[j / 2], KV{}), KV{});
+                pl[j / 2] = pack2(e[j] - unpack_lo(ph[j / 2], PT{}), e[j + 1] - unpack_hi(ph[j / 2], PT{}), PT{});
             }
         }
         pin(ph[2], ph[3]);
@@ -305,13 +331,13 @@ void attention_prefill(PrefillArgs a) {
         pin(l);
         qk_chunk(std::integral_constant<int, 7>{}, kb, sn);
         static_for<8, KS>([&](auto ks) { qk_chunk(ks, kb, sn); });
-        const V8 p_hi = __builtin_bit_cast(V8, U4{ph[0], ph[1], ph[2], ph[3]});
-        const V8 p_lo = __builtin_bit_cast(V8, U4{pl[0], pl[1], pl[2], pl[3]});
+        const PV8 p_hi = __builtin_bit_cast(PV8, U4{ph[0], ph[1], ph[2], ph[3]});
+        const PV8 p_lo = __builtin_bit_cast(PV8, U4{pl[0], pl[1], pl[2], pl[3]});
 
         // ---- O^T += V^T P^T for page i ----
         // V fragments stream through a window of VW reads.
         constexpr int VW = 4;
-        V8 vf[DT];
+        PV8 vf[DT];
         auto read_v = [&](auto dt_) __attribute__((always_inline)) {
             constexpr int dt = decltype(dt_)::value;
             if constexpr (dt < DT) lds_read<dt * 1024>(vf[dt], vb);
@@ -322,9 +348,6 @@ void attention_prefill(PrefillArgs a) {
 #pragma unroll
             for (int dt = 0; dt < DT; ++dt) acc[dt] *= alpha;
         }
-        // Last page: V slots past the last key are zeroed (stale pages may
-        // hold anything, and 0 * NaN is NaN).
-        const bool tail = i * 32 + 32 > n_keys;
         // Pairs of tiles: the hi and lo products of a tile accumulate into
         // the same registers, so they are issued two apart.
         __builtin_amdgcn_s_setprio(0);
@@ -334,15 +357,6 @@ void attention_prefill(PrefillArgs a) {
             lds_wait<later>(vf[dt], vf[dt + 1]);
             read_v(std::integral_constant<int, dt + VW>{});
             read_v(std::integral_constant<int, dt + VW + 1>{});
-            if (tail) {
-                keep_branch();
-#pragma unroll
-                for (int j = 0; j < 8; ++j)
-                    if (i * 32 + v_slot_token(g, j) >= n_keys) {
-                        vf[dt][j] = (KV)0.f;
-                        vf[dt + 1][j] = (KV)0.f;
-                    }
-            }
             acc[dt] = mfma(vf[dt], p_hi, acc[dt]);
             acc[dt + 1] = mfma(vf[dt + 1], p_hi, acc[dt + 1]);
             if constexpr (PSPLIT) {
@@ -375,9 +389,30 @@ void attention_prefill(PrefillArgs a) {
     // whose rows see those pages.  Every wave takes part in every barrier.
     // Meeting once per page instead, with three pages in flight, took 2.5%
     // longer on a 2048-token chunk (458.6 against 447.6 us).
+    // At a meeting, on the workgroup's last page, each loader wave zeroes
+    // the V slots past its last key in its own chunks once they have landed
+    // (stale slots may hold anything, and a masked key's P of 0 times NaN is
+    // NaN).  Chunk c of a page is dims 16c .. 16c+15 of all 32 keys; lane l
+    // holds dim l%16, key group g = (l/16)%4 (keys 4g + j and 16 + 4g + j - 4).
+    const int tail_page = n_keys % 32 ? n_keys / 32 : -1;
+    auto prepare_v = [&](int p) __attribute__((always_inline)) {
+        if (w >= kLoaders || p != tail_page) return;
+#pragma unroll
+        for (int c = 0; c < H; ++c) {
+            U4 *slot = reinterpret_cast<U4 *>(vring + (p & 3) * PAGE + (w * H + c) * 512) + lane;
+            U4 v = *slot;
+#pragma unroll
+            for (int j = 0; j < 8; ++j)
+                if (p * 32 + v_slot_token(g, j) >= n_keys) v[j >> 1] &= (j & 1) ? 0x0000ffffu : 0xffff0000u;
+            *slot = v;
+        }
+        asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+    };
     for (int i = 0; i < n; ++i) {
         if ((i & 1) == 0) {
             wait_vmcnt<0>();
+            prepare_v(i);
+            prepare_v(i + 1);
             ring_barrier();
             if (i + 3 < n) stage(kh, i + 3, kring);
             if (i + 4 < n) stage(kh, i + 4, kring);
@@ -419,39 +454,119 @@ void attention_prefill(PrefillArgs a) {
 // 128 rows (eight waves, two per SIMD).
 constexpr int kPrefillRows = 192, kPreciseRows = 128;
 
+// The raw instances: fp16 pages; bf16 K with V converted to fp16 by the
+// pass below; `exact`: bf16 K and V with P as bf16 hi + lo parts (the heads
+// the pass flagged).
 template <int D>
-const void *prefill_kernel(Dtype dtype, bool out_f32) {
+const void *prefill_kernel(Dtype dtype, bool out_f32, bool exact) {
     constexpr int R = kPrefillRows;
+    if (dtype == Dtype::BF16 && exact)
+        return out_f32 ? (const void *)&attention_prefill<D, __bf16, __bf16, true, false, kOutF32, R>
+                       : (const void *)&attention_prefill<D, __bf16, __bf16, true, false, kOutSame, R>;
     if (dtype == Dtype::BF16)
-        return out_f32 ? (const void *)&attention_prefill<D, __bf16, true, false, kOutF32, R>
-                       : (const void *)&attention_prefill<D, __bf16, true, false, kOutSame, R>;
-    return out_f32 ? (const void *)&attention_prefill<D, _Float16, false, false, kOutF32, R>
-                   : (const void *)&attention_prefill<D, _Float16, false, false, kOutSame, R>;
+        return out_f32 ? (const void *)&attention_prefill<D, __bf16, _Float16, false, false, kOutF32, R>
+                       : (const void *)&attention_prefill<D, __bf16, _Float16, false, false, kOutSame, R>;
+    return out_f32 ? (const void *)&attention_prefill<D, _Float16, _Float16, false, false, kOutF32, R>
+                   : (const void *)&attention_prefill<D, _Float16, _Float16, false, false, kOutSame, R>;
 }
 
 // The fused model path: fp16 pages, fp32 query as hi + lo parts, hi + lo P
 // (the same precision as the split kernels' precise instance).
 template <int D>
 const void *precise_prefill_kernel(bool gated) {
-    return gated ? (const void *)&attention_prefill<D, _Float16, true, true, kOutGated, kPreciseRows>
-                 : (const void *)&attention_prefill<D, _Float16, true, true, kOutF32, kPreciseRows>;
+    return gated ? (const void *)&attention_prefill<D, _Float16, _Float16, true, true, kOutGated, kPreciseRows>
+                 : (const void *)&attention_prefill<D, _Float16, _Float16, true, true, kOutF32, kPreciseRows>;
+}
+
+int prefill_workgroups(const Shape &s, bool precise) {
+    const int rows = precise ? kPreciseRows : kPrefillRows;
+    return (s.group() * s.tokens + rows - 1) / rows * s.kv_heads;
+}
+
+// ---- V conversion pass (bf16 calls) ----
+// The call's V pages (keys 0 .. position+tokens-1) of every KV head as fp16
+// pages in the workspace, [kv_heads][pages][32*D], the slots past the last
+// key zeroed.  Block b of a head converts pages kConvPages*b .. +kConvPages-1
+// and writes one word: 1 if some 16-byte operand slot (8 keys of one dim) is
+// neither all zero nor has its largest magnitude in [2^-14, 65280] (a value
+// the conversion cannot hold, or whose slot would lose precision).  Loads
+// are non-temporal (each bf16 page is read once); the fp16 copy keeps the
+// default policy, the prefill kernel reads it next.
+constexpr int kConvPages = 8, kConvThreads = 256;
+
+template <int D>
+__global__ __launch_bounds__(kConvThreads)
+void convert_v_pages(const __bf16 *v_pages, size_t head_stride, _Float16 *out, uint32_t *flags, int pages,
+                     int n_keys, int blocks_per_head) {
+    typedef uint32_t U4 __attribute__((ext_vector_type(4)));
+    constexpr int PAGE = 32 * D, SLOTS = PAGE / 8;   // 16-byte slots per page
+    const int h = blockIdx.x / blocks_per_head, b = blockIdx.x - h * blocks_per_head;
+    const int p0 = b * kConvPages, p1 = min(p0 + kConvPages, pages);
+    const U4 *src = reinterpret_cast<const U4 *>(v_pages + (size_t)h * head_stride);
+    U4 *dst = reinterpret_cast<U4 *>(out + (size_t)h * pages * PAGE);
+    bool ok = true;
+    for (int e = p0 * SLOTS + threadIdx.x; e < p1 * SLOTS; e += kConvThreads) {
+        U4 v = __builtin_nontemporal_load(src + e);
+        const int p = e / SLOTS, g = (e >> 4) & 3;   // slot e: lane e % 64 of its 1 KiB chunk
+        if (p * 32 + 32 > n_keys) {
+#pragma unroll
+            for (int j = 0; j < 8; ++j)
+                if (p * 32 + v_slot_token(g, j) >= n_keys) v[j >> 1] &= (j & 1) ? 0x0000ffffu : 0xffff0000u;
+        }
+        uint32_t mx = 0;
+#pragma unroll
+        for (int k = 0; k < 4; ++k) {
+            const uint32_t m = v[k] & 0x7fff7fffu;
+            mx = max(mx, max(m & 0xffffu, m >> 16));
+        }
+        ok = ok && (mx == 0 || (mx >= 0x3880u && mx <= 0x477fu));
+#pragma unroll
+        for (int k = 0; k < 4; ++k)
+            v[k] = pack2(__uint_as_float(v[k] << 16), __uint_as_float(v[k] & 0xffff0000u), _Float16{});
+        dst[e] = v;
+    }
+    const int bad = __syncthreads_or(!ok);
+    if (threadIdx.x == 0) flags[blockIdx.x] = bad ? 1u : 0u;
+}
+
+struct ConvPlan {
+    int pages, blocks_per_head;
+    size_t copy_bytes, flag_offset, bytes;
+};
+
+ConvPlan conv_plan(const Shape &s) {
+    ConvPlan c;
+    c.pages = (s.n_keys() + 31) / 32;
+    c.blocks_per_head = (c.pages + kConvPages - 1) / kConvPages;
+    c.copy_bytes = (size_t)s.kv_heads * c.pages * 32 * s.head_dim * 2;
+    c.flag_offset = (c.copy_bytes + 255) / 256 * 256;
+    c.bytes = c.flag_offset + ((size_t)s.kv_heads * c.blocks_per_head * 4 + 255) / 256 * 256;
+    return c;
 }
 
 }  // namespace
 
+size_t prefill_workspace_bytes(const Shape &s, Dtype dtype, bool precise) {
+    if (dtype != Dtype::BF16 || precise) return 0;
+    return conv_plan(s).bytes;
+}
+
 void launch_prefill(const Shape &s, Dtype dtype, bool precise, float scale, const void *q,
                     const void *q_lo, const void *k_pages, const void *v_pages, void *out, bool out_f32,
-                    const float *gate, hipStream_t stream) {
+                    const float *gate, void *workspace, hipStream_t stream) {
     require(!gate || precise, "a gated prefill needs the precise query");
     require(!precise || (dtype == Dtype::F16 && out_f32 && q_lo), "a precise prefill runs on fp16 pages with fp32 output");
-    PrefillArgs a;
+    require(prefill_workspace_bytes(s, dtype, precise) == 0 || workspace != nullptr,
+            "a bf16 prefill needs its workspace");
+    require(s.head_dim == 256 || s.head_dim == 128, "unsupported head_dim for the prefill kernel");
+    PrefillArgs a = {};
     a.q = q;
     a.q_lo = q_lo;
     a.gate = gate;
     a.k_pages = k_pages;
     a.v_pages = v_pages;
     a.out = out;
-    a.head_stride = (size_t)s.capacity * s.head_dim;
+    a.head_stride = a.v_head_stride = (size_t)s.capacity * s.head_dim;
     a.q_heads = s.q_heads;
     a.kv_heads = s.kv_heads;
     a.group = s.group();
@@ -460,16 +575,46 @@ void launch_prefill(const Shape &s, Dtype dtype, bool precise, float scale, cons
     const int rows = precise ? kPreciseRows : kPrefillRows;
     a.n_tiles = (a.rows + rows - 1) / rows;
     a.scale_log2 = scale * 1.4426950408889634f;
-    const void *kernel = precise ? (s.head_dim == 256   ? precise_prefill_kernel<256>(gate != nullptr)
-                                    : s.head_dim == 128 ? precise_prefill_kernel<128>(gate != nullptr)
-                                                        : nullptr)
-                       : s.head_dim == 256 ? prefill_kernel<256>(dtype, out_f32)
-                       : s.head_dim == 128 ? prefill_kernel<128>(dtype, out_f32) : nullptr;
-    require(kernel != nullptr, "unsupported head_dim for the prefill kernel");
-    void *args[] = {&a};
+    const bool d256 = s.head_dim == 256;
     const int threads = (rows / 16) * kWave;
-    require((long long)a.n_tiles * s.kv_heads * threads < (1LL << 32), "prefill launch exceeds 2^32 work-items");
-    check(hipLaunchKernel(kernel, dim3(a.n_tiles * s.kv_heads), dim3(threads), args, 0, stream));
+    const int grid = prefill_workgroups(s, precise);
+    require((long long)grid * threads < (1LL << 32), "prefill launch exceeds 2^32 work-items");
+    void *args[] = {&a};
+    if (precise) {
+        const void *kernel = d256 ? precise_prefill_kernel<256>(gate != nullptr) : precise_prefill_kernel<128>(gate != nullptr);
+        check(hipLaunchKernel(kernel, dim3(grid), dim3(threads), args, 0, stream));
+        return;
+    }
+    if (dtype == Dtype::F16) {
+        const void *kernel = d256 ? prefill_kernel<256>(dtype, out_f32, false) : prefill_kernel<128>(dtype, out_f32, false);
+        check(hipLaunchKernel(kernel, dim3(grid), dim3(threads), args, 0, stream));
+        return;
+    }
+    // bf16: V pages to fp16 (with the range words), the prefill on them for
+    // the unflagged KV heads, then the exact instance for the flagged ones.
+    const ConvPlan c = conv_plan(s);
+    _Float16 *copy = static_cast<_Float16 *>(workspace);
+    uint32_t *flags = reinterpret_cast<uint32_t *>(static_cast<char *>(workspace) + c.flag_offset);
+    const int conv_blocks = c.blocks_per_head * s.kv_heads;
+    if (d256)
+        convert_v_pages<256><<<conv_blocks, kConvThreads, 0, stream>>>(static_cast<const __bf16 *>(v_pages), a.head_stride,
+                                                                      copy, flags, c.pages, s.n_keys(), c.blocks_per_head);
+    else
+        convert_v_pages<128><<<conv_blocks, kConvThreads, 0, stream>>>(static_cast<const __bf16 *>(v_pages), a.head_stride,
+                                                                      copy, flags, c.pages, s.n_keys(), c.blocks_per_head);
+    check(hipGetLastError());
+    a.v_flags = flags;
+    a.flag_words = c.blocks_per_head;
+    a.run_flagged = 0;
+    a.v_pages = copy;
+    a.v_head_stride = (size_t)c.pages * 32 * s.head_dim;
+    const void *kernel = d256 ? prefill_kernel<256>(dtype, out_f32, false) : prefill_kernel<128>(dtype, out_f32, false);
+    check(hipLaunchKernel(kernel, dim3(grid), dim3(threads), args, 0, stream));
+    a.run_flagged = 1;
+    a.v_pages = v_pages;
+    a.v_head_stride = a.head_stride;
+    kernel = d256 ? prefill_kernel<256>(dtype, out_f32, true) : prefill_kernel<128>(dtype, out_f32, true);
+    check(hipLaunchKernel(kernel, dim3(grid), dim3(threads), args, 0, stream));
 }
 
 }  // namespace rs

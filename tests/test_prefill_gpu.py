@@ -1,0 +1,107 @@
+"""GPU parity of the chunked prefill on bf16 caches, whose V pages a
+streaming pass converts to fp16 in the workspace (exact for bf16 values in
+[2^-14, 65280]) before the prefill kernel multiplies them by an fp16 P.
+
+The pass flags a KV head with a V value outside that range, and the exact
+instance (bf16 V, P as bf16 hi + lo parts) computes that head's rows
+instead.  These tests put such values in the cache (far above the fp16
+range, a whole KV head below it, one dead head dimension) and hold the
+fp32 output to the oracle's bounds, and check on ordinary data that the
+pass flags nothing (the converted products are the ones that ran).
+"""
+import numpy as np
+import pytest
+
+from oracle import attention_ref as ref
+from redshift_amd import attention as A
+from redshift_amd.workloads import Workload, f32_to_bf16_bits, make_inputs, to_float
+
+pytestmark = pytest.mark.gpu
+
+MAX_ABS, REL_L2 = 2e-3, 1e-3
+
+
+def bf16_bits(x):
+    return f32_to_bf16_bits(np.ascontiguousarray(x, np.float32))
+
+
+def run(w, q, k, v, torch, ws=None):
+    """fp32 output of qv_attention on a bf16 cache whose slots past the last
+    key hold NaN; q, k, v are bf16 bits."""
+    def t(x):
+        return torch.from_numpy(np.ascontiguousarray(x).view(np.int16)).view(torch.bfloat16).cuda()
+    cache = A.PagedKV(w.kv_heads, w.head_dim, A.round_capacity(w.keys), torch.bfloat16)
+    cache.k.fill_(float('nan'))
+    cache.v.fill_(float('nan'))
+    cache.pack(t(k), t(v))
+    if ws is None:
+        ws = A.workspace(A.attention_workspace_bytes(w.q_heads, w.kv_heads, w.head_dim, w.tokens, w.position))
+    out = A.attention(t(q), cache, w.position, w.scale, ws=ws, out_dtype=torch.float32)
+    torch.cuda.synchronize()
+    return out.cpu().numpy().astype(np.float64)
+
+
+def check(got, want, scale=1.0):
+    """Both bounds, relative to the output's own magnitude `scale`."""
+    assert np.all(np.isfinite(got))
+    err = np.abs(got - want).max()
+    rel = np.linalg.norm(got - want) / np.linalg.norm(want)
+    assert err <= MAX_ABS * scale and rel <= REL_L2, (err, rel)
+
+
+def inputs(T, position, q_heads=24, kv_heads=4, head_dim=256, seed=0):
+    w = Workload('prefill_bf16', q_heads, kv_heads, head_dim, T, position, 1 / 16, 'bf16', seed, 1.0, 1.0)
+    q, k, v, _ = make_inputs(w)
+    return w, to_float(q, 'bf16'), to_float(k, 'bf16'), to_float(v, 'bf16')
+
+
+def test_ordinary_values_take_the_converted_products(gpu):
+    """N(0,1) bf16 values all lie in the fp16 range: every word of the
+    conversion pass stays 0 (no head takes the exact instance), and the
+    result meets both bounds."""
+    w, q, k, v = inputs(600, 900, seed=11)
+    ws = A.workspace(A.attention_workspace_bytes(w.q_heads, w.kv_heads, w.head_dim, w.tokens, w.position))
+    ws.fill_(0xAB)
+    got = run(w, bf16_bits(q), bf16_bits(k), bf16_bits(v), gpu, ws=ws)
+    check(got, ref.gqa_attention(q, k, v, w.position, w.scale))
+    # The workspace holds the fp16 copy of the V pages, then (256-byte
+    # aligned) one word per conversion block of 8 pages, per KV head.
+    pages = -(-w.keys // 32)
+    offset = -(-(w.kv_heads * pages * 32 * w.head_dim * 2) // 256) * 256
+    blocks = w.kv_heads * -(-pages // 8)
+    words = ws[offset:offset + 4 * blocks].cpu().numpy().view(np.uint32)
+    assert np.all(words == 0), words
+
+
+@pytest.mark.parametrize('case', ['huge_page', 'tiny_head', 'dead_dim', 'huge_page_d128'])
+def test_values_outside_the_fp16_range(gpu, case):
+    """V values the fp16 conversion cannot hold: the KV heads that have
+    them take the exact bf16 products."""
+    if case == 'huge_page_d128':
+        w, q, k, v = inputs(300, 500, q_heads=16, kv_heads=2, head_dim=128, seed=12)
+    else:
+        w, q, k, v = inputs(400, 700, seed=13)
+    scale = 1.0
+    if case.startswith('huge_page'):
+        # Keys 640..671 (one page) of KV head 1 far above 65504, and one
+        # key of head 0 just above it.
+        v[640:672, 1 % w.kv_heads] *= 2.0 ** 20
+        v[100, 0, 7] = 70000.0
+        scale = 2.0 ** 20
+    elif case == 'tiny_head':
+        # Every value of KV head 2 below 2^-14 (an fp16 subnormal would keep
+        # a few bits of each); head 3 normal.
+        v[:, 2] *= 2.0 ** -20
+    else:
+        # One head dimension of every key close to zero (2^-30 scale), the
+        # others normal: every page has a lane below 2^-14.
+        v[:, :, 37] *= 2.0 ** -30
+    q16, k16, v16 = bf16_bits(q), bf16_bits(k), bf16_bits(v)
+    q, k, v = to_float(q16, 'bf16'), to_float(k16, 'bf16'), to_float(v16, 'bf16')
+    want = ref.gqa_attention(q, k, v, w.position, w.scale)
+    got = run(w, q16, k16, v16, gpu)
+    check(got, want, scale)
+    if case == 'tiny_head':
+        # The tiny head's rows on their own scale, too.
+        heads = slice(2 * w.q_heads // w.kv_heads, 3 * w.q_heads // w.kv_heads)
+        check(got[:, heads], want[:, heads], 2.0 ** -20)

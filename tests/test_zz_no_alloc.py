@@ -1,9 +1,9 @@
-"""qv_attention_noalloc (no workspace argument, split-K partials in the
+"""qv_attention_noalloc (no workspace argument, its workspace in the
 library's static device array) against qv_attention with its own
 workspace: the same kernels and plan, so the same bits.  Two calls in a row
 share the array, the second with a smaller input; a call with more rows
-than the split kernels take (the prefill kernel, no partials) and a bf16
-one follow."""
+than the split kernels take (the prefill kernel, no workspace), a bf16 one,
+and a bf16 prefill (its fp16 copy of the V pages in the array) follow."""
 import numpy as np
 import pytest
 
@@ -22,7 +22,8 @@ def test_noalloc_equals_workspace_entry(gpu, order):
     if order == 'small_then_large':
         shapes = shapes[::-1]
     shapes += [Workload('prefill', 24, 4, 256, 50, 700, 1 / 16, 'f16', 33, 1.0, 0.5),
-               Workload('bf16', 16, 2, 128, 3, 5000, 1 / 128 ** .5, 'bf16', 34, 1.0, 0.5)]
+               Workload('bf16', 16, 2, 128, 3, 5000, 1 / 128 ** .5, 'bf16', 34, 1.0, 0.5),
+               Workload('bf16_prefill', 24, 4, 256, 100, 2000, 1 / 16, 'bf16', 35, 1.0, 0.5)]
     prepared = []
     for w in shapes:
         q, k, v, _ = make_inputs(w)
