@@ -34,8 +34,8 @@
 // like fp16, where P split into bf16 hi + lo parts would take two.  A KV
 // head with a V value outside that range (larger, tiny but nonzero in all
 // eight keys that one operand slot holds, or not finite) is flagged by the
-// pass; the fp16 instance skips it and the exact instance (bf16 V, P as
-// bf16 hi + lo) runs it instead, returning at once for the other heads.
+// pass, and the workgroups of that head take the exact products instead
+// (bf16 V, P as bf16 hi + lo parts; attention_prefill_bf16).
 //
 // Scheduling: workgroup i serves KV head i % kv_heads (with 4 KV heads the
 // round-robin dispatch over the 8 XCDs keeps every head on the same two XCDs,
@@ -100,13 +100,14 @@ struct PrefillArgs {
     const void *k_pages;
     const void *v_pages;
     void *out;
-    // bf16 calls: the conversion pass's words, flag_words per KV head (a set
-    // word: a V value outside the fp16 range); run_flagged selects the heads
-    // this launch serves (0: the unflagged ones, 1: the flagged ones).
+    // bf16 calls: the fp16 copy of the V pages (packed to the call's pages,
+    // v_copy_stride elements per KV head) and the conversion pass's words,
+    // flag_words per KV head (a set word: a V value outside the fp16 range).
+    const void *v_copy;
+    size_t v_copy_stride;
     const uint32_t *v_flags;
-    int flag_words, run_flagged;
-    size_t head_stride;       // K (and q-side) pages
-    size_t v_head_stride;     // V pages (the converted copy is packed to the call's pages)
+    int flag_words;
+    size_t head_stride;       // K and V pages
     int q_heads, kv_heads, group, rows, position, n_tiles;
     float scale_log2;
 };
@@ -121,22 +122,17 @@ __device__ __forceinline__ int v_slot_token(int g, int j) {
 // bf16 pages).  QSPLIT: the query is an fp32 one given as hi + lo fp16
 // parts, both multiplied by K.  MODE: output of the KV type, fp32, or fp32
 // times sigmoid(gate) (see combine.hpp).
+// The rows of one workgroup; kring and vring are the kernel's two rings of
+// four pages, V pages read from v_pages with v_head_stride elements per KV
+// head.
 template <int D, typename KV, typename VT, bool PSPLIT, bool QSPLIT, int MODE, int ROWS>
-__global__ __launch_bounds__(ROWS / 16 * kWave, 1)
-void attention_prefill(PrefillArgs a) {
+__device__ __forceinline__ void prefill_rows(const PrefillArgs &a, KV *kring, VT *vring, const void *v_pages,
+                                             size_t v_head_stride) {
     using V8 = typename Vec8<KV>::type;
     using OUT = std::conditional_t<MODE == kOutSame, KV, float>;
     typedef uint32_t U4 __attribute__((ext_vector_type(4)));
     using PT = VT;
     using PV8 = typename Vec8<PT>::type;
-    if (a.v_flags) {
-        // This launch serves either the KV heads whose V the conversion pass
-        // flagged or the others; every wave reads the same words.
-        const uint32_t *f = a.v_flags + (size_t)(blockIdx.x % a.kv_heads) * a.flag_words;
-        uint32_t any = 0;
-        for (int i = threadIdx.x & 63; i < a.flag_words; i += 64) any |= f[i];
-        if ((__any(any != 0) != 0) != (a.run_flagged != 0)) return;
-    }
     constexpr int kPWaves = ROWS / 16;
     constexpr int KS = D / 32, DT = D / 16;
     constexpr int PAGE = 32 * D;                       // elements of one K (or V) page
@@ -146,8 +142,6 @@ void attention_prefill(PrefillArgs a) {
     constexpr int kLoaders = kPWaves == 12 ? 8 : kPWaves / 2;
     constexpr int H = PAGE_BYTES / 1024 / kLoaders;
     static_assert(H >= 1 && PAGE_BYTES / 1024 % kLoaders == 0, "loads divide over the loader waves");
-    __shared__ __attribute__((aligned(16))) KV kring[4 * PAGE];
-    __shared__ __attribute__((aligned(16))) VT vring[4 * PAGE];
 
     const int lane = threadIdx.x & 63, g = lane >> 4;
     const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);   // wave index (uniform)
@@ -206,7 +200,7 @@ void attention_prefill(PrefillArgs a) {
     const int wave_first_limit = a.position + max(row0, 0) / a.group;
 
     const KV *kh = static_cast<const KV *>(a.k_pages) + (size_t)h * a.head_stride;
-    const VT *vh = static_cast<const VT *>(a.v_pages) + (size_t)h * a.v_head_stride;
+    const VT *vh = static_cast<const VT *>(v_pages) + (size_t)h * v_head_stride;
     // Loader wave w copies 1 KiB chunks w*H .. w*H+H-1 of page p into the
     // ring's buffer p % 4.  Over a run the pages are requested in the order
     // K0 V0 K1 V1 K2 V2 ..., which the waits below count on.
@@ -448,24 +442,48 @@ void attention_prefill(PrefillArgs a) {
     }
 }
 
+template <int D, typename KV, typename VT, bool PSPLIT, bool QSPLIT, int MODE, int ROWS>
+__global__ __launch_bounds__(ROWS / 16 * kWave, 1)
+void attention_prefill(PrefillArgs a) {
+    __shared__ __attribute__((aligned(16))) KV kring[4 * 32 * D];
+    __shared__ __attribute__((aligned(16))) VT vring[4 * 32 * D];
+    prefill_rows<D, KV, VT, PSPLIT, QSPLIT, MODE, ROWS>(a, kring, vring, a.v_pages, a.head_stride);
+}
+
+// bf16 pages: the workgroups of a KV head that the conversion pass did not
+// flag multiply by the fp16 copy of V with one fp16 P; a flagged head's take
+// the exact products (bf16 V, P as bf16 hi + lo parts).  Every wave reads
+// the same words, so the choice is uniform.
+template <int D, int MODE, int ROWS>
+__global__ __launch_bounds__(ROWS / 16 * kWave, 1)
+void attention_prefill_bf16(PrefillArgs a) {
+    __shared__ __attribute__((aligned(16))) __bf16 kring[4 * 32 * D];
+    __shared__ __attribute__((aligned(16))) uint16_t vring[4 * 32 * D];
+    const uint32_t *f = a.v_flags + (size_t)(blockIdx.x % a.kv_heads) * a.flag_words;
+    uint32_t any = 0;
+    for (int i = threadIdx.x & 63; i < a.flag_words; i += 64) any |= f[i];
+    if (__any(any != 0))
+        prefill_rows<D, __bf16, __bf16, true, false, MODE, ROWS>(a, kring, reinterpret_cast<__bf16 *>(vring),
+                                                                 a.v_pages, a.head_stride);
+    else
+        prefill_rows<D, __bf16, _Float16, false, false, MODE, ROWS>(a, kring, reinterpret_cast<_Float16 *>(vring),
+                                                                    a.v_copy, a.v_copy_stride);
+}
+
 // Rows per workgroup: 192 (twelve waves, three per SIMD; 2048 tokens of six
 // query heads per KV head make 64 workgroups per KV head, one round on 256
 // CUs).  A precise query (hi + lo parts) needs twice the query registers:
 // 128 rows (eight waves, two per SIMD).
 constexpr int kPrefillRows = 192, kPreciseRows = 128;
 
-// The raw instances: fp16 pages; bf16 K with V converted to fp16 by the
-// pass below; `exact`: bf16 K and V with P as bf16 hi + lo parts (the heads
-// the pass flagged).
+// The raw instances: fp16 pages; bf16 pages, V through the conversion pass
+// below (attention_prefill_bf16).
 template <int D>
-const void *prefill_kernel(Dtype dtype, bool out_f32, bool exact) {
+const void *prefill_kernel(Dtype dtype, bool out_f32) {
     constexpr int R = kPrefillRows;
-    if (dtype == Dtype::BF16 && exact)
-        return out_f32 ? (const void *)&attention_prefill<D, __bf16, __bf16, true, false, kOutF32, R>
-                       : (const void *)&attention_prefill<D, __bf16, __bf16, true, false, kOutSame, R>;
     if (dtype == Dtype::BF16)
-        return out_f32 ? (const void *)&attention_prefill<D, __bf16, _Float16, false, false, kOutF32, R>
-                       : (const void *)&attention_prefill<D, __bf16, _Float16, false, false, kOutSame, R>;
+        return out_f32 ? (const void *)&attention_prefill_bf16<D, kOutF32, R>
+                       : (const void *)&attention_prefill_bf16<D, kOutSame, R>;
     return out_f32 ? (const void *)&attention_prefill<D, _Float16, _Float16, false, false, kOutF32, R>
                    : (const void *)&attention_prefill<D, _Float16, _Float16, false, false, kOutSame, R>;
 }
@@ -486,61 +504,66 @@ int prefill_workgroups(const Shape &s, bool precise) {
 // ---- V conversion pass (bf16 calls) ----
 // The call's V pages (keys 0 .. position+tokens-1) of every KV head as fp16
 // pages in the workspace, [kv_heads][pages][32*D], the slots past the last
-// key zeroed.  Block b of a head converts pages kConvPages*b .. +kConvPages-1
-// and writes one word: 1 if some 16-byte operand slot (8 keys of one dim) is
-// neither all zero nor has its largest magnitude in [2^-14, 65280] (a value
-// the conversion cannot hold, or whose slot would lose precision).  Loads
-// are non-temporal (each bf16 page is read once); the fp16 copy keeps the
-// default policy, the prefill kernel reads it next.
-constexpr int kConvPages = 8, kConvThreads = 256;
+// key zeroed.  Block (head, page) converts one page, every thread its 16-byte
+// slots (all loads issued first), and writes one word: 1 if some slot (8
+// keys of one dim, an operand's lane) is neither all zero nor has its
+// largest magnitude in [2^-14, 65280] (a value the conversion cannot hold,
+// or whose slot would lose precision).  Loads are non-temporal (each bf16
+// page is read once); the fp16 copy keeps the default policy, the prefill
+// kernel reads it next.
+constexpr int kConvThreads = 256;
 
 template <int D>
 __global__ __launch_bounds__(kConvThreads)
 void convert_v_pages(const __bf16 *v_pages, size_t head_stride, _Float16 *out, uint32_t *flags, int pages,
-                     int n_keys, int blocks_per_head) {
+                     int n_keys) {
     typedef uint32_t U4 __attribute__((ext_vector_type(4)));
     constexpr int PAGE = 32 * D, SLOTS = PAGE / 8;   // 16-byte slots per page
-    const int h = blockIdx.x / blocks_per_head, b = blockIdx.x - h * blocks_per_head;
-    const int p0 = b * kConvPages, p1 = min(p0 + kConvPages, pages);
-    const U4 *src = reinterpret_cast<const U4 *>(v_pages + (size_t)h * head_stride);
-    U4 *dst = reinterpret_cast<U4 *>(out + (size_t)h * pages * PAGE);
+    constexpr int PER = SLOTS / kConvThreads;
+    static_assert(PER * kConvThreads == SLOTS, "slots divide over the threads");
+    const int h = blockIdx.x / pages, p = blockIdx.x - h * pages;
+    const U4 *src = reinterpret_cast<const U4 *>(v_pages + (size_t)h * head_stride + (size_t)p * PAGE);
+    U4 *dst = reinterpret_cast<U4 *>(out + ((size_t)h * pages + p) * PAGE);
+    U4 v[PER];
+#pragma unroll
+    for (int i = 0; i < PER; ++i) v[i] = __builtin_nontemporal_load(src + threadIdx.x + i * kConvThreads);
     bool ok = true;
-    for (int e = p0 * SLOTS + threadIdx.x; e < p1 * SLOTS; e += kConvThreads) {
-        U4 v = __builtin_nontemporal_load(src + e);
-        const int p = e / SLOTS, g = (e >> 4) & 3;   // slot e: lane e % 64 of its 1 KiB chunk
+#pragma unroll
+    for (int i = 0; i < PER; ++i) {
+        const int e = threadIdx.x + i * kConvThreads, g = (e >> 4) & 3;   // slot e: lane e % 64 of its 1 KiB chunk
         if (p * 32 + 32 > n_keys) {
 #pragma unroll
             for (int j = 0; j < 8; ++j)
-                if (p * 32 + v_slot_token(g, j) >= n_keys) v[j >> 1] &= (j & 1) ? 0x0000ffffu : 0xffff0000u;
+                if (p * 32 + v_slot_token(g, j) >= n_keys) v[i][j >> 1] &= (j & 1) ? 0x0000ffffu : 0xffff0000u;
         }
         uint32_t mx = 0;
 #pragma unroll
         for (int k = 0; k < 4; ++k) {
-            const uint32_t m = v[k] & 0x7fff7fffu;
+            const uint32_t m = v[i][k] & 0x7fff7fffu;
             mx = max(mx, max(m & 0xffffu, m >> 16));
         }
         ok = ok && (mx == 0 || (mx >= 0x3880u && mx <= 0x477fu));
 #pragma unroll
         for (int k = 0; k < 4; ++k)
-            v[k] = pack2(__uint_as_float(v[k] << 16), __uint_as_float(v[k] & 0xffff0000u), _Float16{});
-        dst[e] = v;
+            v[i][k] = pack2(__uint_as_float(v[i][k] << 16), __uint_as_float(v[i][k] & 0xffff0000u), _Float16{});
+        dst[e] = v[i];
     }
     const int bad = __syncthreads_or(!ok);
     if (threadIdx.x == 0) flags[blockIdx.x] = bad ? 1u : 0u;
 }
 
+// Workspace of a bf16 call: the fp16 copy, then one word per page.
 struct ConvPlan {
-    int pages, blocks_per_head;
-    size_t copy_bytes, flag_offset, bytes;
+    int pages;
+    size_t flag_offset, bytes;
 };
 
 ConvPlan conv_plan(const Shape &s) {
     ConvPlan c;
     c.pages = (s.n_keys() + 31) / 32;
-    c.blocks_per_head = (c.pages + kConvPages - 1) / kConvPages;
-    c.copy_bytes = (size_t)s.kv_heads * c.pages * 32 * s.head_dim * 2;
-    c.flag_offset = (c.copy_bytes + 255) / 256 * 256;
-    c.bytes = c.flag_offset + ((size_t)s.kv_heads * c.blocks_per_head * 4 + 255) / 256 * 256;
+    const size_t copy = (size_t)s.kv_heads * c.pages * 32 * s.head_dim * 2;
+    c.flag_offset = (copy + 255) / 256 * 256;
+    c.bytes = c.flag_offset + ((size_t)s.kv_heads * c.pages * 4 + 255) / 256 * 256;
     return c;
 }
 
@@ -566,7 +589,7 @@ void launch_prefill(const Shape &s, Dtype dtype, bool precise, float scale, cons
     a.k_pages = k_pages;
     a.v_pages = v_pages;
     a.out = out;
-    a.head_stride = a.v_head_stride = (size_t)s.capacity * s.head_dim;
+    a.head_stride = (size_t)s.capacity * s.head_dim;
     a.q_heads = s.q_heads;
     a.kv_heads = s.kv_heads;
     a.group = s.group();
@@ -585,35 +608,26 @@ void launch_prefill(const Shape &s, Dtype dtype, bool precise, float scale, cons
         check(hipLaunchKernel(kernel, dim3(grid), dim3(threads), args, 0, stream));
         return;
     }
-    if (dtype == Dtype::F16) {
-        const void *kernel = d256 ? prefill_kernel<256>(dtype, out_f32, false) : prefill_kernel<128>(dtype, out_f32, false);
-        check(hipLaunchKernel(kernel, dim3(grid), dim3(threads), args, 0, stream));
-        return;
+    if (dtype == Dtype::BF16) {
+        // V pages to fp16 with their range words, then the prefill (which
+        // takes the exact products on a flagged KV head).
+        const ConvPlan c = conv_plan(s);
+        _Float16 *copy = static_cast<_Float16 *>(workspace);
+        uint32_t *flags = reinterpret_cast<uint32_t *>(static_cast<char *>(workspace) + c.flag_offset);
+        const int conv_blocks = c.pages * s.kv_heads;
+        if (d256)
+            convert_v_pages<256><<<conv_blocks, kConvThreads, 0, stream>>>(
+                static_cast<const __bf16 *>(v_pages), a.head_stride, copy, flags, c.pages, s.n_keys());
+        else
+            convert_v_pages<128><<<conv_blocks, kConvThreads, 0, stream>>>(
+                static_cast<const __bf16 *>(v_pages), a.head_stride, copy, flags, c.pages, s.n_keys());
+        check(hipGetLastError());
+        a.v_copy = copy;
+        a.v_copy_stride = (size_t)c.pages * 32 * s.head_dim;
+        a.v_flags = flags;
+        a.flag_words = c.pages;
     }
-    // bf16: V pages to fp16 (with the range words), the prefill on them for
-    // the unflagged KV heads, then the exact instance for the flagged ones.
-    const ConvPlan c = conv_plan(s);
-    _Float16 *copy = static_cast<_Float16 *>(workspace);
-    uint32_t *flags = reinterpret_cast<uint32_t *>(static_cast<char *>(workspace) + c.flag_offset);
-    const int conv_blocks = c.blocks_per_head * s.kv_heads;
-    if (d256)
-        convert_v_pages<256><<<conv_blocks, kConvThreads, 0, stream>>>(static_cast<const __bf16 *>(v_pages), a.head_stride,
-                                                                      copy, flags, c.pages, s.n_keys(), c.blocks_per_head);
-    else
-        convert_v_pages<128><<<conv_blocks, kConvThreads, 0, stream>>>(static_cast<const __bf16 *>(v_pages), a.head_stride,
-                                                                      copy, flags, c.pages, s.n_keys(), c.blocks_per_head);
-    check(hipGetLastError());
-    a.v_flags = flags;
-    a.flag_words = c.blocks_per_head;
-    a.run_flagged = 0;
-    a.v_pages = copy;
-    a.v_head_stride = (size_t)c.pages * 32 * s.head_dim;
-    const void *kernel = d256 ? prefill_kernel<256>(dtype, out_f32, false) : prefill_kernel<128>(dtype, out_f32, false);
-    check(hipLaunchKernel(kernel, dim3(grid), dim3(threads), args, 0, stream));
-    a.run_flagged = 1;
-    a.v_pages = v_pages;
-    a.v_head_stride = a.head_stride;
-    kernel = d256 ? prefill_kernel<256>(dtype, out_f32, true) : prefill_kernel<128>(dtype, out_f32, true);
+    const void *kernel = d256 ? prefill_kernel<256>(dtype, out_f32) : prefill_kernel<128>(dtype, out_f32);
     check(hipLaunchKernel(kernel, dim3(grid), dim3(threads), args, 0, stream));
 }
 

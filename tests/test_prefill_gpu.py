@@ -65,10 +65,10 @@ def test_ordinary_values_take_the_converted_products(gpu):
     got = run(w, bf16_bits(q), bf16_bits(k), bf16_bits(v), gpu, ws=ws)
     check(got, ref.gqa_attention(q, k, v, w.position, w.scale))
     # The workspace holds the fp16 copy of the V pages, then (256-byte
-    # aligned) one word per conversion block of 8 pages, per KV head.
+    # aligned) one word per page, per KV head.
     pages = -(-w.keys // 32)
     offset = -(-(w.kv_heads * pages * 32 * w.head_dim * 2) // 256) * 256
-    blocks = w.kv_heads * -(-pages // 8)
+    blocks = w.kv_heads * pages
     words = ws[offset:offset + 4 * blocks].cpu().numpy().view(np.uint32)
     assert np.all(words == 0), words
 
