@@ -105,3 +105,38 @@ def test_values_outside_the_fp16_range(gpu, case):
         # The tiny head's rows on their own scale, too.
         heads = slice(2 * w.q_heads // w.kv_heads, 3 * w.q_heads // w.kv_heads)
         check(got[:, heads], want[:, heads], 2.0 ** -20)
+
+
+def random_prefill_shapes(n, seed=4096):
+    """Seeded prefill shapes: KV heads 1-8, groups 1-8, head_dim 128/256,
+    fp16/bf16, more than 48 query rows per KV head (the prefill kernel),
+    up to 1,400 of them (several workgroups per KV head), positions 0-4000
+    (tail pages of every fill), with and without outlier keys."""
+    rng = np.random.default_rng(seed)
+    shapes = []
+    for i in range(n):
+        kv = int(rng.choice([1, 2, 4, 8]))
+        group = int(rng.integers(1, 9))
+        tokens = int(rng.integers(49 // group + 1, 1400 // group + 1))
+        shapes.append((kv * group, kv, int(rng.choice([128, 256])), tokens, int(rng.integers(0, 4001)),
+                       str(rng.choice(['f16', 'bf16'])), int(rng.choice([0, 16])), 1700 + i))
+    return shapes
+
+
+@pytest.mark.parametrize('q_heads,kv_heads,head_dim,T,position,dtype,outliers,seed', random_prefill_shapes(12))
+def test_random_prefill_shapes(gpu, q_heads, kv_heads, head_dim, T, position, dtype, outliers, seed):
+    """The prefill path on seeded random shapes, cache slots past the last
+    key NaN: the float32 output to both bounds, the 16-bit output within
+    the max-abs bound plus its own rounding (half an ulp)."""
+    from tests.test_attention_gpu import gpu_attention
+    outliers = min(outliers, position + T)
+    w = Workload('random_prefill', q_heads, kv_heads, head_dim, T, position, 1 / head_dim ** .5, dtype, seed,
+                 1.0, 0.5, outliers, 8.0)
+    assert T * (q_heads // kv_heads) > 48
+    q, k, v, _ = make_inputs(w)
+    want = ref.gqa_attention(to_float(q, dtype), to_float(k, dtype), to_float(v, dtype), position, w.scale)
+    got32 = gpu_attention(w, q, k, v, gpu, fill_nan=True, out_dtype=gpu.float32)
+    check(got32, want)
+    got16 = gpu_attention(w, q, k, v, gpu, fill_nan=True)
+    half_ulp = np.abs(want) * (2.0 ** -8 if dtype == 'bf16' else 2.0 ** -11)
+    assert np.all(np.abs(got16 - want) <= MAX_ABS + half_ulp)
