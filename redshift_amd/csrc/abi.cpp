@@ -122,8 +122,9 @@ void run_attention(const rs::Shape &s, rs::Dtype dtype, bool precise, float scal
                    void *workspace, void *out, bool out_f32, const float *gate,
                    hipStream_t stream) {
     if (s.group() * s.tokens > rs::kMaxRows) {
-        // Long token runs (chunked prefill): one launch (two for bf16 pages,
-        // whose workspace holds one word per workgroup).
+        // Long token runs (chunked prefill): the prefill kernel, after a V
+        // conversion pass for bf16 pages and before a combine when the call
+        // splits its keys (the workspace holds the V copy and the partials).
         rs::launch_prefill(s, dtype, precise, scale, q, q_lo, k_pages, v_pages, out, out_f32, gate, workspace,
                            stream);
         return;

@@ -155,10 +155,13 @@ void launch_fused_short(const FusedToken &tok, float *out, hipStream_t stream);
 // Chunked prefill: all group*tokens query rows against the pages; `dtype` q
 // and out, [tokens][q_heads][D].  A precise call (fp16 pages) takes the query
 // as hi + lo fp16 parts and writes fp32, times sigmoid of the gate half of
-// q_gate [tokens][q_heads][2D] when `gate` is given.  A bf16 call runs two
-// launches (V converted to fp16, then an exact redo of the workgroups that
-// met a V value outside the fp16 range) and keeps one word per workgroup in
-// the workspace (prefill_workspace_bytes; 0 for the other calls).
+// q_gate [tokens][q_heads][2D] when `gate` is given.  A raw bf16 call first
+// converts the call's V pages to fp16 in the workspace, with one range word
+// per page (the prefill kernel takes the exact bf16 products on a KV head
+// whose V leaves the fp16 range).  A call with too few row workgroups to fill
+// the device splits their pages over more workgroups, whose fp32 partial
+// rows (in the workspace, after the V copy) the combine kernel merges.
+// prefill_workspace_bytes: the workspace of a call (0 when it needs none).
 size_t prefill_workspace_bytes(const Shape &s, Dtype dtype, bool precise);
 void launch_prefill(const Shape &s, Dtype dtype, bool precise, float scale, const void *q,
                     const void *q_lo, const void *k_pages, const void *v_pages, void *out, bool out_f32,

@@ -110,6 +110,15 @@ struct PrefillArgs {
     size_t head_stride;       // K and V pages
     int q_heads, kv_heads, group, rows, position, n_tiles;
     float scale_log2;
+    // Key splits (a call whose row workgroups alone would leave CUs idle):
+    // workgroup (split, j, h) takes pages split*split_pages ..
+    // +split_pages-1 of those its rows see, and stores fp32 partials for the
+    // combine kernel: its rows unnormalised ([kv_heads][splits][rows][D]),
+    // their max (base 2) and sum ([kv_heads][splits][2][rows]).  One split:
+    // split_pages covers every page and the rows are stored normalised.
+    float *part_o;
+    float *part_ml;
+    int splits, split_pages;
 };
 
 __device__ __forceinline__ int v_slot_token(int g, int j) {
@@ -159,7 +168,8 @@ __device__ __forceinline__ void prefill_rows(const PrefillArgs &a, KV *kring, VT
     // same work.  Negative tiles are padding, and rows from R on are not
     // stored.  Workgroup j's last row lies in its round-0 tile of slot 4j.
     const int R = a.rows;
-    const int j = blockIdx.x / a.kv_heads;
+    const int rest = blockIdx.x / a.kv_heads;
+    const int j = rest % a.n_tiles, split = rest / a.n_tiles;
     static_assert(kPWaves % 4 == 0 && kPWaves / 4 <= 3, "one to three rounds of four waves");
     const int T = (R + 15) / 16, K = 4 * a.n_tiles, slot = 4 * j + (w & 3), round = w >> 2;
     const int tile = round == 0 ? T - 1 - slot : round == 1 ? T - 2 * K + slot : T - 3 * K + slot;
@@ -192,22 +202,28 @@ __device__ __forceinline__ void prefill_rows(const PrefillArgs &a, KV *kring, VT
     // the last valid row of tile T-1-4j).
     const int n_keys = a.position + (min(16 * (T - 4 * j), R) - 1) / a.group + 1;
     const int n = (n_keys + 31) / 32;
+    // This split's pages: p0 + i for i = 0 .. nl-1 (local index i, ring
+    // buffer i % 4).  nl is uniform over the workgroup; nl = 0 leaves empty
+    // partials (no keys: sum 0, rows 0).
+    const int p0 = split * a.split_pages;
+    const int nl = max(0, min(n, p0 + a.split_pages) - p0);
     // Pages of this wave: those its last valid row sees (none without one).
     const int wave_last = min(row0 + 15, row_end - 1);
     const int n_wave = wave_last >= max(row0, 0) ? (a.position + wave_last / a.group + 1 + 31) / 32 : 0;
+    const int nw = min(max(n_wave - p0, 0), nl);
     // Pages from which on some row of this wave masks keys (every row sees
     // the keys up to position + its first row's token).
     const int wave_first_limit = a.position + max(row0, 0) / a.group;
 
     const KV *kh = static_cast<const KV *>(a.k_pages) + (size_t)h * a.head_stride;
     const VT *vh = static_cast<const VT *>(v_pages) + (size_t)h * v_head_stride;
-    // Loader wave w copies 1 KiB chunks w*H .. w*H+H-1 of page p into the
-    // ring's buffer p % 4.  Over a run the pages are requested in the order
-    // K0 V0 K1 V1 K2 V2 ..., which the waits below count on.
-    auto stage = [&](const auto *src, int p, auto *ring) __attribute__((always_inline)) {
+    // Loader wave w copies 1 KiB chunks w*H .. w*H+H-1 of page p0 + i into
+    // the ring's buffer i % 4.  Over a run the pages are requested in the
+    // order K0 V0 K1 V1 K2 V2 ..., which the waits below count on.
+    auto stage = [&](const auto *src, int i, auto *ring) __attribute__((always_inline)) {
         if (w >= kLoaders) return;
-        const auto *page = src + (size_t)p * PAGE + w * H * 512;       // uniform
-        auto *buf = ring + (p & 3) * PAGE + w * H * 512;
+        const auto *page = src + (size_t)(p0 + i) * PAGE + w * H * 512;       // uniform
+        auto *buf = ring + (i & 3) * PAGE + w * H * 512;
 #pragma unroll
         for (int c = 0; c < H; ++c)
             __builtin_amdgcn_global_load_lds(reinterpret_cast<const void *>(page + c * 512 + lane * 8),
@@ -219,6 +235,10 @@ __device__ __forceinline__ void prefill_rows(const PrefillArgs &a, KV *kring, VT
     f32x4 acc[DT];
 #pragma unroll
     for (int dt = 0; dt < DT; ++dt) acc[dt] = f32x4{0.f, 0.f, 0.f, 0.f};
+    // m stays -inf for a row that sees no key of its pages (a split past its
+    // last key).  Its exponents are then NaN, which stays in that row's own
+    // lanes and accumulators (every cross-lane step combines the four lanes
+    // of one row); its partial is stored as empty instead.
     float m = -INFINITY, l = 0.f;
     f32x4 s[2];            // scores of the page whose softmax comes next
 
@@ -264,15 +284,16 @@ __device__ __forceinline__ void prefill_rows(const PrefillArgs &a, KV *kring, VT
         __builtin_amdgcn_s_setprio(1);
         read_k(std::integral_constant<int, 0>{}, kb);
         read_k(std::integral_constant<int, 1>{}, kb);
-        // Scores of page i; keys past a row's limit are masked.
+        // Scores of page p0 + i; keys past a row's limit are masked.
+        const int key0 = (p0 + i) * 32;
         float x[8];
 #pragma unroll
         for (int j = 0; j < 8; ++j) x[j] = s[j >> 2][j & 3] * a.scale_log2;
-        if (i * 32 + 31 > wave_first_limit) {
+        if (key0 + 31 > wave_first_limit) {
             keep_branch();
 #pragma unroll
             for (int j = 0; j < 8; ++j)
-                if (i * 32 + 16 * (j >> 2) + 4 * g + (j & 3) > limit) x[j] = -INFINITY;
+                if (key0 + 16 * (j >> 2) + 4 * g + (j & 3) > limit) x[j] = -INFINITY;
         }
         float mx = __builtin_fmaxf(max3(x[0], x[1], x[2]), max3(x[3], x[4], x[5]));
         mx = max3(mx, x[6], x[7]);
@@ -282,7 +303,8 @@ __device__ __forceinline__ void prefill_rows(const PrefillArgs &a, KV *kring, VT
         mx = row_group_max(mx);
         pin(mx);
         qk_chunk(std::integral_constant<int, 1>{}, kb, sn);
-        // Every row sees key 0, so the max is finite from the first page on.
+        // A row that sees a key of this split sees its first one on the
+        // split's first page, where its max becomes finite.
         const float bm = mx;
         float alpha = 1.f;
         const bool moved = bm > m + kLazy;
@@ -363,18 +385,20 @@ __device__ __forceinline__ void prefill_rows(const PrefillArgs &a, KV *kring, VT
     };
 
     // ---- prologue: K0 V0 K1 V1 K2 requested, S^T of page 0 ----
-    stage(kh, 0, kring);
-    stage(vh, 0, vring);
-    if (n > 1) { stage(kh, 1, kring); stage(vh, 1, vring); }
-    if (n > 2) stage(kh, 2, kring);
-    if (n > 2) wait_vmcnt<4 * H>();
-    else if (n > 1) wait_vmcnt<3 * H>();
-    else wait_vmcnt<H>();
-    ring_barrier();
     s[0] = s[1] = f32x4{0.f, 0.f, 0.f, 0.f};
-    read_k(std::integral_constant<int, 0>{}, kring_lane);
-    read_k(std::integral_constant<int, 1>{}, kring_lane);
-    static_for<0, KS>([&](auto ks) { qk_chunk(ks, kring_lane, s); });
+    if (nl > 0) {
+        stage(kh, 0, kring);
+        stage(vh, 0, vring);
+        if (nl > 1) { stage(kh, 1, kring); stage(vh, 1, vring); }
+        if (nl > 2) stage(kh, 2, kring);
+        if (nl > 2) wait_vmcnt<4 * H>();
+        else if (nl > 1) wait_vmcnt<3 * H>();
+        else wait_vmcnt<H>();
+        ring_barrier();
+        read_k(std::integral_constant<int, 0>{}, kring_lane);
+        read_k(std::integral_constant<int, 1>{}, kring_lane);
+        static_for<0, KS>([&](auto ks) { qk_chunk(ks, kring_lane, s); });
+    }
 
     // The waves meet every second step (i even): K(i+1), K(i+2), V(i) and
     // V(i+1) have landed (every request), the waves meet (K(i-1), K(i),
@@ -389,11 +413,12 @@ __device__ __forceinline__ void prefill_rows(const PrefillArgs &a, KV *kring, VT
     // NaN).  Chunk c of a page is dims 16c .. 16c+15 of all 32 keys; lane l
     // holds dim l%16, key group g = (l/16)%4 (keys 4g + j and 16 + 4g + j - 4).
     const int tail_page = n_keys % 32 ? n_keys / 32 : -1;
-    auto prepare_v = [&](int p) __attribute__((always_inline)) {
-        if (w >= kLoaders || p != tail_page) return;
+    auto prepare_v = [&](int i) __attribute__((always_inline)) {
+        const int p = p0 + i;
+        if (w >= kLoaders || i >= nl || p != tail_page) return;
 #pragma unroll
         for (int c = 0; c < H; ++c) {
-            U4 *slot = reinterpret_cast<U4 *>(vring + (p & 3) * PAGE + (w * H + c) * 512) + lane;
+            U4 *slot = reinterpret_cast<U4 *>(vring + (i & 3) * PAGE + (w * H + c) * 512) + lane;
             U4 v = *slot;
 #pragma unroll
             for (int j = 0; j < 8; ++j)
@@ -402,23 +427,39 @@ __device__ __forceinline__ void prefill_rows(const PrefillArgs &a, KV *kring, VT
         }
         asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
     };
-    for (int i = 0; i < n; ++i) {
+    for (int i = 0; i < nl; ++i) {
         if ((i & 1) == 0) {
             wait_vmcnt<0>();
             prepare_v(i);
             prepare_v(i + 1);
             ring_barrier();
-            if (i + 3 < n) stage(kh, i + 3, kring);
-            if (i + 4 < n) stage(kh, i + 4, kring);
-            if (i + 2 < n) stage(vh, i + 2, vring);
-            if (i + 3 < n) stage(vh, i + 3, vring);
+            if (i + 3 < nl) stage(kh, i + 3, kring);
+            if (i + 4 < nl) stage(kh, i + 4, kring);
+            if (i + 2 < nl) stage(vh, i + 2, vring);
+            if (i + 3 < nl) stage(vh, i + 3, vring);
         }
-        if (i < n_wave) step(i);
+        if (i < nw) step(i);
     }
 
-    // ---- normalise and store rows ----
     l = row_group_sum(l);
     const int row = row0 + (lane & 15);
+    if (a.splits > 1) {
+        // ---- partial rows: unnormalised, with their max and sum ----
+        if (row >= 0 && row < row_end) {
+            const size_t part = (size_t)h * a.splits + split;
+            const bool none = m == -INFINITY;   // no key of this split: empty
+            float *po = a.part_o + (part * R + row) * D + 4 * g;
+#pragma unroll
+            for (int dt = 0; dt < DT; ++dt)
+                *reinterpret_cast<f32x4 *>(po + dt * 16) = none ? f32x4{0.f, 0.f, 0.f, 0.f} : acc[dt];
+            if (g == 0) {
+                a.part_ml[part * 2 * R + row] = m;
+                a.part_ml[part * 2 * R + R + row] = none ? 0.f : l;
+            }
+        }
+        return;
+    }
+    // ---- normalise and store rows ----
     if (row >= 0 && row < row_end) {
         const int t = row / a.group, gg = row - t * a.group;
         OUT *dst = static_cast<OUT *>(a.out) + ((size_t)t * a.q_heads + (size_t)h * a.group + gg) * D + 4 * g;
@@ -496,10 +537,6 @@ const void *precise_prefill_kernel(bool gated) {
                  : (const void *)&attention_prefill<D, _Float16, _Float16, true, true, kOutF32, kPreciseRows>;
 }
 
-int prefill_workgroups(const Shape &s, bool precise) {
-    const int rows = precise ? kPreciseRows : kPrefillRows;
-    return (s.group() * s.tokens + rows - 1) / rows * s.kv_heads;
-}
 
 // ---- V conversion pass (bf16 calls) ----
 // The call's V pages (keys 0 .. position+tokens-1) of every KV head as fp16
@@ -567,11 +604,46 @@ ConvPlan conv_plan(const Shape &s) {
     return c;
 }
 
+// Key splits.  A prefill workgroup fills a CU (its LDS rings), so a call with
+// fewer row workgroups (rows / 192, or / 128, times kv_heads) than the device
+// has CUs leaves the rest idle: a 64-token chunk on a 16K prefix runs in 12
+// workgroups.  Such a call splits every workgroup's pages over up to
+// CUs / row workgroups workgroups of at least kMinSplitPages pages each
+// (a workgroup's fixed costs, its query load and first page loads, take a
+// few microseconds; a page about 1.5), and the combine kernel merges the
+// partial rows.
+constexpr int kMinSplitPages = 8;
+
+struct PrefillPlan {
+    int rows;          // query rows per workgroup
+    int row_wgs;       // workgroups of rows per KV head
+    int pages;         // pages of keys 0 .. n_keys-1
+    int splits, split_pages;
+    size_t part_offset;  // partials in the workspace (after a bf16 call's V copy)
+    size_t bytes;        // workspace
+};
+
+PrefillPlan plan_prefill(const Shape &s, Dtype dtype, bool precise) {
+    PrefillPlan p;
+    p.rows = precise ? kPreciseRows : kPrefillRows;
+    const int R = s.group() * s.tokens;
+    p.row_wgs = (R + p.rows - 1) / p.rows;
+    p.pages = (s.n_keys() + 31) / 32;
+    const int base = p.row_wgs * s.kv_heads;
+    p.splits = std::max(1, std::min(device_cu_count() / base, p.pages / kMinSplitPages));
+    p.split_pages = (p.pages + p.splits - 1) / p.splits;
+    p.splits = (p.pages + p.split_pages - 1) / p.split_pages;
+    p.part_offset = dtype == Dtype::BF16 && !precise ? conv_plan(s).bytes : 0;
+    p.bytes = p.part_offset;
+    if (p.splits > 1)
+        p.bytes += ((size_t)s.kv_heads * p.splits * R * (s.head_dim + 2) * sizeof(float) + 255) / 256 * 256;
+    return p;
+}
+
 }  // namespace
 
 size_t prefill_workspace_bytes(const Shape &s, Dtype dtype, bool precise) {
-    if (dtype != Dtype::BF16 || precise) return 0;
-    return conv_plan(s).bytes;
+    return plan_prefill(s, dtype, precise).bytes;
 }
 
 void launch_prefill(const Shape &s, Dtype dtype, bool precise, float scale, const void *q,
@@ -579,9 +651,9 @@ void launch_prefill(const Shape &s, Dtype dtype, bool precise, float scale, cons
                     const float *gate, void *workspace, hipStream_t stream) {
     require(!gate || precise, "a gated prefill needs the precise query");
     require(!precise || (dtype == Dtype::F16 && out_f32 && q_lo), "a precise prefill runs on fp16 pages with fp32 output");
-    require(prefill_workspace_bytes(s, dtype, precise) == 0 || workspace != nullptr,
-            "a bf16 prefill needs its workspace");
     require(s.head_dim == 256 || s.head_dim == 128, "unsupported head_dim for the prefill kernel");
+    const PrefillPlan plan = plan_prefill(s, dtype, precise);
+    require(plan.bytes == 0 || workspace != nullptr, "this prefill needs its workspace");
     PrefillArgs a = {};
     a.q = q;
     a.q_lo = q_lo;
@@ -595,17 +667,33 @@ void launch_prefill(const Shape &s, Dtype dtype, bool precise, float scale, cons
     a.group = s.group();
     a.rows = s.group() * s.tokens;
     a.position = s.position;
-    const int rows = precise ? kPreciseRows : kPrefillRows;
-    a.n_tiles = (a.rows + rows - 1) / rows;
+    a.n_tiles = plan.row_wgs;
     a.scale_log2 = scale * 1.4426950408889634f;
+    a.splits = plan.splits;
+    a.split_pages = plan.split_pages;
+    if (plan.splits > 1) {
+        a.part_o = reinterpret_cast<float *>(static_cast<char *>(workspace) + plan.part_offset);
+        a.part_ml = a.part_o + (size_t)s.kv_heads * plan.splits * a.rows * s.head_dim;
+    }
     const bool d256 = s.head_dim == 256;
-    const int threads = (rows / 16) * kWave;
-    const int grid = prefill_workgroups(s, precise);
-    require((long long)grid * threads < (1LL << 32), "prefill launch exceeds 2^32 work-items");
+    const int threads = (plan.rows / 16) * kWave;
+    const long long grid = (long long)plan.row_wgs * s.kv_heads * plan.splits;
+    require(grid * threads < (1LL << 32), "prefill launch exceeds 2^32 work-items");
     void *args[] = {&a};
+    // The combine of split calls (fp32 partial rows, stored with the default
+    // policy).
+    auto combine = [&] {
+        if (plan.splits == 1) return;
+        SplitPlan cp = {};
+        cp.kind = SplitKind::Stream;
+        cp.rows = a.rows;
+        cp.splits = plan.splits;
+        launch_combine(s, cp, dtype, a.part_o, out, out_f32, gate, stream);
+    };
     if (precise) {
         const void *kernel = d256 ? precise_prefill_kernel<256>(gate != nullptr) : precise_prefill_kernel<128>(gate != nullptr);
-        check(hipLaunchKernel(kernel, dim3(grid), dim3(threads), args, 0, stream));
+        check(hipLaunchKernel(kernel, dim3((unsigned)grid), dim3(threads), args, 0, stream));
+        combine();
         return;
     }
     if (dtype == Dtype::BF16) {
@@ -628,7 +716,8 @@ void launch_prefill(const Shape &s, Dtype dtype, bool precise, float scale, cons
         a.flag_words = c.pages;
     }
     const void *kernel = d256 ? prefill_kernel<256>(dtype, out_f32) : prefill_kernel<128>(dtype, out_f32);
-    check(hipLaunchKernel(kernel, dim3(grid), dim3(threads), args, 0, stream));
+    check(hipLaunchKernel(kernel, dim3((unsigned)grid), dim3(threads), args, 0, stream));
+    combine();
 }
 
 }  // namespace rs

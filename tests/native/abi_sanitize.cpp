@@ -365,7 +365,7 @@ void device_calls(hipStream_t stream) {
         HIP_OK(hipStreamSynchronize(stream));
         EXPECT(all_finite(fetch(dout.p, n, c.out_dtype)));
         // qv_attention_workspace covers both page types; an fp16 prefill
-        // (more than 48 rows per KV head) needs none of it.
+        // (more than 48 rows per KV head) needs less of it (no V copy).
         const bool f16_prefill = c.dtype == QV_F16 && c.tokens * (H / HKV) > 48;
         if (ws_bytes > 0 && !f16_prefill) {
             EXPECT(failed_with(qv_attention(dout.p, dq.p, kp.p, vp.p, c.dtype, c.out_dtype, H, HKV, D, c.tokens,

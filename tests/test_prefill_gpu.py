@@ -140,3 +140,28 @@ def test_random_prefill_shapes(gpu, q_heads, kv_heads, head_dim, T, position, dt
     got16 = gpu_attention(w, q, k, v, gpu, fill_nan=True)
     half_ulp = np.abs(want) * (2.0 ** -8 if dtype == 'bf16' else 2.0 ** -11)
     assert np.all(np.abs(got16 - want) <= MAX_ABS + half_ulp)
+
+
+@pytest.mark.parametrize('q_heads,kv_heads,head_dim,T,position,dtype', [
+    (24, 4, 256, 16, 16000, 'f16'),    # 4 row workgroups: 62 key splits of about 8 pages
+    (24, 4, 256, 64, 16000, 'bf16'),   # 8 row workgroups: 32 splits, V through the fp16 copy
+    (16, 2, 128, 40, 9000, 'bf16'),
+    (24, 4, 256, 300, 300, 'f16'),     # 2 splits; the first rows see no key of the second
+    (8, 1, 256, 500, 0, 'f16'),        # from an empty cache: early workgroups' later splits empty
+])
+def test_split_prefill_against_oracle(gpu, q_heads, kv_heads, head_dim, T, position, dtype):
+    """Calls with too few row workgroups to fill the device split their keys
+    over more workgroups and combine the partial rows: every row against the
+    oracle, cache slots past the last key NaN; the float32 output to both
+    bounds, the 16-bit output within the max-abs bound plus half an ulp."""
+    from tests.test_attention_gpu import gpu_attention
+    w = Workload('split_prefill', q_heads, kv_heads, head_dim, T, position, 1 / head_dim ** .5, dtype, 40 + T,
+                 1.0, 0.5, min(16, position + T), 8.0)
+    q, k, v, _ = make_inputs(w)
+    want = ref.gqa_attention(to_float(q, dtype), to_float(k, dtype), to_float(v, dtype), position, w.scale)
+    got32 = gpu_attention(w, q, k, v, gpu, fill_nan=True, out_dtype=gpu.float32)
+    check(got32, want)
+    got16 = gpu_attention(w, q, k, v, gpu, fill_nan=True)
+    half_ulp = np.abs(want) * (2.0 ** -8 if dtype == 'bf16' else 2.0 ** -11)
+    assert np.all(np.abs(got16 - want) <= MAX_ABS + half_ulp)
+
