@@ -68,9 +68,10 @@ def time_workload(torch, A, w, layers, steps, warmup, seed):
     """Times `steps` steps of `layers` attention calls.
 
     Returns dict(ms_per_step: one step replayed as a captured HIP graph,
-    eager_ms_per_step: the same launches issued one by one, split_us: average
+    eager_ms_per_step: the same launches issued one by one, split_us: median
     duration of the split-K (or prefill) kernel from events recorded around
-    each of its launches in the eager loop, on the stream it runs on)."""
+    each of its launches in the eager loop, on the stream it runs on, and
+    split_us_mean: their mean)."""
     caches, queries = make_layers(torch, A, w, layers, seed)
     ws = A.workspace(A.attention_workspace_bytes(w.q_heads, w.kv_heads, w.head_dim, w.tokens, w.position))
     outs = [torch.empty_like(q) for q in queries]
@@ -144,7 +145,8 @@ def time_workload(torch, A, w, layers, steps, warmup, seed):
     del caches
     torch.cuda.empty_cache()
     return dict(ms_per_step=graph_ms, eager_ms_per_step=eager_ms,
-                split_us=1000.0 * sum(split_ms) / len(split_ms), split_graph_us=split_graph_us)
+                split_us=1000.0 * float(np.median(split_ms)), split_us_mean=1000.0 * sum(split_ms) / len(split_ms),
+                split_graph_us=split_graph_us)
 
 
 def measured_traffic():
@@ -365,8 +367,8 @@ def main():
     ap.add_argument('--no-cpu', action='store_true', help='skip the CPU baseline')
     ap.add_argument('--no-extra', action='store_true', help='skip the secondary workloads')
     ap.add_argument('--extras', default='verify8_16k,decode_16k,decode_4k,prefill_2k,fused_verify8_16k,fused_decode_139k,'
-                                        'fused_prefill_2k,fused_verify8_prefix16,fused_verify8_prefix128,'
-                                        'kv_checkpoint_139k',
+                                        'fused_prefill_2k,fused_prefill64_16k,fused_verify8_prefix16,'
+                                        'fused_verify8_prefix128,kv_checkpoint_139k',
                     help='comma-separated secondary workloads to run')
     ap.add_argument('--drop-in', action='store_true',
                     help='only time the host-buffer qv_test_attention (PCIe-inclusive) and exit')
@@ -412,11 +414,13 @@ def main():
         'us_per_layer': round(1000 * r['ms_per_step'] / args.layers, 2),
         'eager_us_per_layer': round(1000 * r['eager_ms_per_step'] / args.layers, 2),
         'timing': 'step = 16 layers x (split-K kernel + combine kernel) replayed as one HIP graph; '
-                  'roofline kernel_us = split-K kernel alone, HIP events in an eager loop',
+                  'roofline kernel_us = split-K kernel alone, median of HIP-event-timed launches in an '
+                  'eager loop (kernel_us_mean: their mean)',
         'roofline': {'bound': 'hbm', 'kernel': 'attention_stream (decode split-K)',
                      'achieved': round(split_gbs, 1), 'peak': HBM_PEAK_GBS, 'unit': 'GB/s',
                      'frac': round(split_gbs / HBM_PEAK_GBS, 4), 'traffic': measured_traffic(),
-                     'kernel_us': round(r['split_us'], 2), 'bytes_per_launch': w.kv_bytes(),
+                     'kernel_us': round(r['split_us'], 2), 'kernel_us_mean': round(r['split_us_mean'], 2),
+                     'bytes_per_launch': w.kv_bytes(),
                      'frac_step': round(gbs / HBM_PEAK_GBS, 4),
                      'frac_is': 'frac: the split-K kernel alone (kernel_us); frac_step: the whole layer, '
                                 'split-K + combine kernels in the graph step (us_per_layer)'},
@@ -443,10 +447,14 @@ def main():
         if 'prefill_2k' in chosen:
             wp = WORKLOADS['prefill_2k']
             log('prefill_2k: 4 layers')
-            rp = time_workload(torch, A, wp, 4, max(3, args.steps // 4), 2, seed=2)
+            # At least 52 timed calls at the default 50 steps (13 steps of 4 layers).
+            rp = time_workload(torch, A, wp, 4, max(3, (args.steps + 3) // 4), 2, seed=2)
             kernel_s = rp['split_us'] * 1e-6
             extra['prefill_2k'] = {'us_per_layer': round(1000 * rp['ms_per_step'] / 4, 1),
                                    'kernel_us': round(rp['split_us'], 1),
+                                   'kernel_us_mean': round(rp['split_us_mean'], 1),
+                                   'kernel_is': 'conversion pass + prefill kernel of one eager call, median '
+                                                'of the HIP-event-timed calls',
                                    'TFLOP/s': round(wp.flops() / kernel_s / 1e12, 1),
                                    'frac_mfma_peak': round(wp.flops() / kernel_s / MFMA_BF16_PEAK, 4),
                                    'flops_per_layer': wp.flops()}
@@ -475,6 +483,22 @@ def main():
                                          'frac_mfma_peak': round(wq.flops() / (us * 1e-6) / MFMA_BF16_PEAK, 4),
                                          'what': 'qv_attention_fused on a 2048-token chunk at 6144: prepare + '
                                                  'append + precise prefill (fp32 q as fp16 hi + lo, hi + lo P) + gate'}
+        if 'fused_prefill64_16k' in chosen:
+            # A short prefill chunk on a long prefix (64 tokens at 16,384): six
+            # query heads per KV head make 384 rows, three workgroups of 128
+            # per KV head, so the call splits its keys over the device's CUs
+            # and combines the partial rows (with the gate).
+            wc = Workload('fused_prefill64_16k', 24, 4, 256, 64, 16384, 1 / 16, 'f16', 9, kv_std=0.5)
+            log(f'fused_prefill64_16k: {args.layers} layers')
+            us = 1000 * time_fused(torch, A, wc, args.layers, args.steps, args.warmup, seed=10) / args.layers
+            extra['fused_prefill64_16k'] = {
+                'us_per_layer': round(us, 2),
+                'TFLOP/s': round(wc.flops() / (us * 1e-6) / 1e12, 1),
+                'frac_mfma_peak': round(wc.flops() / (us * 1e-6) / MFMA_BF16_PEAK, 4),
+                'GB/s': round(wc.kv_bytes() / (us * 1e-6) / 1e9, 1),
+                'frac_hbm': round(wc.kv_bytes() / (us * 1e-6) / 1e9 / HBM_PEAK_GBS, 4),
+                'what': 'qv_attention_fused on a 64-token chunk at 16,384: prepare + append + precise prefill '
+                        'with its keys split over the CUs + gated combine, graph step'}
         for prefix in (16, 128):
             name = f'fused_verify8_prefix{prefix}'
             if name not in chosen:
