@@ -460,17 +460,19 @@ def test_short_context_direct_output_equals_combined(gpu, q_heads, kv_heads, hea
     assert np.abs(direct - combined).max() <= tolerance
 
 
-@pytest.mark.parametrize('T,position', [(1, 50000), (8, 2000), (8, 100)])
-def test_graph_replay_matches_eager(gpu, T, position):
+@pytest.mark.parametrize('T,position,dtype', [(1, 50000, 'f16'), (8, 2000, 'f16'), (8, 100, 'f16'),
+                                              (16, 16000, 'f16'),    # prefill, keys split + combine
+                                              (64, 9000, 'bf16')])   # V conversion, split prefill, combine
+def test_graph_replay_matches_eager(gpu, T, position, dtype):
     """The device entry points enqueue kernels only (no allocation, no
     synchronisation, no memset), so they can be captured in a HIP graph; every
     replay, with eager work and synchronisations in between, reproduces the
     eager result bit for bit."""
     torch = gpu
-    w = Workload('graph', 24, 4, 256, T, position, 1 / 16, 'f16', 21, 1.0, 0.5)
+    w = Workload('graph', 24, 4, 256, T, position, 1 / 16, dtype, 21, 1.0, 0.5)
     q, k, v, _ = make_inputs(w)
     cache = make_cache(k, v, w, torch)
-    qt = to_torch(q, 'f16', torch)
+    qt = to_torch(q, dtype, torch)
     ws = A.workspace(A.attention_workspace_bytes(24, 4, 256, T, position))
     eager = A.attention(qt, cache, position, w.scale, ws=ws).clone()
     out = torch.empty_like(qt)

@@ -107,23 +107,26 @@ def test_values_outside_the_fp16_range(gpu, case):
         check(got[:, heads], want[:, heads], 2.0 ** -20)
 
 
-def random_prefill_shapes(n, seed=4096):
+def random_prefill_shapes(n, seed=4096, max_rows=1400, max_position=4000, first_seed=1700):
     """Seeded prefill shapes: KV heads 1-8, groups 1-8, head_dim 128/256,
     fp16/bf16, more than 48 query rows per KV head (the prefill kernel),
-    up to 1,400 of them (several workgroups per KV head), positions 0-4000
-    (tail pages of every fill), with and without outlier keys."""
+    up to max_rows of them (several workgroups per KV head), positions up to
+    max_position (tail pages of every fill; most calls split their keys),
+    with and without outlier keys."""
     rng = np.random.default_rng(seed)
     shapes = []
     for i in range(n):
         kv = int(rng.choice([1, 2, 4, 8]))
         group = int(rng.integers(1, 9))
-        tokens = int(rng.integers(49 // group + 1, 1400 // group + 1))
-        shapes.append((kv * group, kv, int(rng.choice([128, 256])), tokens, int(rng.integers(0, 4001)),
-                       str(rng.choice(['f16', 'bf16'])), int(rng.choice([0, 16])), 1700 + i))
+        tokens = int(rng.integers(49 // group + 1, max_rows // group + 1))
+        shapes.append((kv * group, kv, int(rng.choice([128, 256])), tokens, int(rng.integers(0, max_position + 1)),
+                       str(rng.choice(['f16', 'bf16'])), int(rng.choice([0, 16])), first_seed + i))
     return shapes
 
 
-@pytest.mark.parametrize('q_heads,kv_heads,head_dim,T,position,dtype,outliers,seed', random_prefill_shapes(12))
+@pytest.mark.parametrize('q_heads,kv_heads,head_dim,T,position,dtype,outliers,seed',
+                         random_prefill_shapes(12) + random_prefill_shapes(8, seed=9000, max_rows=400,
+                                                                            max_position=20000, first_seed=2300))
 def test_random_prefill_shapes(gpu, q_heads, kv_heads, head_dim, T, position, dtype, outliers, seed):
     """The prefill path on seeded random shapes, cache slots past the last
     key NaN: the float32 output to both bounds, the 16-bit output within
