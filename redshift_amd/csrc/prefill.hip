@@ -110,15 +110,14 @@ struct PrefillArgs {
     size_t head_stride;       // K and V pages
     int q_heads, kv_heads, group, rows, position, n_tiles;
     float scale_log2;
-    // Key splits (a call whose row workgroups alone would leave CUs idle):
-    // workgroup (split, j, h) takes pages split*split_pages ..
-    // +split_pages-1 of those its rows see, and stores fp32 partials for the
+    // Key splits: workgroup (split, j, h) takes the split-th of `splits`
+    // equal runs of the pages its rows see, and stores fp32 partials for the
     // combine kernel: its rows unnormalised ([kv_heads][splits][rows][D]),
     // their max (base 2) and sum ([kv_heads][splits][2][rows]).  One split:
-    // split_pages covers every page and the rows are stored normalised.
+    // the rows are stored normalised.
     float *part_o;
     float *part_ml;
-    int splits, split_pages;
+    int splits;
 };
 
 __device__ __forceinline__ int v_slot_token(int g, int j) {
@@ -205,8 +204,9 @@ __device__ __forceinline__ void prefill_rows(const PrefillArgs &a, KV *kring, VT
     // This split's pages: p0 + i for i = 0 .. nl-1 (local index i, ring
     // buffer i % 4).  nl is uniform over the workgroup; nl = 0 leaves empty
     // partials (no keys: sum 0, rows 0).
-    const int p0 = split * a.split_pages;
-    const int nl = max(0, min(n, p0 + a.split_pages) - p0);
+    const int sp = (n + a.splits - 1) / a.splits;
+    const int p0 = split * sp;
+    const int nl = max(0, min(n, p0 + sp) - p0);
     // Pages of this wave: those its last valid row sees (none without one).
     const int wave_last = min(row0 + 15, row_end - 1);
     const int n_wave = wave_last >= max(row0, 0) ? (a.position + wave_last / a.group + 1 + 31) / 32 : 0;
@@ -607,18 +607,27 @@ ConvPlan conv_plan(const Shape &s) {
 // Key splits.  A prefill workgroup fills a CU (its LDS rings), so a call with
 // fewer row workgroups (rows / 192, or / 128, times kv_heads) than the device
 // has CUs leaves the rest idle: a 64-token chunk on a 16K prefix runs in 12
-// workgroups.  Such a call splits every workgroup's pages over up to
-// CUs / row workgroups workgroups of at least kMinSplitPages pages each
-// (a workgroup's fixed costs, its query load and first page loads, take a
-// few microseconds; a page about 1.5), and the combine kernel merges the
-// partial rows.
-constexpr int kMinSplitPages = 8;
+// workgroups.  Such a call splits every row workgroup's pages into up to
+// CUs / row workgroups equal runs of at least kMinSplitPages pages, and
+// combine_prefill merges the partial rows.  A call over fewer than
+// kMinSplitKeyPages pages stays whole: a workgroup's fixed costs (its query
+// load, first page loads and partial stores) outweigh the pages it would
+// shed (300 tokens at 300: 27.8 us whole, 26 us for the split kernel alone).
+// Neither does a call with at least as many row workgroups as CUs split:
+// the precise 2048-token chunk (384 workgroups, 1.5 rounds) measured
+// 610-709 us split in two against 669 us whole.
+constexpr int kMinSplitPages = 8, kMinSplitKeyPages = 32, kMaxSplits = 64;
+
+size_t split_partial_bytes(const Shape &s, int splits) {
+    return splits > 1
+        ? ((size_t)s.kv_heads * splits * s.group() * s.tokens * (s.head_dim + 2) * sizeof(float) + 255) / 256 * 256
+        : 0;
+}
 
 struct PrefillPlan {
     int rows;          // query rows per workgroup
     int row_wgs;       // workgroups of rows per KV head
-    int pages;         // pages of keys 0 .. n_keys-1
-    int splits, split_pages;
+    int splits;
     size_t part_offset;  // partials in the workspace (after a bf16 call's V copy)
     size_t bytes;        // workspace
 };
@@ -626,18 +635,100 @@ struct PrefillPlan {
 PrefillPlan plan_prefill(const Shape &s, Dtype dtype, bool precise) {
     PrefillPlan p;
     p.rows = precise ? kPreciseRows : kPrefillRows;
-    const int R = s.group() * s.tokens;
-    p.row_wgs = (R + p.rows - 1) / p.rows;
-    p.pages = (s.n_keys() + 31) / 32;
-    const int base = p.row_wgs * s.kv_heads;
-    p.splits = std::max(1, std::min(device_cu_count() / base, p.pages / kMinSplitPages));
-    p.split_pages = (p.pages + p.splits - 1) / p.splits;
-    p.splits = (p.pages + p.split_pages - 1) / p.split_pages;
+    p.row_wgs = (s.group() * s.tokens + p.rows - 1) / p.rows;
+    const int pages = (s.n_keys() + 31) / 32;
+    const long long base = (long long)p.row_wgs * s.kv_heads;
+    p.splits = 1;
+    if (pages >= kMinSplitKeyPages && base < device_cu_count())
+        p.splits = (int)std::max(1LL, std::min<long long>({device_cu_count() / base, pages / kMinSplitPages,
+                                                           kMaxSplits}));
     p.part_offset = dtype == Dtype::BF16 && !precise ? conv_plan(s).bytes : 0;
-    p.bytes = p.part_offset;
-    if (p.splits > 1)
-        p.bytes += ((size_t)s.kv_heads * p.splits * R * (s.head_dim + 2) * sizeof(float) + 255) / 256 * 256;
+    p.bytes = p.part_offset + split_partial_bytes(s, p.splits);
     return p;
+}
+
+// ---- combine of split prefill partials ----
+// One wave per (row, KV head), lane l head dims DV*l .. DV*l+DV-1: the splits'
+// (m, l) pairs (the same address in every lane) and partial rows are loaded
+// kCombineBatch at a time, all in flight together, and folded into a running
+// (max, sum, row) in base 2.  A split that saw no key of the row stored
+// max -inf, sum 0 and a zero row, and weighs 0.
+struct CombinePrefillArgs {
+    const float *part_o;
+    const float *part_ml;
+    void *out;
+    const float *gate;
+    int q_heads, group, rows, kv_heads, splits;
+};
+constexpr int kCombineBatch = 8, kCombineThreads = 256;
+
+template <int D, typename KV, int MODE>
+__global__ __launch_bounds__(kCombineThreads)
+void combine_prefill(CombinePrefillArgs c) {
+    constexpr int DV = D / kWave;
+    typedef float FV __attribute__((ext_vector_type(DV)));
+    const int wave = blockIdx.x * (kCombineThreads / kWave) + (threadIdx.x >> 6), lane = threadIdx.x & 63;
+    if (wave >= c.rows * c.kv_heads) return;
+    const int h = wave / c.rows, row = wave - h * c.rows;
+    const float *ml = c.part_ml + (size_t)h * c.splits * 2 * c.rows + row;
+    const float *po = c.part_o + ((size_t)h * c.splits * c.rows + row) * D + lane * DV;
+    const size_t stride = (size_t)c.rows * D;
+    float M = -INFINITY, L = 0.f;
+    FV acc = {};
+    for (int s0 = 0; s0 < c.splits; s0 += kCombineBatch) {
+        float mv[kCombineBatch], lv[kCombineBatch];
+        FV ov[kCombineBatch];
+#pragma unroll
+        for (int i = 0; i < kCombineBatch; ++i) {
+            const int sc = min(s0 + i, c.splits - 1);
+            mv[i] = ml[(size_t)sc * 2 * c.rows];
+            lv[i] = ml[(size_t)sc * 2 * c.rows + c.rows];
+            ov[i] = *reinterpret_cast<const FV *>(po + sc * stride);
+        }
+        float rm = M;
+#pragma unroll
+        for (int i = 0; i < kCombineBatch; ++i) {
+            if (s0 + i >= c.splits) mv[i] = -INFINITY;
+            rm = fmaxf(rm, mv[i]);
+        }
+        const float mu = rm == -INFINITY ? 0.f : rm;
+        const float f = __builtin_amdgcn_exp2f(M - mu);
+        L *= f;
+        acc *= f;
+#pragma unroll
+        for (int i = 0; i < kCombineBatch; ++i) {
+            const float w = s0 + i < c.splits ? __builtin_amdgcn_exp2f(mv[i] - mu) : 0.f;
+            L += w * lv[i];
+            acc += w * ov[i];
+        }
+        M = rm;
+    }
+    const float inv = 1.f / L;
+    const int t = row / c.group, hq = h * c.group + (row - t * c.group);
+    const size_t idx = ((size_t)t * c.q_heads + hq) * D + lane * DV;
+    if constexpr (MODE == kOutSame) {
+        typedef KV KVV __attribute__((ext_vector_type(DV)));
+        KVV o;
+#pragma unroll
+        for (int d = 0; d < DV; ++d) o[d] = (KV)(acc[d] * inv);
+        *reinterpret_cast<KVV *>(static_cast<KV *>(c.out) + idx) = o;
+    } else {
+        FV o = acc * inv;
+        if constexpr (MODE == kOutGated) {
+            const FV g = *reinterpret_cast<const FV *>(c.gate + ((size_t)t * c.q_heads + hq) * 2 * D + D + lane * DV);
+#pragma unroll
+            for (int d = 0; d < DV; ++d) o[d] *= 1.f / (1.f + expf(-g[d]));
+        }
+        *reinterpret_cast<FV *>(static_cast<float *>(c.out) + idx) = o;
+    }
+}
+
+template <int D>
+const void *combine_prefill_kernel(Dtype dtype, bool out_f32, bool gated) {
+    if (gated) return (const void *)&combine_prefill<D, float, kOutGated>;
+    if (out_f32) return (const void *)&combine_prefill<D, float, kOutF32>;
+    return dtype == Dtype::BF16 ? (const void *)&combine_prefill<D, __bf16, kOutSame>
+                                : (const void *)&combine_prefill<D, _Float16, kOutSame>;
 }
 
 }  // namespace
@@ -670,7 +761,6 @@ void launch_prefill(const Shape &s, Dtype dtype, bool precise, float scale, cons
     a.n_tiles = plan.row_wgs;
     a.scale_log2 = scale * 1.4426950408889634f;
     a.splits = plan.splits;
-    a.split_pages = plan.split_pages;
     if (plan.splits > 1) {
         a.part_o = reinterpret_cast<float *>(static_cast<char *>(workspace) + plan.part_offset);
         a.part_ml = a.part_o + (size_t)s.kv_heads * plan.splits * a.rows * s.head_dim;
@@ -680,15 +770,38 @@ void launch_prefill(const Shape &s, Dtype dtype, bool precise, float scale, cons
     const long long grid = (long long)plan.row_wgs * s.kv_heads * plan.splits;
     require(grid * threads < (1LL << 32), "prefill launch exceeds 2^32 work-items");
     void *args[] = {&a};
-    // The combine of split calls (fp32 partial rows, stored with the default
-    // policy).
+    // The combine of split calls.  Up to 2 kCombineBatch splits (many rows):
+    // combine_prefill, a wave per row.  More splits (then at most CUs / 16
+    // row workgroups, few rows): attention_combine, whose four waves per row
+    // request up to 64 splits in one round (62 splits of 96 rows: 27.5 us
+    // per call against 31.1 us with combine_prefill's batches in turn).
     auto combine = [&] {
         if (plan.splits == 1) return;
-        SplitPlan cp = {};
-        cp.kind = SplitKind::Stream;
-        cp.rows = a.rows;
-        cp.splits = plan.splits;
-        launch_combine(s, cp, dtype, a.part_o, out, out_f32, gate, stream);
+        if (plan.splits > 2 * kCombineBatch) {
+            SplitPlan cp = {};
+            cp.kind = SplitKind::Stream;   // fp32 partial rows, default-policy stores
+            cp.rows = a.rows;
+            cp.splits = plan.splits;
+            launch_combine(s, cp, dtype, a.part_o, out, out_f32, gate, stream);
+            return;
+        }
+        CombinePrefillArgs c;
+        c.part_o = a.part_o;
+        c.part_ml = a.part_ml;
+        c.out = out;
+        c.gate = gate;
+        c.q_heads = s.q_heads;
+        c.group = a.group;
+        c.rows = a.rows;
+        c.kv_heads = s.kv_heads;
+        c.splits = plan.splits;
+        const long long waves = (long long)a.rows * s.kv_heads;
+        const long long blocks = (waves + kCombineThreads / kWave - 1) / (kCombineThreads / kWave);
+        require(blocks < (1LL << 31), "prefill combine exceeds the grid");
+        const void *kernel = d256 ? combine_prefill_kernel<256>(dtype, out_f32, gate != nullptr)
+                                  : combine_prefill_kernel<128>(dtype, out_f32, gate != nullptr);
+        void *cargs[] = {&c};
+        check(hipLaunchKernel(kernel, dim3((unsigned)blocks), dim3(kCombineThreads), cargs, 0, stream));
     };
     if (precise) {
         const void *kernel = d256 ? precise_prefill_kernel<256>(gate != nullptr) : precise_prefill_kernel<128>(gate != nullptr);

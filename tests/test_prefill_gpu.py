@@ -149,8 +149,9 @@ def test_random_prefill_shapes(gpu, q_heads, kv_heads, head_dim, T, position, dt
     (24, 4, 256, 16, 16000, 'f16'),    # 4 row workgroups: 62 key splits of about 8 pages
     (24, 4, 256, 64, 16000, 'bf16'),   # 8 row workgroups: 32 splits, V through the fp16 copy
     (16, 2, 128, 40, 9000, 'bf16'),
-    (24, 4, 256, 300, 300, 'f16'),     # 2 splits; the first rows see no key of the second
-    (8, 1, 256, 500, 0, 'f16'),        # from an empty cache: early workgroups' later splits empty
+    (1, 1, 128, 2400, 0, 'f16'),       # 9 splits; a workgroup's early rows see no key of its last run
+    (8, 1, 256, 1100, 0, 'bf16'),      # 4 splits; the early workgroups' later runs are empty
+    (24, 4, 256, 300, 300, 'f16'),     # 19 pages: not split
 ])
 def test_split_prefill_against_oracle(gpu, q_heads, kv_heads, head_dim, T, position, dtype):
     """Calls with too few row workgroups to fill the device split their keys
@@ -168,3 +169,16 @@ def test_split_prefill_against_oracle(gpu, q_heads, kv_heads, head_dim, T, posit
     half_ulp = np.abs(want) * (2.0 ** -8 if dtype == 'bf16' else 2.0 ** -11)
     assert np.all(np.abs(got16 - want) <= MAX_ABS + half_ulp)
 
+
+
+@pytest.mark.parametrize('scale,dtype', [(0.0, 'f16'), (-1 / 16, 'bf16')])
+def test_split_prefill_any_scale(gpu, scale, dtype):
+    """A split call (100 tokens after 2,000: 8 runs of pages per row
+    workgroup) under a zero scale (the mean of the visible values) and a
+    negative one, cache slots past the last key NaN, float32 output against
+    the oracle to both bounds."""
+    from tests.test_attention_gpu import gpu_attention
+    w = Workload('split_scale', 24, 4, 256, 100, 2000, scale, dtype, 61, 1.0, 0.5)
+    q, k, v, _ = make_inputs(w)
+    want = ref.gqa_attention(to_float(q, dtype), to_float(k, dtype), to_float(v, dtype), w.position, scale)
+    check(gpu_attention(w, q, k, v, gpu, fill_nan=True, out_dtype=gpu.float32), want)
