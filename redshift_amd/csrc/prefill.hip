@@ -39,7 +39,11 @@
 //
 // Scheduling: workgroup i serves KV head i % kv_heads (with 4 KV heads the
 // round-robin dispatch over the 8 XCDs keeps every head on the same two XCDs,
-// whose L2s then hold that head's pages for all of its workgroups).
+// whose L2s then hold that head's pages for all of its workgroups).  A call
+// with too few row workgroups to occupy every CU (a short chunk on a long
+// prefix) splits each row workgroup's pages into equal runs, one workgroup
+// per run; their fp32 partial rows are merged by combine_prefill (below) or,
+// for many runs, attention_combine, as in split-K decode.
 #include "combine.hpp"
 #include "kernels.hpp"
 #include "lds.hpp"
