@@ -18,6 +18,7 @@ attention (oracle/attention_ref.py), run on this host on one layer's decode.
 import argparse
 import json
 import os
+import statistics
 import sys
 import time
 from pathlib import Path
@@ -145,7 +146,7 @@ def time_workload(torch, A, w, layers, steps, warmup, seed):
     del caches
     torch.cuda.empty_cache()
     return dict(ms_per_step=graph_ms, eager_ms_per_step=eager_ms,
-                split_us=1000.0 * float(np.median(split_ms)), split_us_mean=1000.0 * sum(split_ms) / len(split_ms),
+                split_us=1000.0 * statistics.median(split_ms), split_us_mean=1000.0 * sum(split_ms) / len(split_ms),
                 split_graph_us=split_graph_us)
 
 
@@ -450,13 +451,20 @@ def main():
             # At least 52 timed calls at the default 50 steps (13 steps of 4 layers).
             rp = time_workload(torch, A, wp, 4, max(3, (args.steps + 3) // 4), 2, seed=2)
             kernel_s = rp['split_us'] * 1e-6
+            layer_s = rp['ms_per_step'] * 1e-3 / 4
             extra['prefill_2k'] = {'us_per_layer': round(1000 * rp['ms_per_step'] / 4, 1),
                                    'kernel_us': round(rp['split_us'], 1),
                                    'kernel_us_mean': round(rp['split_us_mean'], 1),
                                    'kernel_is': 'conversion pass + prefill kernel of one eager call, median '
                                                 'of the HIP-event-timed calls',
-                                   'TFLOP/s': round(wp.flops() / kernel_s / 1e12, 1),
-                                   'frac_mfma_peak': round(wp.flops() / kernel_s / MFMA_BF16_PEAK, 4),
+                                   'TFLOP/s': round(wp.flops() / layer_s / 1e12, 1),
+                                   'frac_mfma_peak': round(wp.flops() / layer_s / MFMA_BF16_PEAK, 4),
+                                   'kernel_TFLOP/s': round(wp.flops() / kernel_s / 1e12, 1),
+                                   'frac_mfma_peak_kernel': round(wp.flops() / kernel_s / MFMA_BF16_PEAK, 4),
+                                   'frac_is': 'frac_mfma_peak: the layer (conversion pass + prefill kernel) '
+                                              'replayed in a HIP graph, us_per_layer; frac_mfma_peak_kernel: '
+                                              'the eager HIP-event median, kernel_us, whose calls run the same '
+                                              'kernels between host launch gaps',
                                    'flops_per_layer': wp.flops()}
         for name in ('fused_verify8_16k', 'fused_decode_139k'):
             if name not in chosen:
