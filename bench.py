@@ -367,7 +367,8 @@ def main():
     ap.add_argument('--layers', type=int, default=LAYERS)
     ap.add_argument('--no-cpu', action='store_true', help='skip the CPU baseline')
     ap.add_argument('--no-extra', action='store_true', help='skip the secondary workloads')
-    ap.add_argument('--extras', default='verify8_16k,decode_16k,decode_4k,prefill_2k,fused_verify8_16k,fused_decode_139k,'
+    ap.add_argument('--extras', default='verify8_16k,decode_16k,decode_4k,prefill_2k,prefill512_6k,fused_verify8_16k,'
+                                        'fused_decode_139k,'
                                         'fused_prefill_2k,fused_prefill64_16k,fused_verify8_prefix16,'
                                         'fused_verify8_prefix128,kv_checkpoint_139k',
                     help='comma-separated secondary workloads to run')
@@ -466,6 +467,20 @@ def main():
                                               'the eager HIP-event median, kernel_us, whose calls run the same '
                                               'kernels between host launch gaps',
                                    'flops_per_layer': wp.flops()}
+        if 'prefill512_6k' in chosen:
+            # A 512-token bf16 chunk after 6144 cached tokens: 16 row workgroups
+            # per KV head, 64 in all, so the call splits every workgroup's pages
+            # into 4 runs and combines the partial rows (combine_prefill).
+            w5 = Workload('prefill512_6k', 24, 4, 256, 512, 6144, 1 / 16, 'bf16', 2)
+            log('prefill512_6k: 4 layers')
+            r5 = time_workload(torch, A, w5, 4, max(3, (args.steps + 3) // 4), 2, seed=11)
+            layer_s = r5['ms_per_step'] * 1e-3 / 4
+            extra['prefill512_6k'] = {'us_per_layer': round(1e6 * layer_s, 1),
+                                      'eager_call_us': round(r5['split_us'], 1),
+                                      'TFLOP/s': round(w5.flops() / layer_s / 1e12, 1),
+                                      'frac_mfma_peak': round(w5.flops() / layer_s / MFMA_BF16_PEAK, 4),
+                                      'what': 'qv_attention, 512 bf16 tokens at 6144, graph step: V conversion '
+                                              '+ prefill with its keys split in 4 + combine_prefill'}
         for name in ('fused_verify8_16k', 'fused_decode_139k'):
             if name not in chosen:
                 continue
