@@ -97,6 +97,14 @@ __device__ __forceinline__ float unpack_hi(uint32_t w, _Float16) {
 
 constexpr float kLazy = 8.f;
 
+// A 16-byte global load that the compiler does not track: the kernel's own
+// vmcnt waits cover it.  (Loads complete in order, so an untracked load never
+// weakens a wait the compiler places for its own loads.)
+template <typename V>
+__device__ __forceinline__ void global_load16(V &v, const void *p) {
+    asm volatile("global_load_dwordx4 %0, %1, off" : "=v"(v) : "v"(p) : "memory");
+}
+
 struct PrefillArgs {
     const void *q;
     const void *q_lo;       // lo parts of a precise (fp32) query, or null
@@ -181,9 +189,12 @@ __device__ __forceinline__ void prefill_rows(const PrefillArgs &a, KV *kring, VT
 
     // Query fragments (B operand): k-step ks of lane l holds row row0 + l%16,
     // dims 32*ks + 8*(l/16) .. +7.  Padded rows load a valid row; their
-    // results are not stored.  They are in registers before the first page
-    // is requested (a workgroup runs for hundreds of pages, so this one round
-    // trip is negligible, and the page loop never waits on them).
+    // results are not stored.  The first pages are requested right behind
+    // them (a split workgroup runs for a few pages only), and the prologue's
+    // wait covers both: loads complete in order, so a loader wave's wait for
+    // the first K page covers its query, and the other waves wait for their
+    // query alone.  (As compiler-tracked loads, the compiler would wait for
+    // every page in flight before their first use.)
     V8 qf[KS], qlo[QSPLIT ? KS : 1];
     int limit;
     {
@@ -193,14 +204,13 @@ __device__ __forceinline__ void prefill_rows(const PrefillArgs &a, KV *kring, VT
         const KV *src = static_cast<const KV *>(a.q) +
                         ((size_t)t * a.q_heads + (size_t)h * a.group + gg) * D + 8 * g;
 #pragma unroll
-        for (int ks = 0; ks < KS; ++ks) qf[ks] = *reinterpret_cast<const V8 *>(src + 32 * ks);
+        for (int ks = 0; ks < KS; ++ks) global_load16(qf[ks], src + 32 * ks);
         if constexpr (QSPLIT) {
             const KV *lo = static_cast<const KV *>(a.q_lo) + (src - static_cast<const KV *>(a.q));
 #pragma unroll
-            for (int ks = 0; ks < KS; ++ks) qlo[ks] = *reinterpret_cast<const V8 *>(lo + 32 * ks);
+            for (int ks = 0; ks < KS; ++ks) global_load16(qlo[ks], lo + 32 * ks);
         }
     }
-    wait_vmcnt<0>();
     // Keys this workgroup can see: 0 .. position + (token of its last row,
     // the last valid row of tile T-1-4j).
     const int n_keys = a.position + (min(16 * (T - 4 * j), R) - 1) / a.group + 1;
@@ -395,13 +405,18 @@ __device__ __forceinline__ void prefill_rows(const PrefillArgs &a, KV *kring, VT
         stage(vh, 0, vring);
         if (nl > 1) { stage(kh, 1, kring); stage(vh, 1, vring); }
         if (nl > 2) stage(kh, 2, kring);
-        if (nl > 2) wait_vmcnt<4 * H>();
+        // Loader waves: K0 has landed, and the query loads before it.  The
+        // others issued no page loads: their query loads.
+        if (w >= kLoaders) wait_vmcnt<0>();
+        else if (nl > 2) wait_vmcnt<4 * H>();
         else if (nl > 1) wait_vmcnt<3 * H>();
         else wait_vmcnt<H>();
         ring_barrier();
         read_k(std::integral_constant<int, 0>{}, kring_lane);
         read_k(std::integral_constant<int, 1>{}, kring_lane);
         static_for<0, KS>([&](auto ks) { qk_chunk(ks, kring_lane, s); });
+    } else {
+        wait_vmcnt<0>();   // no page of this split: the query loads only
     }
 
     // The waves meet every second step (i even): K(i+1), K(i+2), V(i) and
