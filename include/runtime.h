@@ -129,8 +129,11 @@ int qv_attention_workspace(uint64_t *bytes, int q_heads, int kv_heads, int head_
  * capacity. Up to 48 query
  * rows per KV head (G*tokens): split-K over all CUs plus a log-sum-exp
  * combine (qv_attention_split then qv_attention_combine). More rows (chunked
- * prefill): one workgroup per 192 rows streams the visible pages through LDS;
- * the workspace is then 0 bytes and may be NULL. */
+ * prefill): one workgroup per 192 rows streams the visible pages through LDS.
+ * Its workspace holds, for bf16 pages, an fp16 copy of the call's V pages,
+ * and, for a call with fewer such workgroups than the device has CUs (a short
+ * chunk on a long prefix), the fp32 partial rows of its key splits; an fp16
+ * call that needs neither takes 0 bytes and the pointer may be NULL. */
 int qv_attention(void *out, const void *q, const void *k_pages, const void *v_pages,
                  int dtype, int out_dtype, int q_heads, int kv_heads, int head_dim,
                  int tokens, int position, int capacity, float scale,
@@ -153,11 +156,12 @@ int qv_attention_combine(void *out, int dtype, int out_dtype, int q_heads, int k
  * allocate device memory (code under HIP graph capture, tight serving loops,
  * harnesses that forbid hipMalloc).  No counterpart in the reference.  It
  * runs the same kernels, and gives the same bits, as qv_attention; the
- * workspace (split-K partials, or a bf16 prefill's fp16 copy of its V pages)
- * lives in a static device array of 64 MiB per GPU, held until the process
- * ends (the largest split-K plan on a 256-CU MI355X takes 12.1 MiB, a bf16
- * prefill kv_heads*keys*head_dim*2 bytes; a shape that needs more is
- * refused).  The call itself allocates
+ * workspace (split-K partials, a bf16 prefill's fp16 copy of its V pages,
+ * a split prefill's partials) lives in a static device array of 64 MiB per
+ * GPU, held until the process ends (the largest split-K plan on a 256-CU
+ * MI355X takes 12.1 MiB, a bf16 prefill kv_heads*keys*head_dim*2 bytes, a
+ * split prefill's partials at most about 51 MB at head_dim 256; a shape that
+ * needs more is refused).  The call itself allocates
  * nothing.  Every call on one GPU shares that GPU's array: calls that
  * overlap on one GPU (concurrent streams, or threads) race on it, so
  * serialise them.  No kernel reads a partial it has not written in the same
