@@ -115,7 +115,8 @@ int qv_kv_copy(void *dst_k, void *dst_v, const void *src_k, const void *src_v,
                void *stream);
 
 /* Workspace bytes that qv_attention needs for this shape on the current
- * device (split-K partials). */
+ * device: split-K partials, or a prefill's fp16 V copy (bf16 pages) and key
+ * split partials; the larger of the fp16 and bf16 page types. */
 int qv_attention_workspace(uint64_t *bytes, int q_heads, int kv_heads, int head_dim,
                            int tokens, int position);
 /* Raw causal GQA attention core, the reference's attention / attention_tiled

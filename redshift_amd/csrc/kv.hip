@@ -110,9 +110,13 @@ void split_query(_Float16 *hi, _Float16 *lo, const float *q, size_t n) {
 // stride dst_stride.  Each thread moves kCopyUnroll 16-byte pieces of one
 // head, all loads issued before the stores, non-temporal (every byte is
 // touched once).  n is a whole number of pages, so per_head (16-byte pieces
-// per head) is a multiple of 32 * D / 8 = 512 (D = 128) or 1024 (D = 256),
-// and thus of kCopyUnroll * kCopyThreads.
-constexpr int kCopyUnroll = 4, kCopyThreads = 128;
+// per head) is a multiple of 32 * D / 8 = 512 (D = 128) or 1024 (D = 256):
+// the launch takes kCopyThreads threads when kCopyUnroll * kCopyThreads
+// divides it, else half as many.  A sweep on the 139,264-token K and V
+// prefix (4 KV heads, D = 256; per call, K and V): 2 x 512 174.4 us, 4 x 256
+// 177.7, 2 x 256 180.2, 4 x 128 184.8, 4 x 512 185.4, default-policy
+// loads and stores 202.1.
+constexpr int kCopyUnroll = 2, kCopyThreads = 512;
 __global__ __launch_bounds__(kCopyThreads)
 void copy_pages(uint4 *dst, const uint4 *src, size_t dst_stride, size_t src_stride, size_t n,
                 int kv_heads) {
@@ -139,14 +143,15 @@ void launch_copy(void *dst_k, void *dst_v, const void *src_k, const void *src_v,
                  int head_dim, int dst_capacity, int src_capacity, int pages, hipStream_t stream) {
     const size_t n = (size_t)pages * kPageTokens * head_dim;   // 16-bit elements per head
     if (!n) return;
-    require((n / 8) % (kCopyUnroll * kCopyThreads) == 0, "page copy needs whole 512-piece chunks per head");
-    const size_t chunks = n / 8 / (kCopyUnroll * kCopyThreads) * kv_heads;
+    const int threads = (n / 8) % (kCopyUnroll * kCopyThreads) == 0 ? kCopyThreads : kCopyThreads / 2;
+    require((n / 8) % (kCopyUnroll * threads) == 0, "page copy needs whole chunks of 16-byte pieces per head");
+    const size_t chunks = n / 8 / (kCopyUnroll * threads) * kv_heads;
     const unsigned blocks = (unsigned)std::min<size_t>(chunks, 16384);
     const size_t ds = (size_t)dst_capacity * head_dim, ss = (size_t)src_capacity * head_dim;
-    hipLaunchKernelGGL(copy_pages, dim3(blocks), dim3(kCopyThreads), 0, stream, static_cast<uint4 *>(dst_k),
+    hipLaunchKernelGGL(copy_pages, dim3(blocks), dim3(threads), 0, stream, static_cast<uint4 *>(dst_k),
                        static_cast<const uint4 *>(src_k), ds, ss, n, kv_heads);
     check(hipGetLastError());
-    hipLaunchKernelGGL(copy_pages, dim3(blocks), dim3(kCopyThreads), 0, stream, static_cast<uint4 *>(dst_v),
+    hipLaunchKernelGGL(copy_pages, dim3(blocks), dim3(threads), 0, stream, static_cast<uint4 *>(dst_v),
                        static_cast<const uint4 *>(src_v), ds, ss, n, kv_heads);
     check(hipGetLastError());
 }

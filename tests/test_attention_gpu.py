@@ -574,24 +574,27 @@ def test_one_workspace_across_shapes_and_phases(gpu):
 
 # ---- KV-cache manager (checkpoint / restore / commit) ----------------------
 
-@pytest.mark.parametrize('head_dim,kv_heads', [(256, 4), (128, 2)])
-def test_kv_copy_prefix_bitwise(gpu, head_dim, kv_heads):
+@pytest.mark.parametrize('head_dim,kv_heads,tokens', [(256, 4, 1000), (128, 2, 1000),
+                                                     (128, 2, 970),    # 31 pages: the half-size blocks
+                                                     (256, 4, 970)])
+def test_kv_copy_prefix_bitwise(gpu, head_dim, kv_heads, tokens):
     """qv_kv_copy moves the pages of a prefix between caches of different
-    capacities, every value bit for bit; a snapshot of 1000 tokens needs 1024."""
+    capacities, every value bit for bit; a snapshot of 1000 tokens needs 1024
+    (970 tokens: 992)."""
     from redshift_amd.kvcache import copy_prefix
     rng = np.random.default_rng(7)
     rows = gpu.from_numpy(rng.standard_normal((3000, kv_heads, head_dim)).astype(np.float16)).cuda()
     big = A.PagedKV(kv_heads, head_dim, 4096, gpu.float16).pack(rows, -rows)
-    snap = A.PagedKV(kv_heads, head_dim, 1024, gpu.float16)
-    copy_prefix(snap, big, 1000)
+    snap = A.PagedKV(kv_heads, head_dim, A.round_capacity(tokens), gpu.float16)
+    copy_prefix(snap, big, tokens)
     other = A.PagedKV(kv_heads, head_dim, 2048, gpu.float16)
     other.k.fill_(float('nan'))
     other.v.fill_(float('nan'))
-    copy_prefix(other, snap, 1000)
+    copy_prefix(other, snap, tokens)
     for cache in (snap, other):
-        k, v = cache.unpack(0, 1000)
-        np.testing.assert_array_equal(k.cpu().numpy().view(np.uint16), rows[:1000].cpu().numpy().view(np.uint16))
-        np.testing.assert_array_equal(v.cpu().numpy().view(np.uint16), (-rows[:1000]).cpu().numpy().view(np.uint16))
+        k, v = cache.unpack(0, tokens)
+        np.testing.assert_array_equal(k.cpu().numpy().view(np.uint16), rows[:tokens].cpu().numpy().view(np.uint16))
+        np.testing.assert_array_equal(v.cpu().numpy().view(np.uint16), (-rows[:tokens]).cpu().numpy().view(np.uint16))
 
 
 def random_shapes(n, seed=2024):
