@@ -623,3 +623,50 @@ def test_random_shapes_against_oracle(gpu, q_heads, kv_heads, head_dim, T, posit
     q, k, v, _ = make_inputs(w)
     want = ref.gqa_attention(to_float(q, dtype), to_float(k, dtype), to_float(v, dtype), position, w.scale)
     assert_parity(gpu_attention(w, q, k, v, gpu, fill_nan=True, out_dtype=gpu.float32), want)
+
+
+def random_fused_shapes(n, seed=77):
+    """Seeded (batch, position) pairs over every route of the fused entry:
+    one launch on short contexts, decode, verification batches, prefill
+    chunks whole or with their keys split (longer batches on shorter
+    prefixes, to keep the oracle quick)."""
+    rng = np.random.default_rng(seed)
+    shapes = []
+    for i in range(n):
+        batch = int(rng.choice([1, 2, 3, 5, 8, 9, 16, 33, 64, 100]))
+        limit = 20000 if batch <= 64 else 4000
+        position = int(rng.choice([int(rng.integers(0, 256)), int(rng.integers(256, limit + 1))]))
+        shapes.append((batch, min(position, 139264 - batch), 3000 + i))
+    return shapes
+
+
+@pytest.mark.parametrize('batch,position,seed', random_fused_shapes(14))
+def test_fused_random_shapes_against_oracle(gpu, batch, position, seed):
+    """qv_attention_fused on seeded random inputs (fp16 prefix caches of
+    N(0,1)/2 values, q_gate, key and value N(0,1), norms 1 +- 1/4) against the
+    oracle's fused attention, with the reference test's tolerances: output
+    3e-4, appended K 2e-3, V exact; the prefix unchanged."""
+    torch = gpu
+    rng = np.random.default_rng(seed)
+    kc = (rng.standard_normal((position, 4, 256)) * .5).astype(np.float16)
+    vc = (rng.standard_normal((position, 4, 256)) * .5).astype(np.float16)
+    q_gate = rng.standard_normal((batch, 24, 512)).astype(np.float32)
+    key = rng.standard_normal((batch, 4, 256)).astype(np.float32)
+    value = rng.standard_normal((batch, 4, 256)).astype(np.float32)
+    q_norm = (1 + .25 * rng.uniform(-1, 1, 256)).astype(np.float32)
+    k_norm = (1 + .25 * rng.uniform(-1, 1, 256)).astype(np.float32)
+    eps = 1e-6
+    print(f'fused random: batch={batch} position={position} seed={seed}', flush=True)
+    expected = ref.fused_attention(kc, vc, q_gate, key, value, q_norm, k_norm, batch, position, eps)
+    cache = A.PagedKV(4, 256, A.round_capacity(position + batch), torch.float16)
+    cache.k.fill_(float('nan'))
+    cache.v.fill_(float('nan'))
+    if position:
+        cache.pack(torch.from_numpy(kc).cuda(), torch.from_numpy(vc).cuda())
+    dev = [torch.from_numpy(x).cuda() for x in (q_gate, key, value, q_norm, k_norm)]
+    out = A.attention_fused(*dev, cache, position, eps)
+    kcache, vcache = cache.unpack(0, position + batch)
+    torch.cuda.synchronize()
+    assert_close(out.cpu().numpy(), expected[0], 3e-4)
+    assert_close(kcache.float().cpu().numpy(), expected[1], 2e-3)
+    assert_close(vcache.float().cpu().numpy(), expected[2], 0)
