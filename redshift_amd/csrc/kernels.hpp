@@ -163,6 +163,24 @@ void launch_fused_short(const FusedToken &tok, float *out, hipStream_t stream);
 // rows (in the workspace, after the V copy) the combine kernel merges.
 // prefill_workspace_bytes: the workspace of a call (0 when it needs none).
 size_t prefill_workspace_bytes(const Shape &s, Dtype dtype, bool precise);
+
+// The prefill's launch plan for a device of `cus` CUs: rows per workgroup
+// (kPrefillRows, or kPreciseRows for a precise query), row workgroups per
+// KV head, key splits (1, or up to kPrefillMaxSplits runs of at least
+// kPrefillMinSplitPages pages when the row workgroups number fewer than the
+// CUs and the call covers at least kPrefillMinSplitKeyPages pages; at most
+// one workgroup per CU then), and its workspace: a raw bf16 call's fp16 V
+// copy and range words, then (at part_offset) the split partials.
+constexpr int kPrefillRows = 192, kPreciseRows = 128;
+constexpr int kPrefillMinSplitPages = 8, kPrefillMinSplitKeyPages = 32, kPrefillMaxSplits = 64;
+struct PrefillPlan {
+    int rows;            // query rows per workgroup
+    int row_wgs;         // workgroups of rows per KV head
+    int splits;
+    size_t part_offset;  // split partials in the workspace
+    size_t bytes;        // workspace
+};
+PrefillPlan plan_prefill_for(const Shape &s, Dtype dtype, bool precise, int cus);
 void launch_prefill(const Shape &s, Dtype dtype, bool precise, float scale, const void *q,
                     const void *q_lo, const void *k_pages, const void *v_pages, void *out, bool out_f32,
                     const float *gate, void *workspace, hipStream_t stream);

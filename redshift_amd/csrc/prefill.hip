@@ -530,11 +530,10 @@ void attention_prefill_bf16(PrefillArgs a) {
                                                                     a.v_copy, a.v_copy_stride);
 }
 
-// Rows per workgroup: 192 (twelve waves, three per SIMD; 2048 tokens of six
-// query heads per KV head make 64 workgroups per KV head, one round on 256
-// CUs).  A precise query (hi + lo parts) needs twice the query registers:
-// 128 rows (eight waves, two per SIMD).
-constexpr int kPrefillRows = 192, kPreciseRows = 128;
+// Rows per workgroup (kPrefillRows, kernels.hpp): 192 (twelve waves, three
+// per SIMD; 2048 tokens of six query heads per KV head make 64 workgroups
+// per KV head, one round on 256 CUs).  A precise query (hi + lo parts) needs
+// twice the query registers: kPreciseRows = 128 (eight waves, two per SIMD).
 
 // The raw instances: fp16 pages; bf16 pages, V through the conversion pass
 // below (attention_prefill_bf16).
@@ -627,15 +626,14 @@ ConvPlan conv_plan(const Shape &s) {
 // fewer row workgroups (rows / 192, or / 128, times kv_heads) than the device
 // has CUs leaves the rest idle: a 64-token chunk on a 16K prefix runs in 12
 // workgroups.  Such a call splits every row workgroup's pages into up to
-// CUs / row workgroups equal runs of at least kMinSplitPages pages, and
-// combine_prefill merges the partial rows.  A call over fewer than
-// kMinSplitKeyPages pages stays whole: a workgroup's fixed costs (its query
+// CUs / row workgroups equal runs of at least kPrefillMinSplitPages pages,
+// and combine_prefill merges the partial rows.  A call over fewer than
+// kPrefillMinSplitKeyPages pages stays whole: a workgroup's fixed costs (its query
 // load, first page loads and partial stores) outweigh the pages it would
 // shed (300 tokens at 300: 27.8 us whole, 26 us for the split kernel alone).
 // Neither does a call with at least as many row workgroups as CUs split:
 // the precise 2048-token chunk (384 workgroups, 1.5 rounds) measured
 // 610-709 us split in two against 669 us whole.
-constexpr int kMinSplitPages = 8, kMinSplitKeyPages = 32, kMaxSplits = 64;
 
 size_t split_partial_bytes(const Shape &s, int splits) {
     return splits > 1
@@ -643,27 +641,26 @@ size_t split_partial_bytes(const Shape &s, int splits) {
         : 0;
 }
 
-struct PrefillPlan {
-    int rows;          // query rows per workgroup
-    int row_wgs;       // workgroups of rows per KV head
-    int splits;
-    size_t part_offset;  // partials in the workspace (after a bf16 call's V copy)
-    size_t bytes;        // workspace
-};
+}  // namespace
 
-PrefillPlan plan_prefill(const Shape &s, Dtype dtype, bool precise) {
+PrefillPlan plan_prefill_for(const Shape &s, Dtype dtype, bool precise, int cus) {
     PrefillPlan p;
     p.rows = precise ? kPreciseRows : kPrefillRows;
     p.row_wgs = (s.group() * s.tokens + p.rows - 1) / p.rows;
-    const int pages = (s.n_keys() + 31) / 32;
+    const long long pages = ((long long)s.n_keys() + 31) / 32;
     const long long base = (long long)p.row_wgs * s.kv_heads;
     p.splits = 1;
-    if (pages >= kMinSplitKeyPages && base < device_cu_count())
-        p.splits = (int)std::max(1LL, std::min<long long>({device_cu_count() / base, pages / kMinSplitPages,
-                                                           kMaxSplits}));
+    if (pages >= kPrefillMinSplitKeyPages && base < cus)
+        p.splits = (int)std::max(1LL, std::min<long long>({cus / base, pages / kPrefillMinSplitPages,
+                                                           kPrefillMaxSplits}));
     p.part_offset = dtype == Dtype::BF16 && !precise ? conv_plan(s).bytes : 0;
     p.bytes = p.part_offset + split_partial_bytes(s, p.splits);
     return p;
+}
+
+namespace {
+PrefillPlan plan_prefill(const Shape &s, Dtype dtype, bool precise) {
+    return plan_prefill_for(s, dtype, precise, device_cu_count());
 }
 
 // ---- combine of split prefill partials ----

@@ -11,8 +11,9 @@
 //     with its messages (invalid inputs only, each rejected before any device
 //     work, with heap buffers of one element where a buffer is passed, so a
 //     read before validation is an ASan report), qv_kv_bytes over a sweep
-//     including int32 extremes, and the split planner (plan_split_for, no
-//     device query) over a sweep of shapes with its invariants;
+//     including int32 extremes, and the split-K and prefill planners
+//     (plan_split_for, plan_prefill_for; no device query) over sweeps of
+//     shapes with their invariants;
 //   * device mode (a GPU is present): the same plus small real calls of
 //     every entry point on device buffers, the workspace queries against the
 //     planner, the error paths that need a device, and qv_test_attention on
@@ -273,6 +274,62 @@ void planner_sweep() {
     std::printf("abi_sanitize: %d split plans checked\n", plans);
 }
 
+// The prefill planner on a sweep of shapes and devices (no device query):
+// rows per workgroup, key splits only for calls of at least
+// kPrefillMinSplitKeyPages pages whose row workgroups leave CUs idle, then at
+// most one workgroup per CU in runs of at least kPrefillMinSplitPages pages,
+// as many as those bounds allow; the workspace is the documented sum without
+// overflow, and the launch stays within 2^32 work-items.
+void prefill_planner_sweep() {
+    const int heads[][2] = {{24, 4}, {8, 2}, {16, 2}, {24, 1}, {48, 1}, {64, 8}, {256, 256}};
+    const int positions[] = {0, 31, 32, 1000, 6144, 16384, 139263, 1 << 20, (1 << 30) - 1};
+    int plans = 0;
+    for (const auto &hk : heads)
+        for (int d : {128, 256})
+            for (int cus : {1, 8, 80, 256, 304})
+                for (int pos : positions)
+                    for (long long t : {0LL, 64LL, 300LL, 2048LL, 8192LL, 1LL << 28})
+                        for (int dt = 0; dt < 2; ++dt)
+                            for (int precise = 0; precise < 2; ++precise) {
+                                const int group = hk[0] / hk[1];
+                                long long tokens = t ? t : 48 / group + 1;   // 0: the fewest prefill tokens
+                                tokens = std::min(tokens, (1LL << 28) / hk[0]);
+                                if (tokens < 1 || (long long)group * tokens <= rs::kMaxRows ||
+                                    (long long)pos + tokens > 2147483616LL)
+                                    continue;
+                                const rs::Shape s{hk[0], hk[1], d, (int)tokens, pos, 0};
+                                const rs::Dtype dtype = dt ? rs::Dtype::BF16 : rs::Dtype::F16;
+                                const rs::PrefillPlan p = rs::plan_prefill_for(s, dtype, precise, cus);
+                                ++plans;
+                                const long long R = (long long)group * tokens;
+                                const long long pages = ((long long)pos + tokens + 31) / 32;
+                                EXPECT(p.rows == (precise ? rs::kPreciseRows : rs::kPrefillRows));
+                                EXPECT(p.row_wgs == (R + p.rows - 1) / p.rows);
+                                const long long base = (long long)p.row_wgs * hk[1];
+                                EXPECT(p.splits >= 1 && p.splits <= rs::kPrefillMaxSplits);
+                                if (pages < rs::kPrefillMinSplitKeyPages || base >= cus) {
+                                    EXPECT(p.splits == 1);
+                                } else {
+                                    // Within every bound, and one more split would break one.
+                                    EXPECT(base * p.splits <= cus && p.splits * rs::kPrefillMinSplitPages <= pages);
+                                    EXPECT(p.splits == rs::kPrefillMaxSplits || base * (p.splits + 1) > cus ||
+                                           (p.splits + 1) * rs::kPrefillMinSplitPages > pages);
+                                }
+                                const auto r256 = [](unsigned __int128 x) { return (x + 255) / 256 * 256; };
+                                const unsigned __int128 conv =
+                                    dt && !precise ? r256((unsigned __int128)hk[1] * pages * 32 * d * 2) +
+                                                         r256((unsigned __int128)hk[1] * pages * 4)
+                                                   : 0;
+                                const unsigned __int128 parts =
+                                    p.splits > 1 ? r256((unsigned __int128)hk[1] * p.splits * R * (d + 2) * 4) : 0;
+                                EXPECT((unsigned __int128)p.part_offset == conv);
+                                EXPECT((unsigned __int128)p.bytes == conv + parts);
+                                EXPECT((unsigned __int128)p.row_wgs * hk[1] * p.splits * (p.rows / 16) * 64 <
+                                       ((unsigned __int128)1 << 32));
+                            }
+    std::printf("abi_sanitize: %d prefill plans checked\n", plans);
+}
+
 // ---- device mode -------------------------------------------------------------
 
 #define HIP_OK(call) EXPECT((call) == hipSuccess)
@@ -463,6 +520,7 @@ int main(int argc, char **argv) {
     kv_bytes_sweep();
     device_entry_validation();
     planner_sweep();
+    prefill_planner_sweep();
     int devices = 0;
     const bool gpu = hipGetDeviceCount(&devices) == hipSuccess && devices > 0;
     std::printf("abi_sanitize: host checks done (%d checks, %d failed); %s\n", checks, failures,
