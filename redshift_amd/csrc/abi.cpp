@@ -416,7 +416,9 @@ extern "C" int qv_attention(void *out, const void *q, const void *k_pages, const
 // x 48 rows x (256 + 2) floats = 12.1 MiB (split counts are capped by the
 // resident workgroups, and a KV head never has fewer than one split); a bf16
 // prefill keeps an fp16 copy of its V pages there, kv_heads x keys x
-// head_dim x 2 bytes (32 MiB for 4 x 256 at 16,384 keys).
+// head_dim x 2 bytes (32 MiB for 4 x 256 at 16,384 keys), and a prefill that
+// splits its keys its partial rows (at most about 51 MB at head_dim 256 on
+// 256 CUs: one 192-row workgroup per CU).
 constexpr size_t kScratchBytes = size_t(64) << 20;
 static __device__ __align__(256) unsigned char scratch[kScratchBytes];
 
