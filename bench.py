@@ -493,7 +493,10 @@ def main():
                            'what': 'qv_attention_fused per layer: prepare + append + attention + gate'
                                    + (' (one token: query prepared and key and value appended in the '
                                       'split kernel, the new key added in the combine; two launches)'
-                                      if wf.tokens == 1 else '')}
+                                      if wf.tokens == 1 else
+                                      ' (query prepared in the ring kernel while its first pages load, '
+                                      'new keys attended to and appended by its first split; gated '
+                                      'combine; two launches)')}
         if 'fused_prefill_2k' in chosen:
             # The fused drop-in on a 2048-token prefill chunk at position 6144
             # (fp16 pages, the model's fp32 q_gate/key/value), one call per layer.

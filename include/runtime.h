@@ -197,7 +197,10 @@ int qv_attention_fused_workspace(uint64_t *bytes, int batch, int position);
  * the caches are fp16 pages with 24/4/256 geometry. batch is 1..8 as in the
  * reference, or a prefill chunk of up to 8192 tokens (the reference's server
  * prefills in 8-token steps, qvelox/server.py:177-192): more than 8 tokens
- * run the chunked-prefill kernel with the same fp32-query precision. */
+ * run the chunked-prefill kernel with the same fp32-query precision.  Up to
+ * 8 tokens prepare q and k inside the attention kernels (one launch on at
+ * most 256 keys, else the split kernel and the combine); a prefill chunk
+ * runs a prepare launch first. */
 int qv_attention_fused(float *out, void *k_pages, void *v_pages,
                        const float *q_gate, const float *key, const float *value,
                        const float *q_norm, const float *k_norm,

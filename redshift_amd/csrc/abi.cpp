@@ -166,12 +166,15 @@ size_t fused_partials_bytes(int batch, int position) {
 
 // The reference's k_attention on device buffers of the 24/4/256 model.  A
 // short context (up to 8 tokens, position + batch <= 256): one launch that
-// does everything.  One token after at least one cached key (decode): two
-// launches, the split kernel preparing the query and appending the new key
-// and value, the combine adding that key.  Otherwise (verification, a
-// prefill chunk) the prepare kernel writes the query's hi + lo parts to
-// q_hilo (2 * batch * 24 * 256 fp16) and appends the new K/V to the pages,
-// then attention (with the sigmoid gate) runs on them.
+// does everything.  Up to 8 tokens after at least one cached key (decode,
+// verification): two launches, the split kernel preparing the query and
+// appending the new keys and values, the combine merging (and, for one or
+// two tokens, adding the new keys).  A prefill chunk (more than 8 tokens):
+// the prepare kernel writes the query's hi + lo parts to q_hilo
+// (2 * batch * 24 * 256 fp16) and appends the new K/V to the pages, then
+// attention (with the sigmoid gate) runs on them; its workgroups read new
+// keys that other workgroups would append, so the append stays a launch of
+// its own.
 void fused_attention(float *out, void *k_pages, void *v_pages, const float *q_gate, const float *key,
                      const float *value, const float *q_norm, const float *k_norm, int batch,
                      int position, int capacity, float epsilon, uint16_t *q_hilo, void *partials,
@@ -566,8 +569,9 @@ extern "C" int qv_attention_fused(float *out, void *k_pages, void *v_pages,
         constexpr int H = rs::kModelQHeads, HKV = rs::kModelKvHeads, D = rs::kModelHeadDim;
         const rs::Shape s{H, HKV, D, batch, position, capacity};
         fits_cache(s);
-        require(aligned16(out) && aligned16(q_gate) && aligned16(workspace) && aligned16(k_pages) &&
-                aligned16(v_pages), "attention buffers must be 16-byte aligned");
+        require(aligned16(out) && aligned16(q_gate) && aligned16(key) && aligned16(value) && aligned16(q_norm) &&
+                aligned16(k_norm) && aligned16(workspace) && aligned16(k_pages) && aligned16(v_pages),
+                "attention buffers must be 16-byte aligned");
         require(workspace_bytes >= fused_workspace(batch, position), "workspace too small");
         hipStream_t st = static_cast<hipStream_t>(stream);
         uint16_t *q = static_cast<uint16_t *>(workspace);   // hi then lo fp16 parts

@@ -407,8 +407,8 @@ struct CombineArgs {
     void *out;
     const float *gate;   // gated output: q_gate rows of 2*D floats, gate at +D
     int q_heads, group, rows, splits;
-    float scale_log2;     // NEWKEY: the new key's score scale
-    FusedToken tok;       // NEWKEY: the new token
+    float scale_log2;     // NEWKEY: the new keys' score scale
+    FusedToken tok;       // NEWKEY: the new tokens
 };
 
 // Standalone combine: one workgroup (4 waves) per (row, KV head).
@@ -662,8 +662,14 @@ void launch_fused_tokens(const FusedToken &tok, int capacity, void *workspace, f
     FusedToken ft = tok;
     ft.q_prep = reinterpret_cast<float *>(static_cast<char *>(workspace) + fused_prep_offset(T, tok.position));
 
-    require(plan.kind == SplitKind::Stream && plan.rows <= 12, "the prepared-query stream kernel takes one or two tokens");
-    const void *split = (const void *)&attention_stream<D, true, true, _Float16, true>;
+    // One or two tokens (one query tile): the stream kernel, whose first
+    // split appends the new keys and publishes the prepared query rows, from
+    // which the combine adds the new keys.  More: the ring kernel, whose
+    // first split attends to the new keys itself and appends them.
+    const bool ring = plan.kind == SplitKind::Ring;
+    require(ring || plan.rows <= 12, "the prepared-query stream kernel takes one or two tokens");
+    const void *split = ring ? ring_prep_kernel(plan.nqt) : (const void *)&attention_stream<D, true, true, _Float16, true>;
+    require(split != nullptr, "no prepared-query ring kernel for this many tokens");
 
     SplitArgs a = {};
     a.k_pages = tok.k_pages;
@@ -682,7 +688,7 @@ void launch_fused_tokens(const FusedToken &tok, int capacity, void *workspace, f
     a.scale_log2 = kScaleLog2;
     a.tok = ft;
     void *split_args[] = {&a};
-    check(hipLaunchKernel(split, dim3(plan.splits * kv_heads), dim3(kWaves * kWave), split_args, 0, stream));
+    check(hipLaunchKernel(split, dim3(plan.splits * kv_heads), dim3(block_threads(plan)), split_args, 0, stream));
 
     CombineArgs c = {};
     c.part_o = workspace;
@@ -695,9 +701,10 @@ void launch_fused_tokens(const FusedToken &tok, int capacity, void *workspace, f
     c.splits = plan.splits;
     c.scale_log2 = kScaleLog2;
     c.tok = ft;
-    // The stream kernel stores its partials with the default policy; the
-    // combine loads them the same way.
-    const void *combine = (const void *)&attention_combine<D, _Float16, kOutGated, float, false, true>;
+    // The stream kernel stores its partials with the default policy, the
+    // ring kernel non-temporally; the combine loads them the same way.
+    const void *combine = ring ? (const void *)&attention_combine<D, _Float16, kOutGated, float, true, false>
+                               : (const void *)&attention_combine<D, _Float16, kOutGated, float, false, true>;
     void *combine_args[] = {&c};
     check(hipLaunchKernel(combine, dim3(plan.rows, kv_heads), dim3(kWaves * kWave), combine_args, 0, stream));
 }

@@ -22,12 +22,14 @@ enum class SplitKind { Stream, Ring };
 // for a split kernel, its partial rows (the combine then writes the output).
 enum { kOutSame = 0, kOutF32 = 1, kOutGated = 2, kOutPartials = 3 };
 
-// The new token of a fused decode (the reference's attn_prepare inputs for
-// the 24/4/256 model).  The split kernel prepares the query and attends to
-// the cached keys; its first split's workgroups also prepare the new key and
-// value, append them to the pages and publish the prepared query rows in
-// q_prep.  The combine kernel adds the new key from the pages and q_prep.
-// (The kernels take up to two tokens, token t seeing new keys 0..t.)
+// The new tokens of a fused call (the reference's attn_prepare inputs for
+// the 24/4/256 model), token t seeing new keys 0..t.  The split kernel
+// prepares the query and attends to the cached keys; its first split's
+// workgroups also prepare the new keys and values and append them to the
+// pages.  One or two tokens (the stream kernel): the first split publishes
+// the prepared query rows in q_prep, and the combine adds the new keys from
+// the pages and q_prep.  3..8 tokens (the ring kernel): the first split
+// attends to the new keys itself.
 struct FusedToken {
     const float *q_gate;   // [tokens][q_heads][2D]: q, then the gate
     const float *key;      // [tokens][kv_heads][D]
@@ -65,6 +67,10 @@ struct SplitArgs {
 // combinations.  It takes kRingThreads threads and SplitArgs.
 constexpr int kRingThreads = 512;
 const void *ring_kernel(int D, int nqt, Dtype dtype, bool precise, int out_mode);
+// The fused verification's ring instance (24/4/256, fp16 pages, 2 or 3
+// query tiles): the query prepared in the kernel from SplitArgs::tok, every
+// row over the cached keys 0 .. position only, fp32 partials.
+const void *ring_prep_kernel(int nqt);
 
 // The split-K decomposition chosen for one launch of the partial kernel.
 struct SplitPlan {
@@ -130,19 +136,20 @@ void launch_combine(const Shape &s, const SplitPlan &plan, Dtype dtype,
                     const void *workspace, void *out, bool out_f32, const float *gate,
                     hipStream_t stream);
 
-// Fused decode of tok.tokens new tokens (up to kMaxFusedSplitTokens) at
-// tok.position >= 1 (24/4/256, fp16 pages) in two launches: the split kernel
-// prepares the query itself, attends to the cached keys 0 .. position-1 and
-// (first split) appends the new key and value; the combine adds the new key
-// and applies the gate.  No prepare launch.  The workspace holds the split's
-// partials and the prepared query rows (fused_tokens_workspace_bytes).
+// Fused decode or verification of tok.tokens new tokens (up to
+// kMaxFusedSplitTokens) at tok.position >= 1 (24/4/256, fp16 pages) in two
+// launches: the split kernel prepares the query itself (RMSNorm, gamma,
+// RoPE, hi + lo parts) while its first pages are in flight and attends to
+// the cached keys 0 .. position-1, its first split appending the new keys
+// and values; the combine merges and applies the gate.  No prepare launch.
+// One or two tokens run the stream kernel, and the combine adds the new
+// keys (from the pages and the published query rows); 3..8 tokens run the
+// ring kernel, whose first split attends to the new keys as one more block.
+// The workspace holds the split's partials and the prepared query rows
+// (fused_tokens_workspace_bytes).
 void launch_fused_tokens(const FusedToken &tok, int capacity, void *workspace, float *out, hipStream_t stream);
 size_t fused_tokens_workspace_bytes(int tokens, int position);
-// One token (decode).  Verification batches of 2..8 tokens take the
-// prepare kernel instead: for 8 tokens at 16K, preparing 48 query rows in
-// the ring kernel's prologue and the new keys in the combine cost more than
-// the launch they save (28.3-32.2 against 28.8 us per layer).
-constexpr int kMaxFusedSplitTokens = 1;
+constexpr int kMaxFusedSplitTokens = 8;
 
 // The fused k_attention of up to kShortMaxTokens new tokens when position +
 // tokens <= kShortFusedKeys (short.hip): one launch, one workgroup per (token,

@@ -16,6 +16,17 @@ __device__ __forceinline__ void wait_vmcnt() {
     __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | (7 << 4) | (15 << 8));
 }
 
+// A 16-byte global load that the compiler does not track: the kernel's own
+// vmcnt waits cover it.  (Loads complete in order, so an untracked load never
+// weakens a wait the compiler places for its own loads.)  Every use of the
+// result must depend on an asm statement placed after that wait (pin() of
+// the value, or an LDS wait whose result the use also takes), so that the
+// compiler cannot move the use above the wait.
+template <typename V>
+__device__ __forceinline__ void global_load16(V &v, const void *p) {
+    asm volatile("global_load_dwordx4 %0, %1, off" : "=v"(v) : "v"(p) : "memory");
+}
+
 // LDS byte address of a __shared__ object.
 __device__ __forceinline__ uint32_t lds_addr(const void *p) {
     return (uint32_t)(uintptr_t)(__attribute__((address_space(3))) const void *)p;

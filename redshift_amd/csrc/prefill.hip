@@ -97,13 +97,6 @@ __device__ __forceinline__ float unpack_hi(uint32_t w, _Float16) {
 
 constexpr float kLazy = 8.f;
 
-// A 16-byte global load that the compiler does not track: the kernel's own
-// vmcnt waits cover it.  (Loads complete in order, so an untracked load never
-// weakens a wait the compiler places for its own loads.)
-template <typename V>
-__device__ __forceinline__ void global_load16(V &v, const void *p) {
-    asm volatile("global_load_dwordx4 %0, %1, off" : "=v"(v) : "v"(p) : "memory");
-}
 
 struct PrefillArgs {
     const void *q;

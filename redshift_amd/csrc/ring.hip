@@ -21,8 +21,28 @@
 // kernels, so attention_combine merges them.  A precise instance (QSPLIT)
 // takes an fp32 query as fp16 hi + lo parts (the fused path): S^T gets one
 // more MFMA per fragment and P is split into hi + lo parts as well.
+//
+// PREP (the fused verification of 3..8 new tokens): the precise query is
+// not read from q / q_lo but prepared here from a.tok while the first pages
+// are in flight.  Wave w prepares the six query rows of new token w with
+// the prepare kernel's functions and layout (so the same bits): untracked
+// loads requested before the pages, RMSNorm, gamma and RoPE, the fp32 rows
+// then written to a query area in LDS, from which every computing wave
+// reads its tile's fragments and splits them into hi + lo fp16 parts.  The
+// ring has three buffers here (the query area takes the fourth's LDS).
+// Every row sees the cached keys 0 .. a.position; the first split's wave w
+// also prepares new key w in the prologue and writes it into a block of 16
+// keys in the free ring buffer, which the first key half of every tile
+// attends to (row t seeing new keys 0..t) before page 0.  So the partials
+// hold every key, and the plain gated combine merges them.  The first
+// split appends key and value w to the pages after its partials: stores
+// issued among the page loads would share the vector-memory counter that
+// the ring's waits count page loads on.  (Appending in the combine instead,
+// by one workgroup per KV head, measured slower: the combine's critical
+// path grew by more than the split kernel's.)
 #include "kernels.hpp"
 #include "lds.hpp"
+#include "prep.hpp"
 
 #include <cmath>
 #include <cstdint>
@@ -67,10 +87,24 @@ constexpr int kRingBuffers = 4;   // NBUF-1 pages in flight while one is consume
 constexpr int kStreamLoad = 2;
 constexpr float kLazy = 8.f;   // lazy row-max threshold, log2 units
 
+// A 4-byte global load that the compiler does not track (like
+// global_load16), and a 2- or 4-byte LDS write that it does not order against the
+// ring's direct loads (like lds_read); both are awaited explicitly.
+__device__ __forceinline__ void global_load4(float &v, const float *p) {
+    asm volatile("global_load_dword %0, %1, off" : "=v"(v) : "v"(p) : "memory");
+}
+__device__ __forceinline__ void lds_write4(uint32_t addr, float v) {
+    asm volatile("ds_write_b32 %0, %1" : : "v"(addr), "v"(v) : "memory");
+}
+__device__ __forceinline__ void lds_write2(uint32_t addr, _Float16 v) {
+    const unsigned u = __builtin_bit_cast(unsigned short, v);
+    asm volatile("ds_write_b16 %0, %1" : : "v"(addr), "v"(u) : "memory");
+}
+
 // OUT: kOutPartials stores the split's partial rows; a direct output
 // (kOutSame or kOutF32: one split per KV head) stores the final rows
 // instead, and no combine runs.
-template <int D, int NQT, bool PSPLIT, typename KV, bool QSPLIT = false, int OUT = kOutPartials>
+template <int D, int NQT, bool PSPLIT, typename KV, bool QSPLIT = false, int OUT = kOutPartials, bool PREP = false>
 __global__ __launch_bounds__(kRingWaves * kWave, 1)
 void attention_ring(SplitArgs a) {
     using V8 = typename Vec8<KV>::type;
@@ -83,10 +117,18 @@ void attention_ring(SplitArgs a) {
     constexpr int CPW = CHUNKS / kRingWaves;       // chunks (loads) per wave per page
     static_assert(CHUNKS % kRingWaves == 0, "chunks divide over the waves");
     static_assert(NQT >= 1 && NQT <= 4, "four query tiles at most");
-    // The ring: NBUF buffers of one [K page | V page] each (all 160 KiB of
-    // LDS at D=256).
-    constexpr int NBUF = kRingBuffers;
+    static_assert(!PREP || (D == kModelHeadDim && QSPLIT && PSPLIT && OUT == kOutPartials &&
+                            std::is_same<KV, _Float16>::value),
+                  "the prepared query is the fp32 query of the 256-dim fp16 model, as hi + lo parts");
+    // The ring: NBUF buffers of one [K page | V page] each (128 KiB of LDS
+    // at D=256; PREP: three buffers and the query area, 145 KiB).
+    constexpr int NBUF = PREP ? 3 : kRingBuffers;
     __shared__ __attribute__((aligned(16))) KV ring[NBUF][2 * PAGE];
+    // PREP: the prepared fp32 query rows, row r at r * QSTRIDE floats (the
+    // padding keeps the row-wise writes and the fragment reads free of bank
+    // conflicts).
+    constexpr int QSTRIDE = D + 4;
+    __shared__ __attribute__((aligned(16))) float qarea[PREP ? kMaxRows * QSTRIDE : 4];
     KV *const ring0 = ring[0], *const ring1 = ring[1], *const ring2 = ring[2];
 
     const int lane = threadIdx.x & 63, w = threadIdx.x >> 6, g = lane >> 4;
@@ -122,10 +164,11 @@ void attention_ring(SplitArgs a) {
     // is then requested after the fragments have moved to registers.
     const int row = min(16 * qt + (lane & 15), a.rows - 1);
     const int t = row / a.group;
-    const int limit = a.position + t;                            // last key of this row
-    const int tile_limit = a.position + min(16 * qt, a.rows - 1) / a.group;
+    // Last key of this row (PREP: the last cached key, for every row).
+    const int limit = a.position + (PREP ? 0 : t);
+    const int tile_limit = a.position + (PREP ? 0 : min(16 * qt, a.rows - 1) / a.group);
     static_assert(4 * KS * kWave * 8 <= 2 * PAGE, "query fragments fit one ring buffer");
-    if (computes && (kt == 0 || QSPLIT)) {
+    if (!PREP && computes && (kt == 0 || QSPLIT)) {
         const KV *src = static_cast<const KV *>(kt == 0 ? a.q : a.q_lo) +
                         ((size_t)t * a.q_heads + (size_t)h * a.group + (row - t * a.group)) * D + 8 * g;
         KV *dst = kt == 0 ? ring[NBUF - 1] : ring[NBUF - 2];
@@ -142,7 +185,10 @@ void attention_ring(SplitArgs a) {
     for (int dt = 0; dt < DT; ++dt) acc[dt] = f32x4{0.f, 0.f, 0.f, 0.f};
     float m = -INFINITY, l = 0.f;
 
-    auto compute = [&](int p, const KV *cur) __attribute__((always_inline)) {
+    // attend: the wave's 16 keys of the page in `cur` whose first key is
+    // k_first; keys past lim (a row's last key; tlim: the tile's smallest
+    // lim) are masked, and with `tail` the V slots past the last key zeroed.
+    auto attend = [&](int k_first, const KV *cur, int lim, int tlim, bool tail) __attribute__((always_inline)) {
         const uint32_t kbase = lds_addr(cur) + lane * 16 + kt * (16 * D * 2);
         const uint32_t vbase = lds_addr(cur) + PAGE * 2 + lane * 16 + kt * 8;
         // S^T and the softmax run at raised wave priority, P.V at the
@@ -182,15 +228,15 @@ void attention_ring(SplitArgs a) {
         // Online softmax over the wave's 16 keys of the page (lane: keys
         // 16kt + 4g + r for row l%16); keys past the row's limit (later
         // candidates, or past the last key) are masked.
-        const int key0 = p * 32 + 16 * kt + 4 * g;
+        const int key0 = k_first + 16 * kt + 4 * g;
         float x[4];
 #pragma unroll
         for (int r = 0; r < 4; ++r) x[r] = (s0[r] + s1[r]) * a.scale_log2;
-        if (p * 32 + 31 > tile_limit) {
+        if (k_first + 31 > tlim) {
             keep_branch();
 #pragma unroll
             for (int r = 0; r < 4; ++r)
-                if (key0 + r > limit) x[r] = -INFINITY;
+                if (key0 + r > lim) x[r] = -INFINITY;
         }
         const float bm = row_group_max(fmaxf(fmaxf(x[0], x[1]), fmaxf(x[2], x[3])));
         float alpha = 1.f;
@@ -222,7 +268,7 @@ void attention_ring(SplitArgs a) {
         __builtin_amdgcn_s_setprio(0);
         lds_wait<VB - 1>(vf[0]);
         static_for<VB, DT>(read_v);
-        if (p * 32 + 32 > a.n_keys) {
+        if (tail) {
             // Last page: V slots past the last key are zeroed (stale pages
             // may hold anything, and 0 * NaN is NaN).
             keep_branch();
@@ -241,6 +287,10 @@ void attention_ring(SplitArgs a) {
             acc[dt] = mfma(vf[dt], ph, acc[dt]);
             if constexpr (PSPLIT) acc[dt] = mfma(vf[dt], pl, acc[dt]);
         });
+    };
+
+    auto compute = [&](int p, const KV *cur) __attribute__((always_inline)) {
+        attend(p * 32, cur, limit, tile_limit, p * 32 + 32 > a.n_keys);
     };
 
     // Before step i's barrier, pages i+1 .. i+NBUF-2 may stay in flight
@@ -262,7 +312,136 @@ void attention_ring(SplitArgs a) {
         if (computes) compute(p0 + i, ring[B]);
     };
 
-    if (n > 0) {
+    // PREP, first split: new key w prepared in the prologue (fp16, as the
+    // cache holds it), attended to as a block of its own and appended after
+    // the partials.
+    [[maybe_unused]] _Float16 new_k[4] = {}, new_v[4] = {};
+    if constexpr (PREP) {
+      if (n > 0) {
+        constexpr int G = kModelQHeads / kModelKvHeads;
+        const bool preps = w < a.tok.tokens;                  // wave-uniform
+        float xq[G][4] = {}, gq[4] = {};
+        NewKeyRow nk = {};
+        if (preps) {
+            const float *src = a.tok.q_gate + ((size_t)w * a.q_heads + (size_t)h * G) * 2 * D + lane;
+#pragma unroll
+            for (int r = 0; r < G; ++r)
+#pragma unroll
+                for (int i = 0; i < 4; ++i) global_load4(xq[r][i], src + r * 2 * D + 64 * i);
+#pragma unroll
+            for (int i = 0; i < 4; ++i) global_load4(gq[i], a.tok.q_norm + 64 * i + lane);
+            if (split == 0) {
+                const size_t krow = ((size_t)w * a.kv_heads + h) * D + lane;
+#pragma unroll
+                for (int i = 0; i < 4; ++i) {
+                    global_load4(nk.k[0][i], a.tok.key + krow + 64 * i);
+                    global_load4(nk.g[i], a.tok.k_norm + 64 * i + lane);
+                    global_load4(nk.v[i], a.tok.value + krow + 64 * i);
+                }
+            }
+        }
+        static_for<0, NBUF - 1>([&](auto k) {
+            if (decltype(k)::value < n) stage(p0 + decltype(k)::value, ring[decltype(k)::value]);
+        });
+        if (preps) {
+            float c = 1.f, sn = 0.f;
+            if (lane < 32) rope_cos_sin(a.tok.position + w, rope_freq(lane), c, sn);
+            // The inputs were requested before this wave's pages.
+            const int pages = min(n, NBUF - 1);
+            static_for<1, NBUF>([&](auto k) {
+                if (pages == decltype(k)::value) wait_vmcnt<decltype(k)::value * CPW>();
+            });
+#pragma unroll
+            for (int r = 0; r < G; ++r) pin(xq[r][0], xq[r][1], xq[r][2], xq[r][3]);
+            pin(gq[0], gq[1], gq[2], gq[3]);
+            const float cr[G] = {c, c, c, c, c, c}, sr[G] = {sn, sn, sn, sn, sn, sn};
+            norm_rope_rows<G>(xq, gq, cr, sr, a.tok.epsilon, lane);
+            const uint32_t qw = lds_addr(qarea) + ((G * w) * QSTRIDE + lane) * 4;
+#pragma unroll
+            for (int r = 0; r < G; ++r)
+#pragma unroll
+                for (int i = 0; i < 4; ++i) lds_write4(qw + (r * QSTRIDE + 64 * i) * 4, xq[r][i]);
+            if (split == 0) {
+                pin(nk.k[0][0], nk.k[0][1], nk.k[0][2], nk.k[0][3], nk.g[0], nk.g[1], nk.g[2], nk.g[3],
+                    nk.v[0], nk.v[1], nk.v[2], nk.v[3]);
+                const float kc[1] = {c}, ksn[1] = {sn};
+                norm_rope_rows<1>(nk.k, nk.g, kc, ksn, a.tok.epsilon, lane);
+#pragma unroll
+                for (int i = 0; i < 4; ++i) {
+                    new_k[i] = cache_half(nk.k[0][i]);
+                    new_v[i] = cache_half(nk.v[i]);
+                }
+                // Key w of the new-key block in ring buffer NBUF-1 (free
+                // until page NBUF-1 is requested after step 0's barrier).
+                const uint32_t nb = lds_addr(ring[NBUF - 1]);
+#pragma unroll
+                for (int i = 0; i < 4; ++i) {
+                    lds_write2(nb + k_page_offset(w, 64 * i + lane, D) * 2, new_k[i]);
+                    lds_write2(nb + (PAGE + v_page_offset(w, 64 * i + lane, D)) * 2, new_v[i]);
+                }
+            }
+        }
+        if (split == 0) {
+            // The block's other V slots of keys 0..15 (the first key half,
+            // the only one that attends to it) are zero: its masked keys'
+            // P of 0 must not meet stale LDS bits.  Their K slots may hold
+            // anything: those scores are masked.
+            const uint32_t nv = lds_addr(ring[NBUF - 1]) + PAGE * 2;
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                lds_write2(nv + v_page_offset(w + 8, 64 * i + lane, D) * 2, (_Float16)0.f);
+                if (!preps) lds_write2(nv + v_page_offset(w, 64 * i + lane, D) * 2, (_Float16)0.f);
+            }
+        }
+        asm volatile("s_waitcnt lgkmcnt(0)" : : : "memory");
+        ring_barrier();
+        if (computes) {
+            // The tile's fp32 fragments (k-step ks: dims 32ks + 8g .. +7 of
+            // row `row`, two float4), split into hi + lo parts, in two rounds
+            // of eight LDS reads.
+            const uint32_t qb = lds_addr(qarea) + (row * QSTRIDE + 8 * g) * 4;
+            static_for<0, 2>([&](auto half_) {
+                constexpr int K0 = decltype(half_)::value * KS / 2;
+                f32x4 fa[KS / 2][2];
+                static_for<0, KS / 2>([&](auto k_) {
+                    constexpr int k = decltype(k_)::value;
+                    lds_read<(K0 + k) * 128>(fa[k][0], qb);
+                    lds_read<(K0 + k) * 128 + 16>(fa[k][1], qb);
+                });
+                static_for<0, KS / 2>([&](auto k_) {
+                    constexpr int k = decltype(k_)::value;
+                    lds_wait<2 * (KS / 2 - 1 - k)>(fa[k][0], fa[k][1]);
+#pragma unroll
+                    for (int e = 0; e < 8; ++e) {
+                        const float x = fa[k][e / 4][e % 4];
+                        const _Float16 hi = (_Float16)x;
+                        qf[K0 + k][e] = hi;
+                        qlo[K0 + k][e] = (_Float16)(x - (float)hi);
+                    }
+                });
+            });
+            // First split: the new keys n_keys + j, row t seeing j <= t.
+            if (split == 0 && kt == 0)
+                attend(a.n_keys, ring[NBUF - 1], a.n_keys + t, a.n_keys + min(16 * qt, a.rows - 1) / a.group, false);
+        }
+        // Page 0 has landed (pages 1 .. NBUF-2 may stay in flight).
+        {
+            const int ahead = min(NBUF - 2, n - 1);
+            static_for<0, NBUF - 1>([&](auto k) {
+                if (ahead == decltype(k)::value) wait_vmcnt<decltype(k)::value * CPW>();
+            });
+        }
+        ring_barrier();
+        if (NBUF - 1 < n) stage(p0 + NBUF - 1, ring[NBUF - 1]);
+        if (computes) compute(p0, ring[0]);
+        for (int i = 1; i < n; i += NBUF) {
+            static_for<0, NBUF>([&](auto k) {
+                constexpr int B = (decltype(k)::value + 1) % NBUF;
+                if (i + decltype(k)::value < n) step(i + decltype(k)::value, std::integral_constant<int, B>{});
+            });
+        }
+      }
+    } else if (n > 0) {
         // Pages 0 .. NBUF-2 (NBUF-3 with a precise query, whose lo parts
         // occupy buffer NBUF-2) are requested after the query fragments.
         constexpr int FIRST = QSPLIT ? NBUF - 2 : NBUF - 1;
@@ -393,6 +572,21 @@ void attention_ring(SplitArgs a) {
             }
         }
     }
+    if constexpr (PREP) {
+        // First split: new key and value w appended to the pages.  Keys past
+        // n_keys-1 are masked in every split (scores) and their V slots
+        // zeroed, so a split that streams the page receiving them reads
+        // either bits harmlessly.
+        if (split == 0 && n > 0 && w < a.tok.tokens) {
+            _Float16 *kp = static_cast<_Float16 *>(a.tok.k_pages) + (size_t)h * a.tok.head_stride;
+            _Float16 *vp = static_cast<_Float16 *>(a.tok.v_pages) + (size_t)h * a.tok.head_stride;
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                kp[k_page_offset(a.tok.position + w, 64 * i + lane, D)] = new_k[i];
+                vp[v_page_offset(a.tok.position + w, 64 * i + lane, D)] = new_v[i];
+            }
+        }
+    }
 }
 
 // Instances: raw fp16 multiplies V by a 16-bit P, raw bf16 by hi + lo P
@@ -433,6 +627,15 @@ const void *pick_tiles(int nqt, Dtype dtype, bool precise, int out_mode) {
 const void *ring_kernel(int D, int nqt, Dtype dtype, bool precise, int out_mode) {
     if (D == 256) return pick_tiles<256>(nqt, dtype, precise, out_mode);
     if (D == 128) return pick_tiles<128>(nqt, dtype, precise, out_mode);
+    return nullptr;
+}
+
+const void *ring_prep_kernel(int nqt) {
+    constexpr int D = kModelHeadDim;
+    switch (nqt) {
+        case 2: return (const void *)&attention_ring<D, 2, true, _Float16, true, kOutPartials, true>;
+        case 3: return (const void *)&attention_ring<D, 3, true, _Float16, true, kOutPartials, true>;
+    }
     return nullptr;
 }
 

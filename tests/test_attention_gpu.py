@@ -324,13 +324,16 @@ def test_fused_device_path_matches_oracle(gpu):
 
 
 @pytest.mark.parametrize('batch,position', [(5, 5000), (8, 20000), (3, 40), (2, 100), (4, 31), (6, 33),
-                                            (7, 1)])
+                                            (7, 1), (2, 257), (2, 3000), (3, 300), (4, 1000), (6, 4097),
+                                            (7, 9000)])
 def test_fused_verify_matches_oracle(gpu, batch, position):
-    """Fused verification batches of 2-8 tokens (prepare kernel, then the
-    precise split kernels: fp32 query as hi + lo parts) at split lengths of
-    1 to ~11 pages, a first cached page that is full (31 + 1) or holds one
-    key, on the reference's sine-wave fixture and tolerances, with the
-    appended cache rows."""
+    """Fused verification batches of 2-8 tokens on the reference's sine-wave
+    fixture and tolerances, with the appended cache rows: on short contexts
+    the one-launch kernel (a first cached page that is full, 31 + 1, or
+    holds one key); past 256 keys the split kernels preparing the fp32 query
+    in their prologue (two tokens: the stream kernel; 3-8: the ring kernel,
+    whose first split attends to the new keys), at split lengths of 1 to
+    ~11 pages."""
     torch = gpu
     c = kat.sine_wave_case(batch=batch, position=position)
     expected = ref.fused_attention(c['key_cache'], c['value_cache'], c['q_gate'], c['key'], c['value'],
@@ -670,3 +673,48 @@ def test_fused_random_shapes_against_oracle(gpu, batch, position, seed):
     assert_close(out.cpu().numpy(), expected[0], 3e-4)
     assert_close(kcache.float().cpu().numpy(), expected[1], 2e-3)
     assert_close(vcache.float().cpu().numpy(), expected[2], 0)
+
+
+@pytest.mark.parametrize('batch,position', [(1, 16000), (2, 3000), (5, 300), (8, 16000)])
+def test_fused_graph_replay_matches_eager(gpu, batch, position):
+    """The fused entry (prepare in the split kernels' prologue, the new keys
+    appended by the kernels) enqueues kernels only, so it can be captured in
+    a HIP graph: every replay, with eager calls reusing the workspace and
+    synchronisations in between, reproduces the eager output and caches bit
+    for bit."""
+    torch = gpu
+    rng = np.random.default_rng(position + batch)
+    kc = (rng.standard_normal((position, 4, 256)) * .5).astype(np.float16)
+    vc = (rng.standard_normal((position, 4, 256)) * .5).astype(np.float16)
+    cache = A.PagedKV(4, 256, A.round_capacity(position + batch), torch.float16)
+    cache.k.fill_(float('nan'))
+    cache.v.fill_(float('nan'))
+    cache.pack(torch.from_numpy(kc).cuda(), torch.from_numpy(vc).cuda())
+    dev = [torch.from_numpy(x).cuda() for x in (
+        rng.standard_normal((batch, 24, 512)).astype(np.float32),
+        rng.standard_normal((batch, 4, 256)).astype(np.float32),
+        rng.standard_normal((batch, 4, 256)).astype(np.float32),
+        (1 + .25 * rng.uniform(-1, 1, 256)).astype(np.float32),
+        (1 + .25 * rng.uniform(-1, 1, 256)).astype(np.float32))]
+    ws = A.workspace(A.fused_workspace_bytes(batch, position))
+    eager = A.attention_fused(*dev, cache, position, 1e-6, ws=ws).clone()
+    k0, v0 = cache.k.clone(), cache.v.clone()
+    out = torch.empty_like(eager)
+    graph = torch.cuda.CUDAGraph()
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        A.attention_fused(*dev, cache, position, 1e-6, out=out, ws=ws)
+        torch.cuda.synchronize()
+        with torch.cuda.graph(graph, stream=side):
+            A.attention_fused(*dev, cache, position, 1e-6, out=out, ws=ws)
+    torch.cuda.current_stream().wait_stream(side)
+    for _ in range(3):
+        out.zero_()
+        A.attention_fused(*dev, cache, position, 1e-6, ws=ws)   # eager work reusing the workspace
+        torch.cuda.synchronize()
+        graph.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(out, eager)
+        assert torch.equal(cache.k.view(torch.int16), k0.view(torch.int16))   # bits: unused slots hold NaN
+        assert torch.equal(cache.v.view(torch.int16), v0.view(torch.int16))

@@ -168,9 +168,15 @@ def test_device_entry_points_validate_before_touching_the_device(lib):
     assert lib.qv_attention_fused(*([p] * 8), 100, 139200, 139264, 1e-6, p, ws, None) == -1
     assert b'139264' in lib.qv_error()
     # Every device buffer of the fused entry is 16-byte aligned (the prefill
-    # chunk stores 16-byte vectors to out).
+    # chunk stores 16-byte vectors to out; the verification kernels read the
+    # query, the norm weights and the new keys and values 16 bytes at a time).
     assert lib.qv_attention_fused(ct.c_void_p(4100), *([p] * 7), 100, 0, 128, 1e-6, p, ws, None) == -1
     assert b'aligned' in lib.qv_error()
+    for i in range(3, 8):   # q_gate, key, value, q_norm, k_norm
+        args = [p] * 8
+        args[i] = ct.c_void_p(4100)
+        assert lib.qv_attention_fused(*args, 8, 1000, 1024, 1e-6, p, ws, None) == -1
+        assert b'aligned' in lib.qv_error()
 
 
 def test_front_end_rejects_mismatched_tensors(lib):
