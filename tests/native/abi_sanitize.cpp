@@ -458,8 +458,9 @@ void device_calls(hipStream_t stream) {
             EXPECT(all_finite(fetch(dout.p, n, QV_F32)));
         }
     }
-    // The fused entry: short context, decode, verification, prefill chunk.
-    const int fused_cases[][2] = {{3, 10}, {1, 500}, {8, 1000}, {20, 64}};
+    // The fused entry: short context, decode, verification (two tokens on
+    // the stream kernel, 3-8 on the ring kernel), prefill chunk.
+    const int fused_cases[][2] = {{3, 10}, {1, 500}, {2, 700}, {5, 300}, {8, 1000}, {20, 64}};
     std::vector<float> qn(D), kn(D);
     for (int i = 0; i < D; ++i) qn[i] = 1.f + 0.01f * i, kn[i] = 1.f - 0.001f * i;
     Dev<float> dqn(D), dkn(D);
