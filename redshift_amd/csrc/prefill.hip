@@ -669,9 +669,11 @@ struct CombinePrefillArgs {
     const float *gate;
     int q_heads, group, rows, kv_heads, splits;
 };
-constexpr int kCombineBatch = 8, kCombineThreads = 256;
+// Up to 2 kCombineBatch splits take rounds of 8 loads; up to
+// kCombineWideBatch one round of all of them (more registers per wave).
+constexpr int kCombineBatch = 8, kCombineWideBatch = 24, kCombineThreads = 256;
 
-template <int D, typename KV, int MODE>
+template <int D, typename KV, int MODE, int kCombineBatch>
 __global__ __launch_bounds__(kCombineThreads)
 void combine_prefill(CombinePrefillArgs c) {
     constexpr int DV = D / kWave;
@@ -733,11 +735,17 @@ void combine_prefill(CombinePrefillArgs c) {
 }
 
 template <int D>
-const void *combine_prefill_kernel(Dtype dtype, bool out_f32, bool gated) {
-    if (gated) return (const void *)&combine_prefill<D, float, kOutGated>;
-    if (out_f32) return (const void *)&combine_prefill<D, float, kOutF32>;
-    return dtype == Dtype::BF16 ? (const void *)&combine_prefill<D, __bf16, kOutSame>
-                                : (const void *)&combine_prefill<D, _Float16, kOutSame>;
+const void *combine_prefill_kernel(Dtype dtype, bool out_f32, bool gated, bool wide) {
+    if (wide) {
+        if (gated) return (const void *)&combine_prefill<D, float, kOutGated, kCombineWideBatch>;
+        if (out_f32) return (const void *)&combine_prefill<D, float, kOutF32, kCombineWideBatch>;
+        return dtype == Dtype::BF16 ? (const void *)&combine_prefill<D, __bf16, kOutSame, kCombineWideBatch>
+                                    : (const void *)&combine_prefill<D, _Float16, kOutSame, kCombineWideBatch>;
+    }
+    if (gated) return (const void *)&combine_prefill<D, float, kOutGated, kCombineBatch>;
+    if (out_f32) return (const void *)&combine_prefill<D, float, kOutF32, kCombineBatch>;
+    return dtype == Dtype::BF16 ? (const void *)&combine_prefill<D, __bf16, kOutSame, kCombineBatch>
+                                : (const void *)&combine_prefill<D, _Float16, kOutSame, kCombineBatch>;
 }
 
 }  // namespace
@@ -779,14 +787,18 @@ void launch_prefill(const Shape &s, Dtype dtype, bool precise, float scale, cons
     const long long grid = (long long)plan.row_wgs * s.kv_heads * plan.splits;
     require(grid * threads < (1LL << 32), "prefill launch exceeds 2^32 work-items");
     void *args[] = {&a};
-    // The combine of split calls.  Up to 2 kCombineBatch splits (many rows):
-    // combine_prefill, a wave per row.  More splits (then at most CUs / 16
-    // row workgroups, few rows): attention_combine, whose four waves per row
-    // request up to 64 splits in one round (62 splits of 96 rows: 27.5 us
-    // per call against 31.1 us with combine_prefill's batches in turn).
+    // The combine of split calls.  Up to kCombineWideBatch splits (many
+    // rows): combine_prefill, a wave per row, in rounds of 8 splits up to
+    // 16 and in one round of up to 24 beyond (the fused 64-token chunk at
+    // 16,384, 21 splits: 66.3 against 68.1 us per layer with
+    // attention_combine; the wide batch gave nothing at 9-16 splits).
+    // More splits (then few row workgroups, few rows): attention_combine,
+    // whose four waves per row request up to 64 splits in one round (62
+    // splits of 96 rows: 27.5 us per call against 31.1 us with
+    // combine_prefill's batches in turn).
     auto combine = [&] {
         if (plan.splits == 1) return;
-        if (plan.splits > 2 * kCombineBatch) {
+        if (plan.splits > kCombineWideBatch) {
             SplitPlan cp = {};
             cp.kind = SplitKind::Stream;   // fp32 partial rows, default-policy stores
             cp.rows = a.rows;
@@ -807,8 +819,9 @@ void launch_prefill(const Shape &s, Dtype dtype, bool precise, float scale, cons
         const long long waves = (long long)a.rows * s.kv_heads;
         const long long blocks = (waves + kCombineThreads / kWave - 1) / (kCombineThreads / kWave);
         require(blocks < (1LL << 31), "prefill combine exceeds the grid");
-        const void *kernel = d256 ? combine_prefill_kernel<256>(dtype, out_f32, gate != nullptr)
-                                  : combine_prefill_kernel<128>(dtype, out_f32, gate != nullptr);
+        const bool wide = plan.splits > 2 * kCombineBatch;
+        const void *kernel = d256 ? combine_prefill_kernel<256>(dtype, out_f32, gate != nullptr, wide)
+                                  : combine_prefill_kernel<128>(dtype, out_f32, gate != nullptr, wide);
         void *cargs[] = {&c};
         check(hipLaunchKernel(kernel, dim3((unsigned)blocks), dim3(kCombineThreads), cargs, 0, stream));
     };

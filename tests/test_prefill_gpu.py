@@ -152,6 +152,8 @@ def test_random_prefill_shapes(gpu, q_heads, kv_heads, head_dim, T, position, dt
     (1, 1, 128, 2400, 0, 'f16'),       # 9 splits; a workgroup's early rows see no key of its last run
     (8, 1, 256, 1100, 0, 'bf16'),      # 4 splits; the early workgroups' later runs are empty
     (24, 4, 256, 300, 300, 'f16'),     # 19 pages: not split
+    (24, 4, 256, 96, 16000, 'f16'),    # 12 row workgroups: 21 splits, one combine round of 24
+    (24, 4, 256, 70, 9000, 'bf16'),    # 12 row workgroups: 21 splits, V through the fp16 copy
 ])
 def test_split_prefill_against_oracle(gpu, q_heads, kv_heads, head_dim, T, position, dtype):
     """Calls with too few row workgroups to fill the device split their keys
