@@ -325,7 +325,7 @@ def test_fused_device_path_matches_oracle(gpu):
 
 @pytest.mark.parametrize('batch,position', [(5, 5000), (8, 20000), (3, 40), (2, 100), (4, 31), (6, 33),
                                             (7, 1), (2, 257), (2, 3000), (3, 300), (4, 1000), (6, 4097),
-                                            (7, 9000)])
+                                            (7, 9000), (8, 249), (3, 254), (2, 255)])
 def test_fused_verify_matches_oracle(gpu, batch, position):
     """Fused verification batches of 2-8 tokens on the reference's sine-wave
     fixture and tolerances, with the appended cache rows: on short contexts
