@@ -628,6 +628,26 @@ def test_random_shapes_against_oracle(gpu, q_heads, kv_heads, head_dim, T, posit
     assert_parity(gpu_attention(w, q, k, v, gpu, fill_nan=True, out_dtype=gpu.float32), want)
 
 
+@pytest.mark.parametrize('q_heads,kv_heads,head_dim,T,position,dtype', [
+    (48, 1, 128, 1, 1000, 'f16'),     # 48 rows, the group limit: the ring kernel's three tiles
+    (16, 1, 256, 3, 500, 'bf16'),     # 48 rows from three tokens
+    (24, 1, 256, 1, 3000, 'f16'),     # 24 rows: two tiles, one token
+    (12, 1, 128, 4, 100, 'bf16'),     # a direct (one-split) plan
+    (32, 1, 128, 2, 2000, 'f16'),     # 64 rows: the prefill kernel, a group spanning its tiles
+    (48, 2, 256, 5, 300, 'f16'),      # 240 rows per KV head
+    (96, 2, 256, 1, 6000, 'bf16'),    # 48 rows per KV head, two KV heads
+])
+def test_large_groups_against_oracle(gpu, q_heads, kv_heads, head_dim, T, position, dtype):
+    """Query groups of 12-48 heads per KV head (up to the documented limit of
+    48), on both sides of the 48-row split between the split-K kernels and the
+    prefill kernel, float32 output, pages past the last key filled with NaN,
+    against the oracle to the full bounds."""
+    w = Workload('groups', q_heads, kv_heads, head_dim, T, position, 1 / head_dim ** .5, dtype, 31, 1.0, 0.5)
+    q, k, v, _ = make_inputs(w)
+    want = ref.gqa_attention(to_float(q, dtype), to_float(k, dtype), to_float(v, dtype), position, w.scale)
+    assert_parity(gpu_attention(w, q, k, v, gpu, fill_nan=True, out_dtype=gpu.float32), want)
+
+
 def random_fused_shapes(n, seed=77):
     """Seeded (batch, position) pairs over every route of the fused entry:
     one launch on short contexts, decode, verification batches, prefill
