@@ -89,9 +89,13 @@ def test_attention_cpu_prefix_causality_and_chunking(lib, gpu):
     np.testing.assert_array_equal(vc.view(np.uint16), seq_v.view(np.uint16))
 
 
-@pytest.mark.parametrize('position,batch', [(2047, 3), (32767, 1), (139263, 1)])
+@pytest.mark.parametrize('position,batch', [(2047, 3), (32767, 1), (139263, 1), (139262, 2), (139256, 8),
+                                            (16384, 8)])
 def test_attention_long_context_against_closed_form(lib, gpu, position, batch):
-    """tests/test_cuda.py:237-273 (position 139,263 + 1 = the 139,264 capacity)."""
+    """tests/test_cuda.py:237-273 (position 139,263 + 1 = the 139,264 capacity),
+    also with verification batches that end at the capacity: two tokens (the
+    stream kernel preparing its query) and eight (the ring kernel, whose
+    first split attends to the new keys)."""
     c = kat.long_context_case(position, batch)
     out, kc, vc = run_test_attention(lib, c['key_cache'], c['value_cache'], c['q_gate'], c['key'],
                                      c['value'], c['q_norm'], c['k_norm'], batch, position, c['epsilon'])
