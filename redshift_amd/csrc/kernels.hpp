@@ -177,13 +177,19 @@ size_t prefill_workspace_bytes(const Shape &s, Dtype dtype, bool precise);
 // kPrefillMinSplitPages pages when the row workgroups number fewer than the
 // CUs and the call covers at least kPrefillMinSplitKeyPages pages; at most
 // one workgroup per CU then), and its workspace: a raw bf16 call's fp16 V
-// copy and range words, then (at part_offset) the split partials.
-constexpr int kPrefillRows = 192, kPreciseRows = 128;
+// copy and range words, then (at part_offset) the split partials.  A
+// precise call without key splits whose 128-row workgroups would need more
+// rounds over the CUs than 1.5 times those of 192-row ones takes
+// kPreciseTwoPassRows rows per workgroup in two passes of its eight waves
+// (passes = 2): the later 128 rows first, then the earliest 64 rows, which
+// see the fewest keys, on four of the waves.
+constexpr int kPrefillRows = 192, kPreciseRows = 128, kPreciseTwoPassRows = 192;
 constexpr int kPrefillMinSplitPages = 8, kPrefillMinSplitKeyPages = 32, kPrefillMaxSplits = 64;
 struct PrefillPlan {
     int rows;            // query rows per workgroup
     int row_wgs;         // workgroups of rows per KV head
     int splits;
+    int passes;          // 1, or 2 (a precise call, eight waves over 192 rows)
     size_t part_offset;  // split partials in the workspace
     size_t bytes;        // workspace
 };

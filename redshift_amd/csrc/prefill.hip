@@ -138,7 +138,11 @@ __device__ __forceinline__ int v_slot_token(int g, int j) {
 // The rows of one workgroup; kring and vring are the kernel's two rings of
 // four pages, V pages read from v_pages with v_head_stride elements per KV
 // head.
-template <int D, typename KV, typename VT, bool PSPLIT, bool QSPLIT, int MODE, int ROWS>
+// PASS: -1 for a single pass (ROWS / 16 waves, one tile each); 0 and 1 for
+// the two passes of the two-pass instance (eight waves over ROWS = 192 rows:
+// pass 0 gives waves 0-3 the round-0 tiles and waves 4-7 the round-1 tiles,
+// pass 1 gives waves 0-3 the round-2 tiles and waves 4-7 none).
+template <int D, typename KV, typename VT, bool PSPLIT, bool QSPLIT, int MODE, int ROWS, int PASS = -1>
 __device__ __forceinline__ void prefill_rows(const PrefillArgs &a, KV *kring, VT *vring, const void *v_pages,
                                              size_t v_head_stride) {
     using V8 = typename Vec8<KV>::type;
@@ -146,7 +150,8 @@ __device__ __forceinline__ void prefill_rows(const PrefillArgs &a, KV *kring, VT
     typedef uint32_t U4 __attribute__((ext_vector_type(4)));
     using PT = VT;
     using PV8 = typename Vec8<PT>::type;
-    constexpr int kPWaves = ROWS / 16;
+    constexpr int kPWaves = PASS < 0 ? ROWS / 16 : 8;
+    static_assert(PASS < 0 || ROWS == 3 * 4 * 16, "two passes of eight waves over three rounds of tiles");
     constexpr int KS = D / 32, DT = D / 16;
     constexpr int PAGE = 32 * D;                       // elements of one K (or V) page
     constexpr int PAGE_BYTES = PAGE * 2;
@@ -175,8 +180,10 @@ __device__ __forceinline__ void prefill_rows(const PrefillArgs &a, KV *kring, VT
     const int rest = blockIdx.x / a.kv_heads;
     const int j = rest % a.n_tiles, split = rest / a.n_tiles;
     static_assert(kPWaves % 4 == 0 && kPWaves / 4 <= 3, "one to three rounds of four waves");
-    const int T = (R + 15) / 16, K = 4 * a.n_tiles, slot = 4 * j + (w & 3), round = w >> 2;
-    const int tile = round == 0 ? T - 1 - slot : round == 1 ? T - 2 * K + slot : T - 3 * K + slot;
+    const int T = (R + 15) / 16, K = 4 * a.n_tiles, slot = 4 * j + (w & 3);
+    const int round = PASS == 1 ? (w < 4 ? 2 : 3) : w >> 2;   // round 3: no tile
+    const int tile = round == 0 ? T - 1 - slot : round == 1 ? T - 2 * K + slot
+                   : round == 2 ? T - 3 * K + slot : -1;
     const int row0 = 16 * tile;
     const int row_end = R;                                              // valid rows: [0, row_end)
 
@@ -204,9 +211,11 @@ __device__ __forceinline__ void prefill_rows(const PrefillArgs &a, KV *kring, VT
             for (int ks = 0; ks < KS; ++ks) global_load16(qlo[ks], lo + 32 * ks);
         }
     }
-    // Keys this workgroup can see: 0 .. position + (token of its last row,
-    // the last valid row of tile T-1-4j).
-    const int n_keys = a.position + (min(16 * (T - 4 * j), R) - 1) / a.group + 1;
+    // Keys this workgroup can see: 0 .. position + (token of its last row:
+    // the last valid row of tile T-1-4j, or in the second pass of tile
+    // T-3K+4j+3; none when that tile is padding).
+    const int last_tile = PASS == 1 ? T - 3 * K + 4 * j + 3 : T - 1 - 4 * j;
+    const int n_keys = last_tile < 0 ? 0 : a.position + (min(16 * (last_tile + 1), R) - 1) / a.group + 1;
     const int n = (n_keys + 31) / 32;
     // This split's pages: p0 + i for i = 0 .. nl-1 (local index i, ring
     // buffer i % 4).  nl is uniform over the workgroup; nl = 0 leaves empty
@@ -503,6 +512,22 @@ void attention_prefill(PrefillArgs a) {
     prefill_rows<D, KV, VT, PSPLIT, QSPLIT, MODE, ROWS>(a, kring, vring, a.v_pages, a.head_stride);
 }
 
+// The precise rows in two passes of eight waves (192 rows per workgroup):
+// one round of workgroups where 128-row ones would take two.  Between the
+// passes every wave's output stores complete (the second pass's waits count
+// its page loads only) and every wave has finished reading the rings.
+template <int D, typename KV, typename VT, bool PSPLIT, bool QSPLIT, int MODE>
+__global__ __launch_bounds__(8 * kWave, 1)
+void attention_prefill_2pass(PrefillArgs a) {
+    constexpr int ROWS = kPreciseTwoPassRows;
+    __shared__ __attribute__((aligned(16))) KV kring[4 * 32 * D];
+    __shared__ __attribute__((aligned(16))) VT vring[4 * 32 * D];
+    prefill_rows<D, KV, VT, PSPLIT, QSPLIT, MODE, ROWS, 0>(a, kring, vring, a.v_pages, a.head_stride);
+    wait_vmcnt<0>();
+    ring_barrier();
+    prefill_rows<D, KV, VT, PSPLIT, QSPLIT, MODE, ROWS, 1>(a, kring, vring, a.v_pages, a.head_stride);
+}
+
 // bf16 pages: the workgroups of a KV head that the conversion pass did not
 // flag multiply by the fp16 copy of V with one fp16 P; a flagged head's take
 // the exact products (bf16 V, P as bf16 hi + lo parts).  Every wave reads
@@ -543,7 +568,10 @@ const void *prefill_kernel(Dtype dtype, bool out_f32) {
 // The fused model path: fp16 pages, fp32 query as hi + lo parts, hi + lo P
 // (the same precision as the split kernels' precise instance).
 template <int D>
-const void *precise_prefill_kernel(bool gated) {
+const void *precise_prefill_kernel(bool gated, int passes) {
+    if (passes == 2)
+        return gated ? (const void *)&attention_prefill_2pass<D, _Float16, _Float16, true, true, kOutGated>
+                     : (const void *)&attention_prefill_2pass<D, _Float16, _Float16, true, true, kOutF32>;
     return gated ? (const void *)&attention_prefill<D, _Float16, _Float16, true, true, kOutGated, kPreciseRows>
                  : (const void *)&attention_prefill<D, _Float16, _Float16, true, true, kOutF32, kPreciseRows>;
 }
@@ -646,6 +674,17 @@ PrefillPlan plan_prefill_for(const Shape &s, Dtype dtype, bool precise, int cus)
     if (pages >= kPrefillMinSplitKeyPages && base < cus)
         p.splits = (int)std::max(1LL, std::min<long long>({cus / base, pages / kPrefillMinSplitPages,
                                                            kPrefillMaxSplits}));
+    p.passes = 1;
+    if (precise && p.splits == 1) {
+        const long long rows = (long long)s.group() * s.tokens;
+        const long long wgs2 = (rows + kPreciseTwoPassRows - 1) / kPreciseTwoPassRows;
+        const long long rounds1 = (base + cus - 1) / cus, rounds2 = (wgs2 * s.kv_heads + cus - 1) / cus;
+        if (3 * rounds2 < 2 * rounds1) {
+            p.rows = kPreciseTwoPassRows;
+            p.row_wgs = (int)wgs2;
+            p.passes = 2;
+        }
+    }
     p.part_offset = dtype == Dtype::BF16 && !precise ? conv_plan(s).bytes : 0;
     p.bytes = p.part_offset + split_partial_bytes(s, p.splits);
     return p;
@@ -783,7 +822,7 @@ void launch_prefill(const Shape &s, Dtype dtype, bool precise, float scale, cons
         a.part_ml = a.part_o + (size_t)s.kv_heads * plan.splits * a.rows * s.head_dim;
     }
     const bool d256 = s.head_dim == 256;
-    const int threads = (plan.rows / 16) * kWave;
+    const int threads = (plan.passes == 2 ? 8 : plan.rows / 16) * kWave;
     const long long grid = (long long)plan.row_wgs * s.kv_heads * plan.splits;
     require(grid * threads < (1LL << 32), "prefill launch exceeds 2^32 work-items");
     void *args[] = {&a};
@@ -826,7 +865,8 @@ void launch_prefill(const Shape &s, Dtype dtype, bool precise, float scale, cons
         check(hipLaunchKernel(kernel, dim3((unsigned)blocks), dim3(kCombineThreads), cargs, 0, stream));
     };
     if (precise) {
-        const void *kernel = d256 ? precise_prefill_kernel<256>(gate != nullptr) : precise_prefill_kernel<128>(gate != nullptr);
+        const void *kernel = d256 ? precise_prefill_kernel<256>(gate != nullptr, plan.passes)
+                                  : precise_prefill_kernel<128>(gate != nullptr, plan.passes);
         check(hipLaunchKernel(kernel, dim3((unsigned)grid), dim3(threads), args, 0, stream));
         combine();
         return;

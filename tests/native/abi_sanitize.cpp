@@ -303,9 +303,17 @@ void prefill_planner_sweep() {
                                 ++plans;
                                 const long long R = (long long)group * tokens;
                                 const long long pages = ((long long)pos + tokens + 31) / 32;
-                                EXPECT(p.rows == (precise ? rs::kPreciseRows : rs::kPrefillRows));
+                                // A precise call without key splits takes two passes over 192-row
+                                // workgroups when 128-row ones need more than 1.5 times their rounds.
+                                const long long one = (R + rs::kPreciseRows - 1) / rs::kPreciseRows * hk[1];
+                                const long long two = (R + rs::kPreciseTwoPassRows - 1) / rs::kPreciseTwoPassRows * hk[1];
+                                const bool two_pass = precise && p.splits == 1 &&
+                                                      3 * ((two + cus - 1) / cus) < 2 * ((one + cus - 1) / cus);
+                                EXPECT(p.passes == (two_pass ? 2 : 1));
+                                EXPECT(p.rows == (!precise ? rs::kPrefillRows
+                                                  : p.passes == 2 ? rs::kPreciseTwoPassRows : rs::kPreciseRows));
                                 EXPECT(p.row_wgs == (R + p.rows - 1) / p.rows);
-                                const long long base = (long long)p.row_wgs * hk[1];
+                                const long long base = (long long)(p.passes == 2 ? one / hk[1] : p.row_wgs) * hk[1];
                                 EXPECT(p.splits >= 1 && p.splits <= rs::kPrefillMaxSplits);
                                 if (pages < rs::kPrefillMinSplitKeyPages || base >= cus) {
                                     EXPECT(p.splits == 1);
@@ -324,8 +332,8 @@ void prefill_planner_sweep() {
                                     p.splits > 1 ? r256((unsigned __int128)hk[1] * p.splits * R * (d + 2) * 4) : 0;
                                 EXPECT((unsigned __int128)p.part_offset == conv);
                                 EXPECT((unsigned __int128)p.bytes == conv + parts);
-                                EXPECT((unsigned __int128)p.row_wgs * hk[1] * p.splits * (p.rows / 16) * 64 <
-                                       ((unsigned __int128)1 << 32));
+                                EXPECT((unsigned __int128)p.row_wgs * hk[1] * p.splits *
+                                           (p.passes == 2 ? 8 : p.rows / 16) * 64 < ((unsigned __int128)1 << 32));
                             }
     std::printf("abi_sanitize: %d prefill plans checked\n", plans);
 }

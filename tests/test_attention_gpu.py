@@ -385,13 +385,15 @@ def test_short_fused_appends_the_prepare_kernels_bits(gpu, position):
     assert_close(short.cpu().numpy(), chunk[:8].cpu().numpy(), 3e-5)
 
 
-@pytest.mark.parametrize('batch,position', [(100, 300), (57, 1), (64, 6000)])
+@pytest.mark.parametrize('batch,position', [(100, 300), (57, 1), (64, 6000), (2048, 40)])
 def test_fused_prefill_chunk_matches_oracle(gpu, batch, position):
     """A prefill chunk through the fused entry (more than 8 tokens: prepare,
     append, the precise prefill kernel and the gate) on the reference's
     sine-wave fixture (tests/test_cuda.py:201-216), with that test's
     tolerances: output 3e-4, appended K 2e-3, V exact.  64 tokens after
-    6,000 split their keys over several workgroups and combine them (gated)."""
+    6,000 split their keys over several workgroups and combine them (gated);
+    2048 tokens run two passes of 192 rows per workgroup (one round of
+    workgroups on 256 CUs)."""
     torch = gpu
     c = kat.sine_wave_case(batch=batch, position=position)
     expected = ref.fused_attention(c['key_cache'], c['value_cache'], c['q_gate'], c['key'], c['value'],

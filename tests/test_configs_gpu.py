@@ -106,6 +106,7 @@ def test_prefill_chunk_full_size_precise(gpu):
     (24, 4, 256, 64, 16000),    # prefill kernel, keys split over 21 workgroups per row workgroup
     (24, 4, 256, 200, 3000),    # prefill kernel, 6 key splits
     (16, 2, 128, 40, 9000),     # prefill kernel at head_dim 128, 35 key splits
+    (24, 4, 256, 1400, 100),    # two passes of 192 rows (on 256 CUs; three padding tiles)
 ])
 def test_precise_entry_against_oracle(gpu, q_heads, kv_heads, head_dim, T, position):
     """qv_attention_precise across its kernels (fp32 query, fp16 pages,
