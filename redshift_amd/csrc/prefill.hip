@@ -551,7 +551,9 @@ void attention_prefill_bf16(PrefillArgs a) {
 // Rows per workgroup (kPrefillRows, kernels.hpp): 192 (twelve waves, three
 // per SIMD; 2048 tokens of six query heads per KV head make 64 workgroups
 // per KV head, one round on 256 CUs).  A precise query (hi + lo parts) needs
-// twice the query registers: kPreciseRows = 128 (eight waves, two per SIMD).
+// twice the query registers: kPreciseRows = 128 (eight waves, two per SIMD),
+// or kPreciseTwoPassRows = 192 on the same eight waves in two passes
+// (attention_prefill_2pass) when that saves rounds of workgroups.
 
 // The raw instances: fp16 pages; bf16 pages, V through the conversion pass
 // below (attention_prefill_bf16).
