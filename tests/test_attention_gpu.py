@@ -701,13 +701,15 @@ def test_fused_random_shapes_against_oracle(gpu, batch, position, seed):
     assert_close(vcache.float().cpu().numpy(), expected[2], 0)
 
 
-@pytest.mark.parametrize('batch,position', [(1, 16000), (2, 3000), (5, 300), (8, 16000)])
+@pytest.mark.parametrize('batch,position', [(1, 16000), (2, 3000), (5, 300), (8, 16000), (1400, 100), (64, 16000)])
 def test_fused_graph_replay_matches_eager(gpu, batch, position):
     """The fused entry (prepare in the split kernels' prologue, the new keys
-    appended by the kernels) enqueues kernels only, so it can be captured in
-    a HIP graph: every replay, with eager calls reusing the workspace and
-    synchronisations in between, reproduces the eager output and caches bit
-    for bit."""
+    appended by the kernels; for a prefill chunk the prepare launch, the
+    precise prefill in two passes (1400 tokens) or with its keys split (64
+    tokens at 16,000) and the gated combine) enqueues kernels only, so it
+    can be captured in a HIP graph: every replay, with eager calls reusing
+    the workspace and synchronisations in between, reproduces the eager
+    output and caches bit for bit."""
     torch = gpu
     rng = np.random.default_rng(position + batch)
     kc = (rng.standard_normal((position, 4, 256)) * .5).astype(np.float16)
