@@ -239,6 +239,13 @@ def check_fused_inputs(q_gate, key, value, q_norm, k_norm, cache):
     return named
 
 
+def _aligned16(t):
+    """t as a contiguous tensor whose data starts on a 16-byte boundary (the
+    device ABI's requirement): t itself when it already is one, else a copy."""
+    t = t.contiguous()
+    return t if t.data_ptr() % 16 == 0 else t.clone()
+
+
 def attention_fused(q_gate, key, value, q_norm, k_norm, cache, position, epsilon, out=None, ws=None):
     """Device-side fused attention of the fixed 24/4/256 model (the reference's
     k_attention): prepares q/k, appends k/v at position.., attends and gates.
@@ -253,7 +260,7 @@ def attention_fused(q_gate, key, value, q_norm, k_norm, cache, position, epsilon
     if ws is None:
         ws = workspace(fused_workspace_bytes(batch, position), q_gate.device)
     _same_device([('out', out), ('workspace', ws)], cache.k.device)
-    tensors = [t.contiguous() for _, t in named]
+    tensors = [_aligned16(t) for _, t in named]
     check(lib, lib.qv_attention_fused(_ptr(out), _ptr(cache.k), _ptr(cache.v),
                                       *[_ptr(t) for t in tensors], batch, position, cache.capacity,
                                       float(epsilon), _ptr(ws), _nbytes(ws), _stream()))

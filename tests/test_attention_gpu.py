@@ -746,3 +746,38 @@ def test_fused_graph_replay_matches_eager(gpu, batch, position):
         assert torch.equal(out, eager)
         assert torch.equal(cache.k.view(torch.int16), k0.view(torch.int16))   # bits: unused slots hold NaN
         assert torch.equal(cache.v.view(torch.int16), v0.view(torch.int16))
+
+
+def test_fused_front_end_realigns_input_views(gpu):
+    """The device ABI takes 16-byte aligned buffers; the torch front end
+    passes an input view that starts elsewhere (here the norm weights and the
+    key at a 4-byte offset into their storage) as an aligned copy, with the
+    same result bit for bit."""
+    torch = gpu
+    rng = np.random.default_rng(5)
+    batch, position = 8, 3000
+    kc = torch.from_numpy((rng.standard_normal((position, 4, 256)) * .5).astype(np.float16)).cuda()
+    vc = torch.from_numpy((rng.standard_normal((position, 4, 256)) * .5).astype(np.float16)).cuda()
+    q_gate = torch.from_numpy(rng.standard_normal((batch, 24, 512)).astype(np.float32)).cuda()
+    key = torch.from_numpy(rng.standard_normal((batch, 4, 256)).astype(np.float32)).cuda()
+    value = torch.from_numpy(rng.standard_normal((batch, 4, 256)).astype(np.float32)).cuda()
+    norms = torch.from_numpy((1 + .25 * rng.uniform(-1, 1, 512)).astype(np.float32)).cuda()
+    q_norm, k_norm = norms[:256].clone(), norms[256:].clone()
+    outs = []
+    for offset in (False, True):
+        cache = A.PagedKV(4, 256, A.round_capacity(position + batch), torch.float16)
+        cache.pack(kc, vc)
+        args = [q_gate, key, value, q_norm, k_norm]
+        if offset:
+            views = []
+            for t in (key, q_norm, k_norm):
+                buf = torch.empty(t.numel() + 1, dtype=torch.float32, device=t.device)
+                v = buf[1:].view(t.shape)
+                v.copy_(t)
+                assert v.data_ptr() % 16 != 0
+                views.append(v)
+            args = [q_gate, views[0], value, views[1], views[2]]
+        outs.append((A.attention_fused(*args, cache, position, 1e-6).clone(), cache.k.clone()))
+    torch.cuda.synchronize()
+    assert torch.equal(outs[0][0], outs[1][0])
+    assert torch.equal(outs[0][1].view(torch.int16), outs[1][1].view(torch.int16))
