@@ -23,13 +23,12 @@ namespace rs {
 // policy of the combine follows the store policy of the split kernel: the
 // mixed pairs measured slower).
 //
-// NEWKEY (the fused decode's new token; the code takes up to 8 tokens): the
-// splits cover the cached keys only.  Wave w4 takes the new keys j = w4 and
-// w4 + 4 that this row sees (j <= its token t) and folds each in as one
-// more split: score
-// q . k_j with the prepared fp32 query (tok->q_prep) and the fp16 key the
-// split kernel appended at position + j, weight 1 at its own max, value the
-// appended fp16 v_j.
+// NEWKEY (the new tokens of a fused call on the stream kernel, one or two;
+// the code takes up to 8): the splits cover the cached keys only.  Wave w4
+// takes the new keys j = w4 and w4 + 4 that this row sees (j <= its token
+// t) and folds each in as one more split: score q . k_j with the prepared
+// fp32 query (tok->q_prep) and the fp16 key the split kernel appended at
+// position + j, weight 1 at its own max, value the appended fp16 v_j.
 template <int D, typename KV, typename PT, bool NT, bool NEWKEY = false>
 __device__ __forceinline__ void combine_row(const PT *part_o, const float *part_ml, int splits,
                                             int rows, int group, int q_heads, int row, int h,

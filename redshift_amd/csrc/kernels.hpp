@@ -56,7 +56,7 @@ struct SplitArgs {
     size_t head_stride;
     int q_heads, kv_heads, group, rows, position, n_keys, n_pages, splits;
     float scale_log2;
-    FusedToken tok;       // the fused decode instance's query source
+    FusedToken tok;       // the prepared-query instances' inputs (stream: 1-2 tokens, ring: 3-8)
     void *out;            // direct output: [tokens][q_heads][D] (one split per KV head)
 };
 
