@@ -35,9 +35,10 @@
 // keys in the free ring buffer, which the first key half of every tile
 // attends to (row t seeing new keys 0..t) before page 0.  So the partials
 // hold every key, and the plain gated combine merges them.  The first
-// split appends key and value w to the pages after its partials: stores
-// issued among the page loads would share the vector-memory counter that
-// the ring's waits count page loads on.  (Appending in the combine instead,
+// split appends key and value w to the pages once its page loop is done,
+// before the merge of the key halves: stores issued among the page loads
+// would share the vector-memory counter that the ring's waits count page
+// loads on.  (Appending in the combine instead,
 // by one workgroup per KV head, measured slower: the combine's critical
 // path grew by more than the split kernel's.)
 #include "kernels.hpp"
@@ -485,6 +486,23 @@ void attention_ring(SplitArgs a) {
         }
     }
 
+    if constexpr (PREP) {
+        // First split: new key and value w appended to the pages, issued as
+        // soon as the page loop is done (no load is in flight any more), so
+        // the stores overlap the merge below.  Keys past n_keys-1 are masked
+        // in every split (scores) and their V slots zeroed, so a split that
+        // streams the page receiving them reads either bits harmlessly.
+        if (split == 0 && n > 0 && w < a.tok.tokens) {
+            _Float16 *kp = static_cast<_Float16 *>(a.tok.k_pages) + (size_t)h * a.tok.head_stride;
+            _Float16 *vp = static_cast<_Float16 *>(a.tok.v_pages) + (size_t)h * a.tok.head_stride;
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                kp[k_page_offset(a.tok.position + w, 64 * i + lane, D)] = new_k[i];
+                vp[v_page_offset(a.tok.position + w, 64 * i + lane, D)] = new_v[i];
+            }
+        }
+    }
+
     // ---- merge the two key halves of every tile, then store the partials ----
     // The last step waited for every load; once all waves are past this
     // barrier no page is read any more, and ring0..ring2 hold the exchange:
@@ -569,21 +587,6 @@ void attention_ring(SplitArgs a) {
                     const f32x4 o1 = *reinterpret_cast<const f32x4 *>(xacc + (dt * kWave + lane) * 4);
                     __builtin_nontemporal_store(acc[dt] * f0 + o1 * f1, reinterpret_cast<f32x4 *>(po + dt * 16));
                 }
-            }
-        }
-    }
-    if constexpr (PREP) {
-        // First split: new key and value w appended to the pages.  Keys past
-        // n_keys-1 are masked in every split (scores) and their V slots
-        // zeroed, so a split that streams the page receiving them reads
-        // either bits harmlessly.
-        if (split == 0 && n > 0 && w < a.tok.tokens) {
-            _Float16 *kp = static_cast<_Float16 *>(a.tok.k_pages) + (size_t)h * a.tok.head_stride;
-            _Float16 *vp = static_cast<_Float16 *>(a.tok.v_pages) + (size_t)h * a.tok.head_stride;
-#pragma unroll
-            for (int i = 0; i < 4; ++i) {
-                kp[k_page_offset(a.tok.position + w, 64 * i + lane, D)] = new_k[i];
-                vp[v_page_offset(a.tok.position + w, 64 * i + lane, D)] = new_v[i];
             }
         }
     }
