@@ -20,7 +20,12 @@ pytestmark = pytest.mark.gpu
 EPS = 1e-6
 
 
-def test_session_fused_prefill_verify_commit_checkpoint_restore(gpu):
+@pytest.mark.parametrize('first', [40, 300])
+def test_session_fused_prefill_verify_commit_checkpoint_restore(gpu, first):
+    """The sequence after a first prefill chunk of `first` tokens: at 40 the
+    later steps run the one-launch kernel of short contexts; at 300 they run
+    the split kernels that prepare their own query (the stream kernel for one
+    or two tokens, the ring kernel for 5 and 8)."""
     torch = gpu
     from redshift_amd.kvcache import AttentionKV, SessionError
     layers = 2
@@ -55,12 +60,12 @@ def test_session_fused_prefill_verify_commit_checkpoint_restore(gpu):
             assert_close(v_dev.float().cpu().numpy(), vc, 0)
             logical[layer] = [k_dev.cpu().numpy(), v_dev.cpu().numpy()]
 
-    run(40)                          # a prefill chunk (prefill kernel)
+    run(first)                       # a prefill chunk (prefill kernel)
     run(8)                           # the server's 8-token prefill step (split kernels)
     run(1)                           # decode (fused split: query prepared, key appended in-kernel)
-    assert kv.position == 49
+    assert kv.position == first + 9
     run(8, recording=True)           # verification
-    assert (kv.position, kv.pending) == (57, 8)
+    assert (kv.position, kv.pending) == (first + 17, 8)
     with pytest.raises(SessionError, match='commit or abort'):
         kv.begin(1)
     with pytest.raises(SessionError, match='commit or abort'):
@@ -68,18 +73,18 @@ def test_session_fused_prefill_verify_commit_checkpoint_restore(gpu):
     with pytest.raises(SessionError, match='acceptance outside'):
         kv.commit(9)
     kv.commit(1)
-    assert (kv.position, kv.pending) == (50, 0)
+    assert (kv.position, kv.pending) == (first + 10, 0)
     with pytest.raises(SessionError, match='between 1 and 8$'):
         kv.begin(9, recording=True)
-    run(1)                           # overwrites the first rejected row (50)
+    run(1)                           # overwrites the first rejected row (first + 10)
     kv.checkpoint()
     saved = [[a.copy() for a in pair] for pair in logical]
     run(5, recording=True)
     kv.commit(5)
     run(1)
-    assert kv.position == 57
+    assert kv.position == first + 17
     kv.restore()
-    assert (kv.position, kv.pending) == (51, 0)
+    assert (kv.position, kv.pending) == (first + 11, 0)
     logical = saved
     run(2)                           # from the restored prefix
     kv.reset()
