@@ -353,8 +353,11 @@ void attention_stream(SplitArgs a) {
         sml[w][0][lane] = m;
         sml[w][1][lane] = l;
     }
+    // Only the rows that exist are merged (decode: 6 of the tile's 16).
+    if ((lane & 15) < a.rows) {
 #pragma unroll
-    for (int dt = 0; dt < DT; ++dt) so[w][dt * kWave + lane] = acc[dt];
+        for (int dt = 0; dt < DT; ++dt) so[w][dt * kWave + lane] = acc[dt];
+    }
     lds_barrier();
     if (OUT == kOutPartials && w == 0 && lane < a.rows && lane < 16) {
         float M = -INFINITY;
