@@ -121,6 +121,26 @@ def test_precise_entry_against_oracle(gpu, q_heads, kv_heads, head_dim, T, posit
     assert rel_l2(got, want) <= PRECISE_REL_L2
 
 
+@pytest.mark.parametrize('T,dtype', [(1, 'bf16'), (8, 'bf16'), (1, 'f32'), (4, 'f32')])
+def test_full_context_other_precisions(gpu, T, dtype):
+    """The 139,264-token capacity filled to its last slot on the routes the
+    fp16 workloads leave out: bf16 pages (P as hi + lo parts) and the fp32
+    query of qv_attention_precise, for decode (the stream kernel, 48 splits
+    per head) and verification (the ring kernel), 64 outlier keys."""
+    position = 139264 - T
+    w = Workload('full', 24, 4, 256, T, position, 1 / 16, dtype, 900 + T, 0.5, 0.5, 64, 8.0)
+    q, k, v, _ = make_inputs(w)
+    if dtype == 'f32':
+        k16, v16 = k.astype(np.float16), v.astype(np.float16)
+        got = precise_attention(w, q, k16, v16, gpu)
+        want = ref.gqa_attention(q, k16, v16, position, w.scale)
+        assert rel_l2(got, want) <= PRECISE_REL_L2
+    else:
+        got = gpu_attention(w, q, k, v, gpu, fill_nan=True, out_dtype=gpu.float32)
+        want = ref.gqa_attention(to_float(q, dtype), to_float(k, dtype), to_float(v, dtype), position, w.scale)
+    assert_parity(got, want)
+
+
 @pytest.mark.parametrize('T,scale,dtype', [
     (100, 0.0, 'f16'), (100, -1 / 16, 'f16'), (100, -1 / 16, 'bf16'),   # prefill kernel
     (3, 0.0, 'f16'), (8, -0.2, 'bf16'),                                 # ring kernel
