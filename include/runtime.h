@@ -178,8 +178,10 @@ int qv_attention_precise_workspace(uint64_t *bytes, int q_heads, int kv_heads, i
  * pages, fp32 output.  The reference's attention kernels read q as fp32
  * (written by attn_prepare, src/kernels.cu:416-434, read at :435-503) from
  * fp16 caches.  The library splits q into fp16 parts hi = fp16(q) and
- * lo = fp16(q - hi), staged at the start of the workspace, and multiplies
- * both by K; P multiplies V as hi + lo parts too.  The parts hold q to
+ * lo = fp16(q - hi) (in the decode kernel itself for up to 16 query rows
+ * per KV head, otherwise staged at the start of the workspace by a launch
+ * of their own) and multiplies both by K; P multiplies V as hi + lo parts
+ * too.  The parts hold q to
  * about 22 significant bits: |q| < 65504, error at most
  * 2^-25 + 2^-22 |q|.  q and out: [tokens][q_heads][head_dim] float32;
  * shapes, limits and kernels otherwise as qv_attention. */

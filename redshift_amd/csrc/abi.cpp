@@ -528,11 +528,19 @@ extern "C" int qv_attention_precise(float *out, const float *q, const void *k_pa
         raw_buffers(out, q, k_pages, v_pages, workspace);
         require(workspace_bytes >= precise_workspace(s), "workspace too small");
         hipStream_t st = static_cast<hipStream_t>(stream);
+        void *partials = static_cast<char *>(workspace) + precise_query_bytes(s);
+        if (s.group() * s.tokens <= 16) {
+            // One query tile: the stream kernel splits the fp32 query into
+            // its hi + lo parts itself.
+            run_attention(s, rs::Dtype::F16, true, scale, q, nullptr, k_pages, v_pages, partials, out, true, nullptr,
+                          st);
+            return;
+        }
         const size_t n = (size_t)s.tokens * s.q_heads * s.head_dim;
         uint16_t *q_hilo = static_cast<uint16_t *>(workspace);
         rs::launch_split_query(q_hilo, q, n, st);
-        run_attention(s, rs::Dtype::F16, true, scale, q_hilo, q_hilo + n, k_pages, v_pages,
-                      static_cast<char *>(workspace) + precise_query_bytes(s), out, true, nullptr, st);
+        run_attention(s, rs::Dtype::F16, true, scale, q_hilo, q_hilo + n, k_pages, v_pages, partials, out, true,
+                      nullptr, st);
     });
 }
 

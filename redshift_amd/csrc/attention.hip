@@ -61,12 +61,21 @@ constexpr int kMaxSplits = 1024;   // bound on workgroups per KV head
 // then issues its first KV loads, and only afterwards waits for the query
 // (publish: vector-memory counters retire in issue order, so that wait does
 // not drain the KV loads) and hands the fragments over through LDS.
-template <int D, int NQT, bool QSPLIT, typename KV>
+//
+// F32: a.q holds the fp32 query itself, and publish splits each loaded
+// fragment into its hi and lo parts (hi = fp16(q), lo = fp16(q - hi): the
+// rounding of the query split kernel, so the same bits), which saves the
+// split kernel's launch.
+template <int D, int NQT, bool QSPLIT, typename KV, bool F32 = false>
 struct QueryStage {
     using V8 = typename Vec8<KV>::type;
-    static constexpr int KS = D / 32, NQ = QSPLIT ? 2 : 1, N = NQ * NQT * KS, PER = N / kWaves;
-    static_assert(N % kWaves == 0, "fragments divide evenly over the waves");
-    V8 part[PER];
+    static constexpr int KS = D / 32, NQ = QSPLIT ? 2 : 1, N = NQ * NQT * KS;
+    static constexpr int NL = F32 ? NQT * KS : N;    // fragments loaded
+    static constexpr int PER = NL / kWaves;
+    static_assert(NL % kWaves == 0, "fragments divide evenly over the waves");
+    static_assert(!F32 || (QSPLIT && std::is_same<KV, _Float16>::value), "an fp32 query splits into fp16 parts");
+    V8 part[F32 ? 1 : PER];
+    f32x4 part32[F32 ? PER : 1][2];
 
     __device__ __forceinline__ void issue(const SplitArgs &a, int h, int lane, int w) {
 #pragma unroll
@@ -75,14 +84,34 @@ struct QueryStage {
             const int ks = e % KS, qt = (e / KS) % NQT, lo = e / (KS * NQT);
             const int row = min(16 * qt + (lane & 15), a.rows - 1);
             const int t = row / a.group, gg = row - t * a.group;
-            const KV *src = static_cast<const KV *>(lo ? a.q_lo : a.q) +
-                            ((size_t)t * a.q_heads + (size_t)h * a.group + gg) * D + 32 * ks + 8 * (lane >> 4);
-            part[i] = *reinterpret_cast<const V8 *>(src);
+            const size_t at = ((size_t)t * a.q_heads + (size_t)h * a.group + gg) * D + 32 * ks + 8 * (lane >> 4);
+            if constexpr (F32) {
+                const f32x4 *src = reinterpret_cast<const f32x4 *>(static_cast<const float *>(a.q) + at);
+                part32[i][0] = src[0];
+                part32[i][1] = src[1];
+            } else {
+                part[i] = *reinterpret_cast<const V8 *>(static_cast<const KV *>(lo ? a.q_lo : a.q) + at);
+            }
         }
     }
     __device__ __forceinline__ void publish(V8 *sq, int lane, int w) const {
 #pragma unroll
-        for (int i = 0; i < PER; ++i) sq[(w + kWaves * i) * kWave + lane] = part[i];
+        for (int i = 0; i < PER; ++i) {
+            if constexpr (F32) {
+                // Fragment e's hi part is fragment e, its lo part e + NQT*KS.
+                V8 hi, lo;
+#pragma unroll
+                for (int j = 0; j < 8; ++j) {
+                    const float x = part32[i][j >> 2][j & 3];
+                    hi[j] = (KV)x;
+                    lo[j] = (KV)(x - (float)hi[j]);
+                }
+                sq[(w + kWaves * i) * kWave + lane] = hi;
+                sq[(NQT * KS + w + kWaves * i) * kWave + lane] = lo;
+            } else {
+                sq[(w + kWaves * i) * kWave + lane] = part[i];
+            }
+        }
     }
     // After an LDS barrier: all fragments into registers.
     static __device__ __forceinline__ void gather(const V8 *sq, int lane, V8 (&qf)[NQ][NQT][KS]) {
@@ -128,7 +157,9 @@ template <int D, bool QSPLIT, bool PSPLIT, typename KV, bool PREP, int OUT = kOu
 __global__ __launch_bounds__(kWaves * kWave)
 void attention_stream(SplitArgs a) {
     using V8 = typename Vec8<KV>::type;
-    using QS = QueryStage<D, 1, QSPLIT, KV>;
+    // A precise raw call passes its fp32 query as it is (the split kernels'
+    // other precise callers prepare theirs: PREP).
+    using QS = QueryStage<D, 1, QSPLIT, KV, QSPLIT && !PREP>;
     constexpr int KS = D / 32, DT = D / 16, NQ = QSPLIT ? 2 : 1;
     static_assert(!PREP || (D == kModelHeadDim && D == 4 * kWave && QSPLIT && std::is_same<KV, _Float16>::value),
                   "the prepared query is the fp32 query of the 256-dim fp16 model, as hi + lo parts");
