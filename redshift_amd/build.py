@@ -15,6 +15,10 @@ PACKAGE = Path(__file__).resolve().parent
 ROOT = PACKAGE.parent
 SOURCES = ['abi.cpp', 'attention.hip', 'kv.hip', 'prefill.hip', 'ring.hip', 'short.hip']
 LIBRARY = PACKAGE / 'lib' / 'libredshift_hip.so'
+# Measurement probes for bench.py (a plain read of a launch's KV pages), kept
+# out of the attention library.
+PROBE_SOURCES = ['probe.hip']
+PROBE_LIBRARY = PACKAGE / 'lib' / 'libredshift_probe.so'
 ARCH = 'gfx950'
 # The host-sanitizer gate: the library's sources and a driver over its C ABI,
 # with AddressSanitizer and UndefinedBehaviorSanitizer on the host code only
@@ -42,9 +46,46 @@ COMMON_FLAGS = [
 # architectural VGPRs: with AGPR accumulators the compiler copies them out
 # and back on every page (for the rarely taken softmax rescale).
 SOURCE_FLAGS = {name: ['-mllvm', '-amdgpu-mfma-vgpr-form'] for name in ('ring.hip', 'prefill.hip')}
-# The prefill kernel masks keys to -inf and zeroes stale V slots explicitly,
-# so its maxima need no NaN quieting.
+# No operation in prefill.hip makes a NaN from its valid inputs: keys are
+# masked to -inf and stale V slots zeroed explicitly, and every exponent is
+# taken against a finite reference point (0 while a row has seen no key), so
+# -inf - (-inf) never occurs.  Its maxima then need no NaN quieting.
 SOURCE_FLAGS['prefill.hip'] = SOURCE_FLAGS['prefill.hip'] + ['-fno-honor-nans']
+
+
+# Kernels whose MFMA operand registers are filled by asm loads that the
+# compiler does not track (lds.hpp: global_load16 and lds_read; ring.hip:
+# global_load4), each followed later by an explicit wait.  A spill or copy
+# of such a register between the load and its wait would hand stale values
+# to the matrix cores, so the build fails if any of them uses scratch: the
+# compiler's resource remarks give every kernel's scratch bytes and spills.
+UNTRACKED_LOAD_SOURCES = ('ring.hip', 'prefill.hip')
+UNTRACKED_LOAD_KERNELS = ('attention_ring', 'attention_prefill')
+RESOURCE_REMARKS = '-Rpass-analysis=kernel-resource-usage'
+
+
+def check_no_scratch(name, stderr):
+    """Parses the resource remarks of one source's compile; raises if a
+    kernel that uses untracked loads has scratch or VGPR spills.  Returns the
+    messages without the remarks."""
+    kernel, checked, bad, rest = None, 0, [], []
+    for line in stderr.splitlines():
+        if 'remark:' not in line or RESOURCE_REMARKS not in line:
+            rest.append(line)
+            continue
+        text = line.split('remark:', 1)[1].split('[-Rpass', 1)[0].strip()
+        key, _, value = text.partition(':')
+        key, value = key.strip(), value.strip()
+        if key == 'Function Name':
+            kernel = value if any(k in value for k in UNTRACKED_LOAD_KERNELS) else None
+            checked += kernel is not None
+        elif kernel and key in ('ScratchSize [bytes/lane]', 'VGPRs Spill') and value != '0':
+            bad.append(f'{kernel}: {key} {value}')
+    if bad:
+        raise RuntimeError(f'{name}: kernels with untracked loads use scratch:\n' + '\n'.join(bad))
+    if not checked:
+        raise RuntimeError(f'{name}: no resource remarks for its kernels; the scratch check did not run')
+    return '\n'.join(rest)
 
 
 def hipcc():
@@ -74,27 +115,35 @@ def _compile_all(objdir, sources, extra, jobs):
     def compile_one(item):
         name, src = item
         obj = objdir / (name + '.o')
-        cmd = [compiler, '-x', 'hip', *COMMON_FLAGS, *SOURCE_FLAGS.get(name, []), *extra, '-c', str(src),
-               '-o', str(obj)]
-        return obj, _run(cmd)
+        checked = name in UNTRACKED_LOAD_SOURCES
+        cmd = [compiler, '-x', 'hip', *COMMON_FLAGS, *SOURCE_FLAGS.get(name, []), *extra,
+               *([RESOURCE_REMARKS] if checked else []), '-c', str(src), '-o', str(obj)]
+        stderr = _run(cmd)
+        return obj, check_no_scratch(name, stderr) if checked else stderr
 
     jobs = jobs or min(len(sources), os.cpu_count() or 1)
     with ThreadPoolExecutor(jobs) as pool:
         return list(pool.map(compile_one, sources))
 
 
+def _link(objects, library):
+    library.parent.mkdir(exist_ok=True)
+    tmp = library.with_suffix('.so.tmp')
+    _run([hipcc(), '-shared', '-fPIC', f'--offload-arch={ARCH}', *[str(o) for o in objects], '-o', str(tmp)])
+    os.replace(tmp, library)
+
+
 def build(verbose=False, jobs=None):
-    """Compile every source and link the shared library; returns its path."""
-    sources = [(name, PACKAGE / 'csrc' / name) for name in SOURCES]
-    results = _compile_all(PACKAGE / '_build', sources, [], jobs)
+    """Compile every source and link the shared library (and the probe
+    library beside it); returns the attention library's path."""
+    names = SOURCES + PROBE_SOURCES
+    results = _compile_all(PACKAGE / '_build', [(name, PACKAGE / 'csrc' / name) for name in names], [], jobs)
     for _, stderr in results:
         if verbose and stderr:
             print(stderr, file=sys.stderr)
-    LIBRARY.parent.mkdir(exist_ok=True)
-    tmp = LIBRARY.with_suffix('.so.tmp')
-    _run([hipcc(), '-shared', '-fPIC', f'--offload-arch={ARCH}', *[str(o) for o, _ in results],
-          '-o', str(tmp)])
-    os.replace(tmp, LIBRARY)
+    objects = dict(zip(names, (o for o, _ in results)))
+    _link([objects[name] for name in SOURCES], LIBRARY)
+    _link([objects[name] for name in PROBE_SOURCES], PROBE_LIBRARY)
     return LIBRARY
 
 

@@ -252,16 +252,22 @@ __device__ __forceinline__ void prefill_rows(const PrefillArgs &a, KV *kring, VT
 #pragma unroll
     for (int dt = 0; dt < DT; ++dt) acc[dt] = f32x4{0.f, 0.f, 0.f, 0.f};
     // m stays -inf for a row that sees no key of its pages (a split past its
-    // last key).  Its exponents are then NaN, which stays in that row's own
-    // lanes and accumulators (every cross-lane step combines the four lanes
-    // of one row); its partial is stored as empty instead.
+    // last key).  Its exponents are taken against 0 instead (mu below), so
+    // they are exp2(-inf) = 0 and the row's sum and accumulators stay 0: no
+    // operation of this file makes a NaN, which matters because it is
+    // compiled with -fno-honor-nans.  Such a row's partial is stored as
+    // empty.
     float m = -INFINITY, l = 0.f;
     f32x4 s[2];            // scores of the page whose softmax comes next
 
     // ---- S^T of one page, chunk by chunk ----
-    // K fragments stream through a window of two k-steps (four reads in
-    // flight): the pair of k-step ks+2 is requested as soon as that of ks
+    // K fragments stream through a window of KW k-steps (2 KW reads in
+    // flight): the pair of k-step ks+KW is requested as soon as that of ks
     // has landed; the two key tiles are two independent accumulation chains.
+    // The exact bf16 products (hi + lo P) in twelve waves keep one pair
+    // ahead instead of two, which holds them within the 168 VGPRs that
+    // twelve waves leave each (with two they need 171 and spill).
+    constexpr int KW = PSPLIT && !QSPLIT && kPWaves == 12 ? 1 : 2;
     V8 kf[KS][2];
     auto read_k = [&](auto ks_, uint32_t kb) __attribute__((always_inline)) {
         constexpr int ks = decltype(ks_)::value;
@@ -273,9 +279,9 @@ __device__ __forceinline__ void prefill_rows(const PrefillArgs &a, KV *kring, VT
     auto qk_chunk = [&](auto ks_, uint32_t kb, f32x4 *sn) __attribute__((always_inline)) {
         constexpr int ks = decltype(ks_)::value;
         if constexpr (ks < KS) {
-            constexpr int later = ks + 2 < KS ? 2 : 2 * (KS - 1 - ks);
+            constexpr int later = 2 * (KW - 1 < KS - 1 - ks ? KW - 1 : KS - 1 - ks);
             lds_wait<later>(kf[ks][0], kf[ks][1]);
-            read_k(std::integral_constant<int, ks + 2>{}, kb);
+            read_k(std::integral_constant<int, ks + KW>{}, kb);
             sn[0] = mfma(kf[ks][0], qf[ks], sn[0]);
             sn[1] = mfma(kf[ks][1], qf[ks], sn[1]);
             if constexpr (QSPLIT) {
@@ -298,8 +304,7 @@ __device__ __forceinline__ void prefill_rows(const PrefillArgs &a, KV *kring, VT
         // them run ahead through its phase while another's V products fill
         // the matrix pipe (2048-token chunk: 461-469 -> 447-453 us per layer).
         __builtin_amdgcn_s_setprio(1);
-        read_k(std::integral_constant<int, 0>{}, kb);
-        read_k(std::integral_constant<int, 1>{}, kb);
+        static_for<0, KW>([&](auto ks) { read_k(ks, kb); });
         // Scores of page p0 + i; keys past a row's limit are masked.
         const int key0 = (p0 + i) * 32;
         float x[8];
@@ -323,18 +328,22 @@ __device__ __forceinline__ void prefill_rows(const PrefillArgs &a, KV *kring, VT
         // split's first page, where its max becomes finite.
         const float bm = mx;
         float alpha = 1.f;
+        // `moved` implies a finite bm, so m - bm is never -inf - (-inf).
         const bool moved = bm > m + kLazy;
         if (moved) alpha = __builtin_amdgcn_exp2f(m - bm);
         m = moved ? bm : m;
+        // The exponents' reference point: m, or 0 while the row has seen no
+        // key (all its scores are then -inf, and their exponents 0).
+        float mu = m == -INFINITY ? 0.f : m;
         float e[8];
-        pin(alpha, m);
+        pin(alpha, mu);
         qk_chunk(std::integral_constant<int, 2>{}, kb, sn);
 #pragma unroll
-        for (int j = 0; j < 4; ++j) e[j] = __builtin_amdgcn_exp2f(x[j] - m);
+        for (int j = 0; j < 4; ++j) e[j] = __builtin_amdgcn_exp2f(x[j] - mu);
         pin(e[0], e[1], e[2], e[3]);
         qk_chunk(std::integral_constant<int, 3>{}, kb, sn);
 #pragma unroll
-        for (int j = 4; j < 8; ++j) e[j] = __builtin_amdgcn_exp2f(x[j] - m);
+        for (int j = 4; j < 8; ++j) e[j] = __builtin_amdgcn_exp2f(x[j] - mu);
         pin(e[4], e[5], e[6], e[7]);
         qk_chunk(std::integral_constant<int, 4>{}, kb, sn);
         // P^T as B operands: hi parts (and lo parts, bf16).
@@ -414,8 +423,7 @@ __device__ __forceinline__ void prefill_rows(const PrefillArgs &a, KV *kring, VT
         else if (nl > 1) wait_vmcnt<3 * H>();
         else wait_vmcnt<H>();
         ring_barrier();
-        read_k(std::integral_constant<int, 0>{}, kring_lane);
-        read_k(std::integral_constant<int, 1>{}, kring_lane);
+        static_for<0, KW>([&](auto ks) { read_k(ks, kring_lane); });
         static_for<0, KS>([&](auto ks) { qk_chunk(ks, kring_lane, s); });
     } else {
         wait_vmcnt<0>();   // no page of this split: the query loads only

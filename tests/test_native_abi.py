@@ -205,3 +205,28 @@ def test_front_end_rejects_mismatched_tensors(lib):
         A.attention_fused(inputs[0].half(), *inputs[1:], cache, 0, 1e-6)
     with pytest.raises(ValueError, match='value must hold'):
         A.attention_fused(*inputs[:2], torch.zeros((2, 4, 256)), *inputs[3:], cache, 0, 1e-6)
+
+
+def test_build_refuses_scratch_in_kernels_with_untracked_loads():
+    """redshift_amd.build reads the compiler's resource remarks of ring.hip
+    and prefill.hip and fails on scratch or VGPR spills in the kernels whose
+    operands arrive through untracked asm loads; a compile without remarks
+    fails too, so the check cannot pass by not running."""
+    from redshift_amd.build import RESOURCE_REMARKS, check_no_scratch
+
+    def remarks(name, scratch, spills):
+        tag = f' [{RESOURCE_REMARKS}]'
+        return '\n'.join(f'prefill.hip:1:1: remark: {line}{tag}' for line in (
+            f'Function Name: {name}', '    VGPRs: 168', f'    ScratchSize [bytes/lane]: {scratch}',
+            f'    VGPRs Spill: {spills}'))
+
+    kernel = '_ZN2rs12_GLOBAL__N_122attention_prefill_bf16ILi256ELi0ELi192EEEvNS0_11PrefillArgsE'
+    other = '_ZN2rs12_GLOBAL__N_115combine_prefillILi256EfLi2ELi8EEEvNS0_18CombinePrefillArgsE'
+    assert check_no_scratch('prefill.hip', 'a warning\n' + remarks(kernel, 0, 0)) == 'a warning'
+    assert check_no_scratch('prefill.hip', remarks(kernel, 0, 0) + '\n' + remarks(other, 16, 4)) == ''
+    with pytest.raises(RuntimeError, match='ScratchSize'):
+        check_no_scratch('prefill.hip', remarks(kernel, 28, 0))
+    with pytest.raises(RuntimeError, match='VGPRs Spill 6'):
+        check_no_scratch('ring.hip', remarks(kernel.replace('prefill_bf16', 'ring'), 0, 6))
+    with pytest.raises(RuntimeError, match='did not run'):
+        check_no_scratch('ring.hip', 'no remarks at all')
