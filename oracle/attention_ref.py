@@ -120,23 +120,38 @@ def gqa_attention(q, k, v, position, scale, rows=None):
     reads kv head h // (Hq // Hkv); row t sees keys 0..position+t.  ``rows``
     optionally selects a subset of the T query tokens (the result then has
     len(rows) rows).  Returns float64 [T or len(rows), Hq, D].
+
+    The tokens go through BLAS in blocks of about 768 query rows.  Within a
+    block the scores of keys past a row's last key are set to -inf (a
+    select, so stale NaN or huge keys there change nothing), and P.V runs in
+    two parts: one product over the keys every row of the block sees, then
+    each row's remaining visible keys alone, so a value past a row's last
+    key is never multiplied, not even by a zero weight.
     """
     q = np.asarray(q)
     T, Hq, D = q.shape
     Hkv = k.shape[1]
     G = Hq // Hkv
-    tokens = np.arange(T) if rows is None else np.asarray(rows)
+    tokens = np.arange(T) if rows is None else np.asarray(rows).reshape(-1)
     out = np.empty((len(tokens), Hq, D), np.float64)
     n_max = position + int(tokens.max()) + 1
+    block = max(1, 768 // G)
     for g in range(Hkv):
         k_g = np.asarray(k[:n_max, g, :], np.float64)
         v_g = np.asarray(v[:n_max, g, :], np.float64)
-        for r, t in enumerate(tokens):
-            n = position + int(t) + 1                 # keys 0..position+t only
-            q_t = np.asarray(q[t, g * G:(g + 1) * G, :], np.float64)
-            s = (q_t @ k_g[:n].T) * scale
-            s = np.exp(s - s.max(axis=1, keepdims=True))
-            out[r, g * G:(g + 1) * G, :] = (s @ v_g[:n]) / s.sum(axis=1, keepdims=True)
+        for b0 in range(0, len(tokens), block):
+            tb = tokens[b0:b0 + block]
+            last = position + tb + 1                            # keys per row
+            n_b, n_common = int(last.max()), int(last.min())
+            q_b = np.asarray(q[tb, g * G:(g + 1) * G, :], np.float64)     # [B, G, D]
+            s = (q_b @ k_g[:n_b].T) * scale                     # [B, G, n_b]
+            visible = np.arange(n_b)[None, :] < last[:, None]   # [B, n_b]
+            s = np.where(visible[:, None, :], s, -np.inf)
+            s = np.exp(s - s.max(axis=2, keepdims=True))
+            o = s[:, :, :n_common] @ v_g[:n_common]             # [B, G, D]
+            for i in np.flatnonzero(last > n_common):
+                o[i] += s[i, :, n_common:last[i]] @ v_g[n_common:last[i]]
+            out[b0:b0 + len(tb), g * G:(g + 1) * G, :] = o / s.sum(axis=2, keepdims=True)
     return out
 
 

@@ -55,48 +55,51 @@ def test_cpu_plumbing_at_its_stated_precision(gpu):
     assert rel_l2(got, want) < rel_l2(got16, want)
 
 
-SAMPLE = np.unique(np.concatenate([[0, 1, 2, 5, 2047], np.linspace(3, 2046, 27).astype(int)]))
-
-
 @pytest.mark.parametrize('kv_dtype', ['bf16', 'f16'])
 def test_prefill_chunk_full_size_float32_output(gpu, kv_dtype):
     """2048 query tokens appended to a 6144-token cache (8192 keys), causal,
-    24/4/256, inputs N(0,1) from seed 2, float32 output: every head of 32
-    sampled token rows to both bounds (bf16 caches as stated, and fp16
-    caches of the same shape).  The 16-bit output of the same call must
-    equal that float32 value up to its own rounding (half an ulp)."""
+    24/4/256, inputs N(0,1) from seed 2, float32 output: every element of
+    all 2048 token rows x 24 heads to both bounds (bf16 caches as stated,
+    and fp16 caches of the same shape), as the reference's own test compares
+    every output element (tests/test_cuda.py:218).  The 16-bit output of the
+    same call must equal that float32 value up to its own rounding (half an
+    ulp) on every element."""
     w = Workload(**{**WORKLOADS['prefill_2k'].__dict__, 'dtype': kv_dtype})
     q, k, v, _ = make_inputs(w)
     print(f'prefill 2048 at 6144, {kv_dtype}', flush=True)
     got32 = gpu_attention(w, q, k, v, gpu, fill_nan=True, out_dtype=gpu.float32)
-    want = ref.gqa_attention(to_float(q, kv_dtype), to_float(k, kv_dtype), to_float(v, kv_dtype),
-                             w.position, w.scale, rows=SAMPLE)
-    assert_parity(got32[SAMPLE], want)
     got16 = gpu_attention(w, q, k, v, gpu, fill_nan=True)
+    want = ref.gqa_attention(to_float(q, kv_dtype), to_float(k, kv_dtype), to_float(v, kv_dtype),
+                             w.position, w.scale)
+    assert want.shape == got32.shape == (2048, 24, 256)
+    assert_parity(got32, want)
     half_ulp = np.abs(want) * (2.0 ** -8 if kv_dtype == 'bf16' else 2.0 ** -11)
-    assert np.all(np.abs(got16[SAMPLE] - want) <= MAX_ABS + half_ulp)
+    assert np.all(np.abs(got16 - want) <= MAX_ABS + half_ulp)
     if kv_dtype == 'bf16':
         want16 = to_float(f32_to_bf16_bits(want.astype(np.float32)), 'bf16')
-        assert rel_l2(got16[SAMPLE], want16) <= 1e-3
+        assert rel_l2(got16, want16) <= 1e-3
 
 
 def test_prefill_chunk_full_size_precise(gpu):
     """The same chunk with an fp32 query on fp16 caches through the precise
-    entry (the reference's precision: fp32 q, fp16 cache)."""
+    entry (the reference's precision: fp32 q, fp16 cache), every element."""
     w = WORKLOADS['prefill_2k']
     rng = np.random.default_rng(w.seed)
     q = rng.standard_normal((w.tokens, w.q_heads, w.head_dim), dtype=np.float32)
     k = rng.standard_normal((w.keys, w.kv_heads, w.head_dim), dtype=np.float32).astype(np.float16)
     v = rng.standard_normal((w.keys, w.kv_heads, w.head_dim), dtype=np.float32).astype(np.float16)
     got = precise_attention(w, q, k, v, gpu)
-    want = ref.gqa_attention(q, k, v, w.position, w.scale, rows=SAMPLE)
-    assert_parity(got[SAMPLE], want)
-    assert rel_l2(got[SAMPLE], want) <= PRECISE_REL_L2
+    want = ref.gqa_attention(q, k, v, w.position, w.scale)
+    assert want.shape == got.shape == (2048, 24, 256)
+    assert_parity(got, want)
+    assert rel_l2(got, want) <= PRECISE_REL_L2
 
 
 @pytest.mark.parametrize('q_heads,kv_heads,head_dim,T,position', [
     (24, 4, 256, 1, 5000),      # decode: stream kernel
     (24, 4, 256, 2, 31),
+    (16, 2, 128, 1, 5000),      # stream kernel at head_dim 128, split + combine (fp32 query split in-kernel)
+    (8, 2, 128, 2, 3000),       # the same, two tokens of 4 query heads per KV head
     (24, 4, 256, 8, 16384),     # verify-8 at 16K: ring kernel
     (8, 2, 128, 8, 300),        # 32 rows, head_dim 128
     (16, 2, 128, 6, 777),       # 48 rows, head_dim 128
