@@ -30,6 +30,12 @@ step is begin(), one attend() per full-attention layer, end(): any failure
 between begin() and the end of end() (a library error, a device fault that
 the synchronisation in end() reports) leaves the session poisoned until
 reset() or restore(), as a failure inside the reference's evaluate() does.
+
+One addition has no counterpart in the reference: begin_prefill(batch) opens
+a non-recording step of up to 8192 tokens (a whole prompt chunk through the
+prefill kernel, where the reference's server feeds 8 tokens per evaluate(),
+qvelox/server.py:177-192).  begin() itself keeps evaluate()'s 1..8 rule and
+message.
 """
 import torch
 
@@ -39,8 +45,8 @@ from .runtime import check, library
 
 # The reference's fixed attention geometry (src/runtime.h:38-41).
 Q_HEADS, KV_HEADS, HEAD_DIM = 24, 4, 256
-# evaluate() takes 1..8 tokens (src/runtime.cu:65-67,358); a prefill chunk
-# that does not record may hold up to the fused entry's 8192 tokens.
+# evaluate() takes 1..8 tokens (src/runtime.cu:65-67,358); begin_prefill's
+# chunks (no recording) take up to the fused entry's 8192 tokens.
 MAX_BATCH, MAX_CHUNK = 8, 8192
 
 
@@ -93,12 +99,21 @@ class AttentionKV:
 
     # -- one evaluated batch ----------------------------------------------
     def begin(self, batch, recording=False):
-        """Preflight of evaluate() (src/runtime.cu:356-375); afterwards the
-        state counts as poisoned until end() returns."""
+        """Preflight of evaluate() (src/runtime.cu:356-375), with its batch
+        rule (1..8, src/runtime.cu:65-67); afterwards the state counts as
+        poisoned until end() returns."""
+        self._begin(batch, recording, MAX_BATCH, 'batch must be between 1 and 8')
+
+    def begin_prefill(self, batch):
+        """begin() for a prompt chunk of 1..8192 tokens that does not record
+        (no counterpart in the reference, whose server prefills 8 tokens per
+        evaluate()); the same preflight otherwise."""
+        self._begin(batch, False, MAX_CHUNK, 'prefill chunk must be between 1 and 8192 tokens')
+
+    def _begin(self, batch, recording, limit, message):
         self._ready()
         _require(not self.pending, 'commit or abort the pending verification first')
-        limit = MAX_BATCH if recording else MAX_CHUNK
-        _require(type(batch) is int and 1 <= batch <= limit, f'batch must be between 1 and {limit}')
+        _require(type(batch) is int and 1 <= batch <= limit, message)
         _require(self.position <= self.context - batch, 'evaluation exceeds context capacity')
         if recording:
             self.verify_position = self.position

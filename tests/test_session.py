@@ -12,12 +12,16 @@ def session():
 
 def test_preflight_refusals_leave_the_state_clean():
     kv = session()
-    with pytest.raises(SessionError, match='batch must be between 1 and 8192'):
-        kv.begin(0)
-    with pytest.raises(SessionError, match='batch must be between 1 and 8'):
-        kv.begin(9, recording=True)
+    # begin() keeps evaluate()'s rule and message (src/runtime.cu:65-67).
+    for batch, recording in ((0, False), (9, False), (9, True), (0, True)):
+        with pytest.raises(SessionError, match='^batch must be between 1 and 8$'):
+            kv.begin(batch, recording)
+    with pytest.raises(SessionError, match='prefill chunk must be between 1 and 8192 tokens'):
+        kv.begin_prefill(0)
+    with pytest.raises(SessionError, match='prefill chunk must be between 1 and 8192 tokens'):
+        kv.begin_prefill(8193)
     with pytest.raises(SessionError, match='exceeds context capacity'):
-        kv.begin(65)
+        kv.begin_prefill(65)
     with pytest.raises(SessionError, match='no pending verification'):
         kv.commit(0)
     with pytest.raises(SessionError, match='no valid checkpoint'):
@@ -49,3 +53,16 @@ def test_a_failure_inside_a_step_poisons_until_reset():
     assert (kv.position, kv.pending, kv.verify_position) == (1, 1, 0)
     kv.commit(0)
     assert (kv.position, kv.pending) == (0, 0)
+
+
+def test_prefill_chunk_bookkeeping():
+    kv = session()
+    kv.begin_prefill(40)
+    assert kv.poisoned
+    kv.end()
+    assert (kv.position, kv.pending, kv.poisoned) == (40, 0, False)
+    kv.begin(8, recording=True)
+    kv.end()
+    assert (kv.position, kv.pending) == (48, 8)
+    with pytest.raises(SessionError, match='commit or abort'):
+        kv.begin_prefill(1)

@@ -38,7 +38,10 @@ def test_session_fused_prefill_verify_commit_checkpoint_restore(gpu, first):
         return torch.from_numpy(np.ascontiguousarray(x, np.float32)).cuda()
 
     def run(T, recording=False):
-        kv.begin(T, recording)
+        if T > 8:
+            kv.begin_prefill(T)
+        else:
+            kv.begin(T, recording)
         pos = kv.position
         steps = []
         for layer in range(layers):
