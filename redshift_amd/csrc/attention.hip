@@ -629,6 +629,12 @@ void launch_split(const Shape &s, const SplitPlan &plan, Dtype dtype, bool preci
     a.splits = plan.splits;
     a.scale_log2 = scale * 1.4426950408889634f;
     a.out = out;
+    // The precise stream kernel reads q as the fp32 query and splits it
+    // itself; hi + lo parts (q_lo set) are for the ring and prefill kernels.
+    require(!(precise && plan.kind == SplitKind::Stream && q_lo != nullptr),
+            "the precise stream kernel takes the fp32 query, not its hi + lo parts");
+    require(!(precise && plan.kind == SplitKind::Ring && q_lo == nullptr),
+            "the precise ring kernel takes the query's hi + lo parts");
     int out_mode = kOutPartials;
     if (plan.direct) {
         require(out != nullptr && plan.splits == 1, "a direct split plan writes the output");
