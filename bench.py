@@ -65,14 +65,16 @@ def make_layers(torch, A, w, layers, seed):
     return caches, queries
 
 
-def time_workload(torch, A, w, layers, steps, warmup, seed):
+def time_workload(torch, A, w, layers, steps, warmup, seed, sample=None):
     """Times `steps` steps of `layers` attention calls.
 
     Returns dict(ms_per_step: one step replayed as a captured HIP graph,
-    eager_ms_per_step: the same launches issued one by one, split_us: median
-    duration of the split-K (or prefill) kernel from events recorded around
-    each of its launches in the eager loop, on the stream it runs on, and
-    split_us_mean: their mean)."""
+    eager_ms_per_step: the same launches issued one by one, replay_ms: each
+    timed replay, split_us: median duration of the split-K (or prefill)
+    kernel from events recorded around each of its launches in the eager
+    loop, on the stream it runs on, and split_us_mean: their mean).  With
+    `sample`, also its results right before and right after the timed
+    replays (device_before, device_after)."""
     caches, queries = make_layers(torch, A, w, layers, seed)
     ws = A.workspace(A.attention_workspace_bytes(w.q_heads, w.kv_heads, w.head_dim, w.tokens, w.position))
     outs = [torch.empty_like(q) for q in queries]
@@ -123,7 +125,19 @@ def time_workload(torch, A, w, layers, steps, warmup, seed):
     torch.cuda.current_stream().wait_stream(capture_stream)
     for _ in range(warmup):
         graph.replay()
-    graph_ms = timed(lambda s: graph.replay(), steps)
+    # One event pair per replay as well (recorded between replays, outside
+    # the graph): the spread of the step time over the timed steps.
+    replay_ev = [[torch.cuda.Event(enable_timing=True) for _ in range(2)] for _ in range(steps)]
+
+    def replay(s):
+        replay_ev[s][0].record()
+        graph.replay()
+        replay_ev[s][1].record()
+
+    device_before = sample() if sample else None
+    graph_ms = timed(replay, steps)
+    device_after = sample() if sample else None
+    replay_ms = [e[0].elapsed_time(e[1]) for e in replay_ev]
     del graph
     split_graph_us = None
     if one_chunk:
@@ -145,9 +159,110 @@ def time_workload(torch, A, w, layers, steps, warmup, seed):
         del sgraph
     del caches
     torch.cuda.empty_cache()
-    return dict(ms_per_step=graph_ms, eager_ms_per_step=eager_ms,
+    return dict(ms_per_step=graph_ms, eager_ms_per_step=eager_ms, replay_ms=replay_ms,
+                device_before=device_before, device_after=device_after,
                 split_us=1000.0 * statistics.median(split_ms), split_us_mean=1000.0 * sum(split_ms) / len(split_ms),
                 split_graph_us=split_graph_us)
+
+
+def sha256_of(paths):
+    """SHA-256 over the given files' bytes, in order, or None if one is missing."""
+    import hashlib
+    h = hashlib.sha256()
+    try:
+        for path in paths:
+            h.update(path.read_bytes())
+    except OSError:
+        return None
+    return h.hexdigest()
+
+
+def git_head():
+    """The checked-out commit, read from .git as plain files (None where the
+    tree was copied without it)."""
+    try:
+        head = (ROOT / '.git' / 'HEAD').read_text().strip()
+        if head.startswith('ref: '):
+            ref = head[5:]
+            path = ROOT / '.git' / ref
+            if path.exists():
+                return path.read_text().strip()
+            for line in (ROOT / '.git' / 'packed-refs').read_text().splitlines():
+                if line.endswith(' ' + ref):
+                    return line.split()[0]
+            return None
+        return head
+    except OSError:
+        return None
+
+
+def gpu_card(torch):
+    """The DRM card of cuda:0, matched by PCI domain and bus, or None."""
+    props = torch.cuda.get_device_properties(0)
+    want = (getattr(props, 'pci_domain_id', None), getattr(props, 'pci_bus_id', None))
+    for card in sorted(Path('/sys/class/drm').glob('card[0-9]*')):
+        if '-' in card.name:
+            continue
+        try:
+            pci = os.path.basename(os.path.realpath(card / 'device'))   # dddd:bb:dd.f
+            domain, bus = (int(x, 16) for x in pci.split(':')[:2])
+        except (OSError, ValueError):
+            continue
+        if (domain, bus) == want:
+            return card
+    return None
+
+
+def gpu_clocks(card):
+    """The state of cuda:0, read as plain files (no subprocess): the current
+    DPM level of pp_dpm_sclk, pp_dpm_mclk and pp_dpm_fclk (the starred line),
+    and the hwmon readings (temperatures in C, clocks in MHz, power in W)."""
+    clocks = {}
+    if card is None:
+        return clocks
+    for name in ('sclk', 'mclk', 'fclk'):
+        try:
+            lines = (card / 'device' / f'pp_dpm_{name}').read_text().splitlines()
+        except OSError:
+            continue
+        current = [line.split(':', 1)[1].replace('*', '').strip() for line in lines if line.rstrip().endswith('*')]
+        clocks[name] = current[0] if current else None
+    for hwmon in sorted((card / 'device' / 'hwmon').glob('hwmon*')):
+        for path in sorted(hwmon.glob('*_input')) + sorted(hwmon.glob('power*_average')):
+            kind = path.name.split('_')[0]
+            try:
+                label = (hwmon / f'{kind}_label').read_text().strip()
+            except OSError:
+                label = kind
+            try:
+                raw = int(path.read_text().strip())
+            except (OSError, ValueError):
+                continue
+            scale = 1e-3 if kind.startswith('temp') else 1e-6
+            clocks[f'{label}_{path.name.split("_", 1)[1]}'] = round(raw * scale, 1)
+    return clocks
+
+
+def provenance(torch, lib_path):
+    """What the line was measured with: the library's and the sources'
+    SHA-256, the commit where known, the device and its clock levels."""
+    sources = sorted((ROOT / 'redshift_amd' / 'csrc').glob('*')) + sorted((ROOT / 'include').glob('*.h')) + \
+        sorted((ROOT / 'redshift_amd').glob('*.py')) + [ROOT / 'bench.py']
+    props = torch.cuda.get_device_properties(0)
+    card = gpu_card(torch)
+    return {'library_sha256': sha256_of([Path(lib_path)]), 'sources_sha256': sha256_of(sources),
+            'sources': 'redshift_amd/csrc/*, include/*.h, redshift_amd/*.py, bench.py',
+            'git_head': git_head(), 'device': props.name, 'arch': props.gcnArchName,
+            'cus': props.multi_processor_count, 'torch': torch.__version__,
+            'hip': getattr(torch.version, 'hip', None),
+            'drm_card': card.name if card is not None else None}
+
+
+def spread(values_ms, layers):
+    """min / median / max of per-replay step times, in us per layer."""
+    us = sorted(1000.0 * v / layers for v in values_ms)
+    return {'min': round(us[0], 2), 'median': round(statistics.median(us), 2), 'max': round(us[-1], 2),
+            'replays': len(us)}
 
 
 def measured_traffic():
@@ -172,6 +287,86 @@ def copy_probe(mib, repeats=5):
         dst.copy_(src)
     torch.cuda.synchronize()
     log(f'copy probe: {repeats} x {mib} MiB device-to-device copies')
+
+
+def read_probe(torch, A, w, sets=16, rounds=20, ahead=3):
+    """The plain read of one split-K launch's KV pages (rsp_read_pages in
+    libredshift_probe.so): the grid, runs and page addresses of
+    attention_ring for workload `w` (57 splits x 4 KV heads for verify8_16k),
+    non-temporal 16-byte loads, no arithmetic.  `sets` caches of the
+    workload's size rotate, so that the 256 MB Infinity Cache holds none of
+    the pages a launch reads (16 x 67 MB).  Each launch is timed by an event
+    pair, in graphs of `sets` launches replayed `rounds` times; returns the
+    median and mean us per launch and the read rate of the algorithmic bytes."""
+    import ctypes as ct
+
+    from redshift_amd.build import PROBE_LIBRARY
+    from redshift_amd.runtime import library
+    probe = ct.CDLL(str(PROBE_LIBRARY))
+    probe.rsp_read_pages.argtypes = [ct.c_void_p, ct.c_void_p] + [ct.c_int] * 6 + [ct.c_void_p, ct.c_void_p]
+    probe.rsp_read_pages.restype = ct.c_int
+    lib = library()
+    capacity = A.round_capacity(w.keys)
+    caches = [A.PagedKV(w.kv_heads, w.head_dim, capacity, torch.float16) for _ in range(sets)]
+    for c in caches:
+        c.k.normal_()
+        c.v.normal_()
+    # The split plan of the workload's own launch: its workspace is
+    # kv_heads x splits x rows x (head_dim + 2) floats of partials.
+    rows = w.group * w.tokens
+    per_split = w.kv_heads * rows * (w.head_dim + 2) * 4
+    ws = A.attention_workspace_bytes(w.q_heads, w.kv_heads, w.head_dim, w.tokens, w.position)
+    assert rows <= A.MAX_CHUNK_ROWS and ws % per_split == 0, 'not a one-launch split-K workload'
+    n_pages, splits = -(-w.keys // 32), ws // per_split
+    sink = torch.zeros(splits * w.kv_heads * 512, dtype=torch.int32, device='cuda')
+    ev = [[torch.cuda.Event(enable_timing=True) for _ in range(2)] for _ in range(sets * rounds)]
+
+    def launch(c):
+        stream = torch.cuda.current_stream().cuda_stream
+        rc = probe.rsp_read_pages(c.k.data_ptr(), c.v.data_ptr(), w.kv_heads, w.head_dim, capacity, n_pages,
+                                  splits, ahead, sink.data_ptr(), stream)
+        assert rc == 0, 'rsp_read_pages refused its arguments'
+
+    for c in caches:
+        launch(c)
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    capture_stream = torch.cuda.Stream()
+    capture_stream.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(capture_stream):
+        with torch.cuda.graph(graph, stream=capture_stream):
+            for c in caches:
+                launch(c)
+    torch.cuda.current_stream().wait_stream(capture_stream)
+    graph.replay()
+    torch.cuda.synchronize()
+    start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    start.record()
+    for _ in range(rounds):
+        graph.replay()
+    end.record()
+    torch.cuda.synchronize()
+    us_graph = 1000 * start.elapsed_time(end) / (rounds * sets)
+    # The same launches one by one, an event pair around each.
+    for i in range(sets * rounds):
+        ev[i][0].record()
+        launch(caches[i % sets])
+        ev[i][1].record()
+    torch.cuda.synchronize()
+    us = sorted(1000 * e[0].elapsed_time(e[1]) for e in ev)
+    del graph, caches, lib
+    torch.cuda.empty_cache()
+    page_bytes = 2 * w.kv_heads * n_pages * 32 * w.head_dim * 2
+    med = statistics.median(us)
+    return {'workload': w.name, 'grid': f'{splits} splits x {w.kv_heads} KV heads, 512 threads',
+            'pages_per_head': n_pages, 'pages_in_flight': ahead, 'buffer_sets': sets,
+            'us_per_launch_in_graph': round(us_graph, 2), 'us_per_launch_median': round(med, 2),
+            'us_per_launch_min': round(us[0], 2),
+            'GB/s': round(w.kv_bytes() / (us_graph * 1e-6) / 1e9, 1),
+            'frac_hbm': round(w.kv_bytes() / (us_graph * 1e-6) / 1e9 / HBM_PEAK_GBS, 4),
+            'algorithmic_bytes': w.kv_bytes(), 'page_bytes': page_bytes,
+            'what': 'plain non-temporal read of the pages one split-K launch of the workload streams; '
+                    'GB/s and frac_hbm over the algorithmic K+V bytes and the in-graph time per launch'}
 
 
 def drop_in_rate(lib, cases=((1, 139263), (8, 16384), (1, 4095)), repeats=5):
@@ -376,6 +571,10 @@ def main():
                     help='only time the host-buffer qv_test_attention (PCIe-inclusive) and exit')
     ap.add_argument('--copy-probe', type=int, metavar='MIB',
                     help='only run a plain MIB-MiB device copy (counter calibration) and exit')
+    ap.add_argument('--read-probe', nargs='?', const='verify8_16k', metavar='WORKLOAD',
+                    help='only time the plain read of the KV pages one split-K launch of WORKLOAD '
+                         '(default verify8_16k) streams, and exit')
+    ap.add_argument('--ahead', type=int, default=3, help='--read-probe: pages of loads in flight per wave (1-4)')
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get('WORLD_SIZE', '1')) != 1:
         print('bench.py measures one GPU only: the attention path runs on a single MI355X; '
@@ -394,6 +593,10 @@ def main():
         copy_probe(args.copy_probe)
         return
     lib = load_library()
+    if args.read_probe:
+        print(json.dumps({'read_probe': read_probe(torch, A, WORKLOADS[args.read_probe], ahead=args.ahead)}),
+              flush=True)
+        return
     if args.drop_in:
         print(json.dumps({'drop_in': 'qv_test_attention, host buffers, median of 5 after 1 warm-up',
                           'cases': drop_in_rate(lib)}), flush=True)
@@ -401,7 +604,12 @@ def main():
 
     w = WORKLOADS['decode_139k']
     log(f'decode_139k: {args.layers} layers x {w.keys} keys, steps={args.steps} warmup={args.warmup}')
-    r = time_workload(torch, A, w, args.layers, args.steps, args.warmup, seed=3)
+    prov = provenance(torch, lib._name)
+    card = gpu_card(torch)
+    r = time_workload(torch, A, w, args.layers, args.steps, args.warmup, seed=3, sample=lambda: gpu_clocks(card))
+    prov['device_before'], prov['device_after'] = r['device_before'], r['device_after']
+    prov['device_is'] = ('sysfs DPM levels and hwmon readings of the GPU right before and right after '
+                         'the timed graph replays of decode_139k')
     step_bytes = args.layers * w.kv_bytes()
     gbs = step_bytes / (r['ms_per_step'] * 1e-3) / 1e9
     split_gbs = w.kv_bytes() / (r['split_us'] * 1e-6) / 1e9
@@ -426,6 +634,9 @@ def main():
                      'frac_step': round(gbs / HBM_PEAK_GBS, 4),
                      'frac_is': 'frac: the split-K kernel alone (kernel_us); frac_step: the whole layer, '
                                 'split-K + combine kernels in the graph step (us_per_layer)'},
+        'step_spread': {**spread(r['replay_ms'], args.layers),
+                        'what': 'us per layer of each timed graph replay (an event pair around each)'},
+        'provenance': prov,
     }
     chosen = [] if args.no_extra else [x for x in args.extras.split(',') if x]
     if chosen:
@@ -438,6 +649,7 @@ def main():
             rx = time_workload(torch, A, wx, args.layers, args.steps, args.warmup, seed=1)
             us = 1000 * rx['ms_per_step'] / args.layers
             extra[name] = {'us_per_layer': round(us, 2),
+                           'step_spread': spread(rx['replay_ms'], args.layers),
                            'GB/s': round(wx.kv_bytes() / (us * 1e-6) / 1e9, 1),
                            'eager_us_per_layer': round(1000 * rx['eager_ms_per_step'] / args.layers, 2),
                            'split_kernel_us': round(rx['split_us'], 2),

@@ -1,0 +1,97 @@
+// Measurement probes (libredshift_probe.so, loaded by bench.py only; no
+// attention entry point depends on it).
+//
+// rsp_read_pages: the plain read of the KV pages that one split-K launch
+// streams, with no arithmetic and no stores beyond one word per workgroup.
+// Workgroup (h, split) of a grid of splits x kv_heads reads the same
+// contiguous run of K and V pages of KV head h as attention_ring's workgroup
+// of that index (runs of n_pages * split / splits pages), 512 threads, every
+// wave 1 KiB pieces of each [K page | V page] with non-temporal 16-byte
+// loads, `ahead` pages of loads in flight before the first is consumed.  Its
+// time is the floor under any kernel that reads those bytes with that grid.
+#include <hip/hip_runtime.h>
+
+#include <cstddef>
+#include <cstdint>
+
+namespace {
+
+constexpr int kThreads = 512, kWaves = kThreads / 64;
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+
+template <int D, int AHEAD>
+__global__ __launch_bounds__(kThreads, 1)
+void read_pages(const u32x4 *k_pages, const u32x4 *v_pages, size_t head_stride, int n_pages, int splits,
+                uint32_t *sink) {
+    constexpr int PAGE = 32 * D * 2 / 16;             // 16-byte pieces of one K (or V) page
+    constexpr int PER = 2 * PAGE / kThreads;          // pieces of [K | V] per thread per page
+    static_assert(PER * kThreads == 2 * PAGE, "pieces divide over the threads");
+    const int split = blockIdx.x % splits, h = blockIdx.x / splits;
+    const int p0 = (int)((long long)split * n_pages / splits), p1 = (int)((long long)(split + 1) * n_pages / splits);
+    const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+    const u32x4 *kh = k_pages + (size_t)h * head_stride / 8, *vh = v_pages + (size_t)h * head_stride / 8;
+    // Piece c of a page (64 lanes x 16 B = 1 KiB per wave): K for the first
+    // PAGE pieces, V after them; wave w takes pieces w*PER*64 .. +PER*64-1.
+    auto piece = [&](int p, int c) {
+        const int e = (w * PER + c) * 64 + lane;
+        return e < PAGE ? kh + (size_t)p * PAGE + e : vh + (size_t)p * PAGE + (e - PAGE);
+    };
+    u32x4 acc = {0u, 0u, 0u, 0u};
+    u32x4 buf[AHEAD][PER];
+    // Prologue: the first AHEAD pages in flight (pages past the run re-read
+    // the run's first page and are not counted).
+#pragma unroll
+    for (int a = 0; a < AHEAD; ++a) {
+        const int p = p0 + a < p1 ? p0 + a : p0;
+#pragma unroll
+        for (int c = 0; c < PER; ++c) buf[a][c] = __builtin_nontemporal_load(piece(p, c));
+    }
+    for (int i = 0; i < p1 - p0; i += AHEAD) {
+#pragma unroll
+        for (int a = 0; a < AHEAD; ++a) {
+            if (i + a < p1 - p0) {
+#pragma unroll
+                for (int c = 0; c < PER; ++c) acc ^= buf[a][c];
+            }
+            const int next = p0 + i + a + AHEAD;
+            if (next < p1) {
+#pragma unroll
+                for (int c = 0; c < PER; ++c) buf[a][c] = __builtin_nontemporal_load(piece(next, c));
+            }
+        }
+    }
+    const uint32_t x = acc[0] ^ acc[1] ^ acc[2] ^ acc[3];
+    // A store that depends on every load (the data decide it), so no load is
+    // dropped; it is never taken for the zero-filled or random pages read here
+    // unless their xor happens to equal the constant.
+    if (x == 0x9e3779b9u) sink[blockIdx.x * kThreads + threadIdx.x] = x;
+}
+
+template <int D>
+const void *pick(int ahead) {
+    switch (ahead) {
+        case 1: return (const void *)&read_pages<D, 1>;
+        case 2: return (const void *)&read_pages<D, 2>;
+        case 3: return (const void *)&read_pages<D, 3>;
+        case 4: return (const void *)&read_pages<D, 4>;
+    }
+    return nullptr;
+}
+
+}  // namespace
+
+// The caches as PagedKV holds them: kv_heads runs of `capacity` tokens of
+// head_dim 16-bit elements each, K and V apart.  sink: splits * kv_heads *
+// 512 words.  Returns 0, or -1 for arguments outside the probe's range.
+extern "C" int rsp_read_pages(const void *k_pages, const void *v_pages, int kv_heads, int head_dim, int capacity,
+                              int n_pages, int splits, int ahead, void *sink, void *stream) {
+    if (!k_pages || !v_pages || !sink || kv_heads < 1 || splits < 1 || n_pages < splits ||
+        (long long)n_pages * 32 > capacity || capacity % 32 || ahead < 1 || ahead > 4)
+        return -1;
+    const void *kernel = head_dim == 256 ? pick<256>(ahead) : head_dim == 128 ? pick<128>(ahead) : nullptr;
+    if (!kernel) return -1;
+    size_t head_stride = (size_t)capacity * head_dim;
+    void *args[] = {&k_pages, &v_pages, &head_stride, &n_pages, &splits, &sink};
+    return hipLaunchKernel(kernel, dim3(splits * kv_heads), dim3(kThreads), args, 0,
+                           static_cast<hipStream_t>(stream)) == hipSuccess ? 0 : -1;
+}
