@@ -161,7 +161,7 @@ size_t fused_partials_bytes(int batch, int position) {
     size_t parts = rs::attention_workspace_bytes(s, rs::Dtype::F16, true);
     if (batch <= rs::kMaxFusedSplitTokens && position >= 1)
         parts = std::max(parts, rs::fused_tokens_workspace_bytes(batch, position));
-    return parts;
+    return std::max(parts, rs::prefill_prep_workspace_bytes(batch, position));
 }
 
 // The reference's k_attention on device buffers of the 24/4/256 model.  A
@@ -169,12 +169,16 @@ size_t fused_partials_bytes(int batch, int position) {
 // does everything.  Up to 8 tokens after at least one cached key (decode,
 // verification): two launches, the split kernel preparing the query and
 // appending the new keys and values, the combine merging (and, for one or
-// two tokens, adding the new keys).  A prefill chunk (more than 8 tokens):
-// the prepare kernel writes the query's hi + lo parts to q_hilo
-// (2 * batch * 24 * 256 fp16) and appends the new K/V to the pages, then
-// attention (with the sigmoid gate) runs on them; its workgroups read new
-// keys that other workgroups would append, so the append stays a launch of
-// its own.
+// two tokens, adding the new keys).  A short prefill chunk (more than 8
+// tokens whose keys fit four pages from the one holding key `position`):
+// the prepared prefill, whose workgroups prepare their query rows, its
+// cached runs attend to keys 0 .. position-1 and one split per row
+// workgroup prepares, appends and attends to the chunk's keys, then the
+// gated combine.  A longer chunk: the prepare kernel writes the query's hi +
+// lo parts to q_hilo (2 * batch * 24 * 256 fp16) and appends the new K/V to
+// the pages, then attention (with the sigmoid gate) runs on them: its
+// workgroups read new keys that other workgroups would append, so the append
+// stays a launch of its own there.
 void fused_attention(float *out, void *k_pages, void *v_pages, const float *q_gate, const float *key,
                      const float *value, const float *q_norm, const float *k_norm, int batch,
                      int position, int capacity, float epsilon, uint16_t *q_hilo, void *partials,
@@ -182,8 +186,8 @@ void fused_attention(float *out, void *k_pages, void *v_pages, const float *q_ga
     require(partials_bytes >= fused_partials_bytes(batch, position), "workspace too small");
     constexpr int H = rs::kModelQHeads, HKV = rs::kModelKvHeads, D = rs::kModelHeadDim;
     const bool short_context = batch <= rs::kShortMaxTokens && position + batch <= rs::kShortFusedKeys;
-    if (short_context || (batch <= rs::kMaxFusedSplitTokens && position >= 1)) {
-        rs::FusedToken tok;
+    auto fused_token = [&] {
+        rs::FusedToken tok = {};
         tok.q_gate = q_gate;
         tok.key = key;
         tok.value = value;
@@ -195,8 +199,18 @@ void fused_attention(float *out, void *k_pages, void *v_pages, const float *q_ga
         tok.epsilon = epsilon;
         tok.position = position;
         tok.tokens = batch;
-        if (short_context) rs::launch_fused_short(tok, out, stream);
-        else rs::launch_fused_tokens(tok, capacity, partials, out, stream);
+        return tok;
+    };
+    if (short_context) {
+        rs::launch_fused_short(fused_token(), out, stream);
+        return;
+    }
+    if (batch <= rs::kMaxFusedSplitTokens && position >= 1) {
+        rs::launch_fused_tokens(fused_token(), capacity, partials, out, stream);
+        return;
+    }
+    if (rs::prefill_prep_fits(batch, position)) {
+        rs::launch_prefill_prep(fused_token(), out, partials, stream);
         return;
     }
     const rs::Shape s{H, HKV, D, batch, position, capacity};

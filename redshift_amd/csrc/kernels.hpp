@@ -198,6 +198,22 @@ void launch_prefill(const Shape &s, Dtype dtype, bool precise, float scale, cons
                     const void *q_lo, const void *k_pages, const void *v_pages, void *out, bool out_f32,
                     const float *gate, void *workspace, hipStream_t stream);
 
+// The fused prefill chunk of tok.tokens new tokens (more than
+// kMaxFusedSplitTokens) whose keys fit kPrepNewKeyPages pages from the one
+// holding key tok.position (prefill_prep_fits), in at most two launches and
+// no prepare launch: attention_prefill_prep's workgroups prepare their own
+// query rows (RMSNorm, gamma, RoPE, hi + lo parts) and attend to runs of the
+// cached keys 0 .. position-1 (split as plan_prefill_for splits a call's
+// pages); the last run then prepares the chunk's keys into its LDS rings
+// (its workgroup 0 appends them) and attends to them; the gated combine
+// merges the runs (none for one run).  plan_prefill_prep_for gives the plan
+// on `cus` CUs; the workspace holds the fp32 partials.
+constexpr int kPrepNewKeyPages = 4;
+bool prefill_prep_fits(int tokens, int position);
+PrefillPlan plan_prefill_prep_for(int tokens, int position, int cus);
+size_t prefill_prep_workspace_bytes(int tokens, int position);
+void launch_prefill_prep(const FusedToken &tok, float *out, void *workspace, hipStream_t stream);
+
 // Whole pages 0 .. pages-1 of every KV head, K and V, from caches of
 // src_capacity tokens to caches of dst_capacity tokens (checkpoint/restore).
 void launch_copy(void *dst_k, void *dst_v, const void *src_k, const void *src_v, int kv_heads,

@@ -27,6 +27,21 @@ __device__ __forceinline__ void global_load16(V &v, const void *p) {
     asm volatile("global_load_dwordx4 %0, %1, off" : "=v"(v) : "v"(p) : "memory");
 }
 
+// A 4-byte global load that the compiler does not track (like
+// global_load16), and a 2- or 4-byte LDS write that it does not order
+// against the rings' direct loads (like lds_read); both are awaited
+// explicitly.
+__device__ __forceinline__ void global_load4(float &v, const float *p) {
+    asm volatile("global_load_dword %0, %1, off" : "=v"(v) : "v"(p) : "memory");
+}
+__device__ __forceinline__ void lds_write4(uint32_t addr, float v) {
+    asm volatile("ds_write_b32 %0, %1" : : "v"(addr), "v"(v) : "memory");
+}
+__device__ __forceinline__ void lds_write2(uint32_t addr, _Float16 v) {
+    const unsigned u = __builtin_bit_cast(unsigned short, v);
+    asm volatile("ds_write_b16 %0, %1" : : "v"(addr), "v"(u) : "memory");
+}
+
 // LDS byte address of a __shared__ object.
 __device__ __forceinline__ uint32_t lds_addr(const void *p) {
     return (uint32_t)(uintptr_t)(__attribute__((address_space(3))) const void *)p;

@@ -123,6 +123,12 @@ struct PrefillArgs {
     float *part_o;
     float *part_ml;
     int splits;
+    // A fused prefill chunk that prepares its own query and keys
+    // (attention_prefill_prep): the prepare kernel's inputs besides q_gate
+    // (`gate`), and the chunk's token count.
+    const float *key, *value, *q_norm, *k_norm;
+    float epsilon;
+    int tokens;
 };
 
 __device__ __forceinline__ int v_slot_token(int g, int j) {
@@ -142,9 +148,18 @@ __device__ __forceinline__ int v_slot_token(int g, int j) {
 // the two passes of the two-pass instance (eight waves over ROWS = 192 rows:
 // pass 0 gives waves 0-3 the round-0 tiles and waves 4-7 the round-1 tiles,
 // pass 1 gives waves 0-3 the round-2 tiles and waves 4-7 none).
-template <int D, typename KV, typename VT, bool PSPLIT, bool QSPLIT, int MODE, int ROWS, int PASS = -1>
+// PREP (attention_prefill_prep, the fused chunk of 9 .. 128 - position % 32
+// tokens): the query rows are prepared here from q_gate (RMSNorm, gamma,
+// RoPE, hi + lo parts); the splits are runs over the cached keys 0 ..
+// position-1, which every row sees, and the last run then attends to the
+// chunk's own keys as well: it prepares them into its LDS rings (the prepare
+// kernel's functions, so the same bits) and its workgroup 0 appends them to
+// the pages.  No workgroup reads a key that another one appends.
+// (PREP: qn_stage is 1 KiB of LDS per wave, for the q_norm weights.)
+template <int D, typename KV, typename VT, bool PSPLIT, bool QSPLIT, int MODE, int ROWS, int PASS = -1,
+          bool PREP = false>
 __device__ __forceinline__ void prefill_rows(const PrefillArgs &a, KV *kring, VT *vring, const void *v_pages,
-                                             size_t v_head_stride) {
+                                             size_t v_head_stride, float *qn_stage = nullptr) {
     using V8 = typename Vec8<KV>::type;
     using OUT = std::conditional_t<MODE == kOutSame, KV, float>;
     typedef uint32_t U4 __attribute__((ext_vector_type(4)));
@@ -152,6 +167,9 @@ __device__ __forceinline__ void prefill_rows(const PrefillArgs &a, KV *kring, VT
     using PV8 = typename Vec8<PT>::type;
     constexpr int kPWaves = PASS < 0 ? ROWS / 16 : 8;
     static_assert(PASS < 0 || ROWS == 3 * 4 * 16, "two passes of eight waves over three rounds of tiles");
+    static_assert(!PREP || (D == kModelHeadDim && QSPLIT && PSPLIT && MODE == kOutGated && PASS < 0 &&
+                            std::is_same<KV, _Float16>::value && std::is_same<VT, _Float16>::value),
+                  "the prepared chunk is the fused model's: fp32 query as hi + lo parts, gated output");
     constexpr int KS = D / 32, DT = D / 16;
     constexpr int PAGE = 32 * D;                       // elements of one K (or V) page
     constexpr int PAGE_BYTES = PAGE * 2;
@@ -179,6 +197,8 @@ __device__ __forceinline__ void prefill_rows(const PrefillArgs &a, KV *kring, VT
     const int R = a.rows;
     const int rest = blockIdx.x / a.kv_heads;
     const int j = rest % a.n_tiles, split = rest / a.n_tiles;
+    // PREP: the last run attends to the chunk's keys too (uniform per workgroup).
+    const bool new_keys = PREP && split == a.splits - 1;
     static_assert(kPWaves % 4 == 0 && kPWaves / 4 <= 3, "one to three rounds of four waves");
     const int T = (R + 15) / 16, K = 4 * a.n_tiles, slot = 4 * j + (w & 3);
     const int round = PASS == 1 ? (w < 4 ? 2 : 3) : w >> 2;   // round 3: no tile
@@ -197,39 +217,71 @@ __device__ __forceinline__ void prefill_rows(const PrefillArgs &a, KV *kring, VT
     // every page in flight before their first use.)
     V8 qf[KS], qlo[QSPLIT ? KS : 1];
     int limit;
+    [[maybe_unused]] int row_token;
+    // PREP: the row's fp32 query in the same layout (k-step ks: two float4),
+    // and the q_norm weights as the prepare kernel holds them (lane l: dims
+    // 64i + l); prepared once they have landed (prep_query).
+    [[maybe_unused]] f32x4 qx[PREP ? KS : 1][2];
+    [[maybe_unused]] float gw[4];
+    [[maybe_unused]] int qpos = 0, tile_pos = 0;
     {
         const int row = min(max(row0 + (lane & 15), 0), max(row_end, 1) - 1);
         const int t = row / a.group, gg = row - t * a.group;
-        limit = a.position + t;
-        const KV *src = static_cast<const KV *>(a.q) +
-                        ((size_t)t * a.q_heads + (size_t)h * a.group + gg) * D + 8 * g;
+        // PREP's cached runs: every row sees every cached key.
+        row_token = t;
+        limit = PREP ? a.position - 1 : a.position + t;
+        if constexpr (PREP) {
+            qpos = a.position + t;
+            // The position of the tile's first (clamped) row's token; the
+            // tile's rows span at most four tokens (16 rows of 6 heads).
+            tile_pos = a.position + min(max(row0, 0), max(row_end, 1) - 1) / a.group;
+            const float *src = a.gate + ((size_t)t * a.q_heads + (size_t)h * a.group + gg) * 2 * D + 8 * g;
 #pragma unroll
-        for (int ks = 0; ks < KS; ++ks) global_load16(qf[ks], src + 32 * ks);
-        if constexpr (QSPLIT) {
-            const KV *lo = static_cast<const KV *>(a.q_lo) + (src - static_cast<const KV *>(a.q));
+            for (int ks = 0; ks < KS; ++ks) {
+                global_load16(qx[ks][0], src + 32 * ks);
+                global_load16(qx[ks][1], src + 32 * ks + 4);
+            }
 #pragma unroll
-            for (int ks = 0; ks < KS; ++ks) global_load16(qlo[ks], lo + 32 * ks);
+            for (int i = 0; i < 4; ++i) global_load4(gw[i], a.q_norm + 64 * i + lane);
+        } else {
+            const KV *src = static_cast<const KV *>(a.q) +
+                            ((size_t)t * a.q_heads + (size_t)h * a.group + gg) * D + 8 * g;
+#pragma unroll
+            for (int ks = 0; ks < KS; ++ks) global_load16(qf[ks], src + 32 * ks);
+            if constexpr (QSPLIT) {
+                const KV *lo = static_cast<const KV *>(a.q_lo) + (src - static_cast<const KV *>(a.q));
+#pragma unroll
+                for (int ks = 0; ks < KS; ++ks) global_load16(qlo[ks], lo + 32 * ks);
+            }
         }
     }
     // Keys this workgroup can see: 0 .. position + (token of its last row:
     // the last valid row of tile T-1-4j, or in the second pass of tile
     // T-3K+4j+3; none when that tile is padding).
+    // (PREP: the cached keys 0 .. position-1 first.)
     const int last_tile = PASS == 1 ? T - 3 * K + 4 * j + 3 : T - 1 - 4 * j;
-    const int n_keys = last_tile < 0 ? 0 : a.position + (min(16 * (last_tile + 1), R) - 1) / a.group + 1;
+    const int wg_keys = last_tile < 0 ? 0 : a.position + (min(16 * (last_tile + 1), R) - 1) / a.group + 1;
+    int n_keys = PREP && last_tile >= 0 ? a.position : wg_keys;
     const int n = (n_keys + 31) / 32;
     // This split's pages: p0 + i for i = 0 .. nl-1 (local index i, ring
     // buffer i % 4).  nl is uniform over the workgroup; nl = 0 leaves empty
     // partials (no keys: sum 0, rows 0).
     const int sp = (n + a.splits - 1) / a.splits;
-    const int p0 = split * sp;
-    const int nl = max(0, min(n, p0 + sp) - p0);
+    int p0 = split * sp;
+    int nl = max(0, min(n, p0 + sp) - p0);
     // Pages of this wave: those its last valid row sees (none without one).
     const int wave_last = min(row0 + 15, row_end - 1);
-    const int n_wave = wave_last >= max(row0, 0) ? (a.position + wave_last / a.group + 1 + 31) / 32 : 0;
-    const int nw = min(max(n_wave - p0, 0), nl);
+    const int wave_keys = wave_last < max(row0, 0) ? 0 : a.position + wave_last / a.group + 1;
+    int nw = min(max((PREP && wave_keys ? n : (wave_keys + 31) / 32) - p0, 0), nl);
     // Pages from which on some row of this wave masks keys (every row sees
-    // the keys up to position + its first row's token).
-    const int wave_first_limit = a.position + max(row0, 0) / a.group;
+    // the keys up to position + its first row's token; PREP's cached keys:
+    // up to position - 1).  Keys before key_lo are masked too (PREP's
+    // chunk keys: the cached ones of their first page).
+    int wave_first_limit = PREP ? a.position - 1 : a.position + max(row0, 0) / a.group;
+    int key_lo = 0;
+    // PREP: pages come from the LDS rings as the workgroup prepared them
+    // (the chunk's keys) rather than from global memory.
+    [[maybe_unused]] bool from_lds = false;
 
     const KV *kh = static_cast<const KV *>(a.k_pages) + (size_t)h * a.head_stride;
     const VT *vh = static_cast<const VT *>(v_pages) + (size_t)h * v_head_stride;
@@ -237,7 +289,7 @@ __device__ __forceinline__ void prefill_rows(const PrefillArgs &a, KV *kring, VT
     // the ring's buffer i % 4.  Over a run the pages are requested in the
     // order K0 V0 K1 V1 K2 V2 ..., which the waits below count on.
     auto stage = [&](const auto *src, int i, auto *ring) __attribute__((always_inline)) {
-        if (w >= kLoaders) return;
+        if (w >= kLoaders || from_lds) return;
         const auto *page = src + (size_t)(p0 + i) * PAGE + w * H * 512;       // uniform
         auto *buf = ring + (i & 3) * PAGE + w * H * 512;
 #pragma unroll
@@ -310,11 +362,13 @@ __device__ __forceinline__ void prefill_rows(const PrefillArgs &a, KV *kring, VT
         float x[8];
 #pragma unroll
         for (int j = 0; j < 8; ++j) x[j] = s[j >> 2][j & 3] * a.scale_log2;
-        if (key0 + 31 > wave_first_limit) {
+        if (key0 + 31 > wave_first_limit || (PREP && key0 < key_lo)) {
             keep_branch();
 #pragma unroll
-            for (int j = 0; j < 8; ++j)
-                if (key0 + 16 * (j >> 2) + 4 * g + (j & 3) > limit) x[j] = -INFINITY;
+            for (int j = 0; j < 8; ++j) {
+                const int key = key0 + 16 * (j >> 2) + 4 * g + (j & 3);
+                if (key > limit || (PREP && key < key_lo)) x[j] = -INFINITY;
+            }
         }
         float mx = __builtin_fmaxf(max3(x[0], x[1], x[2]), max3(x[3], x[4], x[5]));
         mx = max3(mx, x[6], x[7]);
@@ -409,6 +463,131 @@ __device__ __forceinline__ void prefill_rows(const PrefillArgs &a, KV *kring, VT
         s[1] = sn[1];
     };
 
+    // ---- PREP: the query's hi + lo fragments from its fp32 row ----
+    // RMSNorm over the row's 256 dims (each lane holds 64 of them; the four
+    // lanes of a row sum theirs with lane swaps), times q_norm, RoPE on the
+    // pairs (i, i+32), i < 32 (dims 8g + e of k-step 0 and 1 of the same
+    // lane), with the prepare kernel's formulas and angles.  The prepare
+    // kernel sums the squares in another order, so a value may differ from
+    // its in the last bit of fp32.  The q_norm weights pass through the
+    // wave's LDS slot into the fragment layout.  Each lane evaluates two
+    // angles, pair lane % 32 of the tile's tokens 0 + lane / 32 and
+    // 2 + lane / 32, and every lane takes its eight from those lanes.
+    [[maybe_unused]] auto prep_query = [&]() __attribute__((always_inline)) {
+      if constexpr (PREP) {
+#pragma clang fp contract(off)
+        static_for<0, KS>([&](auto ks) { pin(qx[ks][0], qx[ks][1]); });
+        pin(gw[0], gw[1], gw[2], gw[3]);
+        const uint32_t slot = lds_addr(qn_stage) + w * 1024;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) lds_write4(slot + (64 * i + lane) * 4, gw[i]);
+        asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+        f32x4 qg[KS][2];
+        static_for<0, 2>([&](auto half_) {
+            constexpr int K0 = decltype(half_)::value * KS / 2;
+            static_for<0, KS / 2>([&](auto k_) {
+                constexpr int ks = K0 + decltype(k_)::value;
+                lds_read<ks * 128>(qg[ks][0], slot + 32 * g);
+                lds_read<ks * 128 + 16>(qg[ks][1], slot + 32 * g);
+            });
+            static_for<0, KS / 2>([&](auto k_) {
+                constexpr int ks = K0 + decltype(k_)::value;
+                lds_wait<2 * (KS / 2 - 1 - decltype(k_)::value)>(qg[ks][0], qg[ks][1]);
+            });
+        });
+        const double fq = rope_freq(lane & 31);
+        float ca, sa, cb, sb;
+        rope_cos_sin(tile_pos + (lane >> 5), fq, ca, sa);
+        rope_cos_sin(tile_pos + 2 + (lane >> 5), fq, cb, sb);
+        float sq = 0.f;
+#pragma unroll
+        for (int ks = 0; ks < KS; ++ks)
+#pragma unroll
+            for (int e = 0; e < 8; ++e) sq = (sq + (qx[ks][e >> 2][e & 3] * qx[ks][e >> 2][e & 3]));
+        const float inv = rsqrtf((row_group_sum(sq) * (1.f / D)) + a.epsilon);
+#pragma unroll
+        for (int ks = 0; ks < KS; ++ks)
+#pragma unroll
+            for (int e = 0; e < 8; ++e) qx[ks][e >> 2][e & 3] = ((qx[ks][e >> 2][e & 3] * inv) * qg[ks][e >> 2][e & 3]);
+        const int dt = qpos - tile_pos;                    // 0 .. 3
+        const bool later = dt >= 2;
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+            const int src = ((dt & 1) << 5) + 8 * g + e;
+            const float c0 = __shfl(ca, src, kWave), c1 = __shfl(cb, src, kWave);
+            const float s0 = __shfl(sa, src, kWave), s1 = __shfl(sb, src, kWave);
+            const float c = later ? c1 : c0, sn = later ? s1 : s0;
+            const float x0 = qx[0][e >> 2][e & 3], x1 = qx[1][e >> 2][e & 3];
+            qx[0][e >> 2][e & 3] = ((x0 * c) - (x1 * sn));
+            qx[1][e >> 2][e & 3] = ((x0 * sn) + (x1 * c));
+        }
+#pragma unroll
+        for (int ks = 0; ks < KS; ++ks)
+#pragma unroll
+            for (int e = 0; e < 8; ++e) {
+                const float x = qx[ks][e >> 2][e & 3];
+                const _Float16 hi = (_Float16)x;
+                qf[ks][e] = hi;
+                qlo[ks][e] = (_Float16)(x - (float)hi);
+            }
+      }
+    };
+    // ---- PREP, the last run: the chunk's keys in the rings ----
+    // The K and V buffers of those pages (at most four) are zeroed, then wave
+    // w prepares keys w, w+8, ... (lane l: dims 64i + l, the prepare
+    // kernel's functions, so the bits it appends) and writes those this
+    // workgroup's rows see at their slots; slots of cached keys (before
+    // `position`) and past the last stay zero and are masked.  Workgroup 0
+    // (whose rows include the chunk's last) prepares every key and appends
+    // them to the pages; the cached runs mask and zero the slots from
+    // `position` on of the page they share, so reading them while they are
+    // written is harmless.
+    [[maybe_unused]] auto prep_new_keys = [&]() __attribute__((always_inline)) {
+      if constexpr (PREP) {
+            U4 *kz = reinterpret_cast<U4 *>(kring), *vz = reinterpret_cast<U4 *>(vring);
+            for (int e = threadIdx.x; e < nl * PAGE / 8; e += kPWaves * kWave) {
+                kz[e] = U4{0u, 0u, 0u, 0u};
+                vz[e] = U4{0u, 0u, 0u, 0u};
+            }
+            lds_barrier();
+            const int seen = wg_keys - a.position, todo = j == 0 ? a.tokens : seen;
+            float gk[4];
+    #pragma unroll
+            for (int i = 0; i < 4; ++i) gk[i] = a.k_norm[64 * i + lane];
+            const double fq = rope_freq(lane);
+            _Float16 *kpg = const_cast<_Float16 *>(static_cast<const _Float16 *>(a.k_pages)) + (size_t)h * a.head_stride;
+            _Float16 *vpg = const_cast<_Float16 *>(static_cast<const _Float16 *>(a.v_pages)) + (size_t)h * a.head_stride;
+            for (int jj = w; jj < todo; jj += kPWaves) {
+                const size_t krow = ((size_t)jj * a.kv_heads + h) * D + lane;
+                float xk[1][4], xv[4];
+    #pragma unroll
+                for (int i = 0; i < 4; ++i) {
+                    xk[0][i] = a.key[krow + 64 * i];
+                    xv[i] = a.value[krow + 64 * i];
+                }
+                const int key = a.position + jj;
+                float c[1] = {1.f}, sn[1] = {0.f};
+                if (lane < 32) rope_cos_sin(key, fq, c[0], sn[0]);
+                norm_rope_rows<1>(xk, gk, c, sn, a.epsilon, lane);
+                const int buf = key / 32 - p0;
+    #pragma unroll
+                for (int i = 0; i < 4; ++i) {
+                    const int d = 64 * i + lane;
+                    const _Float16 kv = cache_half(xk[0][i]), vv = cache_half(xv[i]);
+                    if (jj < seen) {
+                        kring[buf * PAGE + k_page_offset(key & 31, d, D)] = kv;
+                        vring[buf * PAGE + v_page_offset(key & 31, d, D)] = vv;
+                    }
+                    if (j == 0) {
+                        kpg[k_page_offset(key, d, D)] = kv;
+                        vpg[v_page_offset(key, d, D)] = vv;
+                    }
+                }
+            }
+            lds_barrier();
+          }
+    };
+
     // ---- prologue: K0 V0 K1 V1 K2 requested, S^T of page 0 ----
     s[0] = s[1] = f32x4{0.f, 0.f, 0.f, 0.f};
     if (nl > 0) {
@@ -416,16 +595,33 @@ __device__ __forceinline__ void prefill_rows(const PrefillArgs &a, KV *kring, VT
         stage(vh, 0, vring);
         if (nl > 1) { stage(kh, 1, kring); stage(vh, 1, vring); }
         if (nl > 2) stage(kh, 2, kring);
+    }
+    if constexpr (PREP) {
+        // The query's loads precede the pages' (loads complete in order):
+        // wait for them alone and prepare the query while the pages are in
+        // flight.
+        if (w >= kLoaders || nl == 0) wait_vmcnt<0>();
+        else if (nl > 2) wait_vmcnt<5 * H>();
+        else if (nl > 1) wait_vmcnt<4 * H>();
+        else wait_vmcnt<2 * H>();
+        prep_query();
+    }
+    // S^T of the run's first page once it is in its buffer (every wave
+    // meets first).
+    auto first_scores = [&]() __attribute__((always_inline)) {
+        ring_barrier();
+        static_for<0, KW>([&](auto ks) { read_k(ks, kring_lane); });
+        static_for<0, KS>([&](auto ks) { qk_chunk(ks, kring_lane, s); });
+    };
+    if (nl > 0) {
         // Loader waves: K0 has landed, and the query loads before it.  The
         // others issued no page loads: their query loads.
         if (w >= kLoaders) wait_vmcnt<0>();
         else if (nl > 2) wait_vmcnt<4 * H>();
         else if (nl > 1) wait_vmcnt<3 * H>();
         else wait_vmcnt<H>();
-        ring_barrier();
-        static_for<0, KW>([&](auto ks) { read_k(ks, kring_lane); });
-        static_for<0, KS>([&](auto ks) { qk_chunk(ks, kring_lane, s); });
-    } else {
+        first_scores();
+    } else if constexpr (!PREP) {
         wait_vmcnt<0>();   // no page of this split: the query loads only
     }
 
@@ -444,7 +640,7 @@ __device__ __forceinline__ void prefill_rows(const PrefillArgs &a, KV *kring, VT
     const int tail_page = n_keys % 32 ? n_keys / 32 : -1;
     auto prepare_v = [&](int i) __attribute__((always_inline)) {
         const int p = p0 + i;
-        if (w >= kLoaders || i >= nl || p != tail_page) return;
+        if (w >= kLoaders || i >= nl || p != tail_page || from_lds) return;
 #pragma unroll
         for (int c = 0; c < H; ++c) {
             U4 *slot = reinterpret_cast<U4 *>(vring + (i & 3) * PAGE + (w * H + c) * 512) + lane;
@@ -456,18 +652,46 @@ __device__ __forceinline__ void prefill_rows(const PrefillArgs &a, KV *kring, VT
         }
         asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
     };
-    for (int i = 0; i < nl; ++i) {
-        if ((i & 1) == 0) {
-            wait_vmcnt<0>();
-            prepare_v(i);
-            prepare_v(i + 1);
-            ring_barrier();
-            if (i + 3 < nl) stage(kh, i + 3, kring);
-            if (i + 4 < nl) stage(kh, i + 4, kring);
-            if (i + 2 < nl) stage(vh, i + 2, vring);
-            if (i + 3 < nl) stage(vh, i + 3, vring);
+    auto run_pages = [&]() __attribute__((always_inline)) {
+        for (int i = 0; i < nl; ++i) {
+            if ((i & 1) == 0) {
+                wait_vmcnt<0>();
+                prepare_v(i);
+                prepare_v(i + 1);
+                ring_barrier();
+                if (i + 3 < nl) stage(kh, i + 3, kring);
+                if (i + 4 < nl) stage(kh, i + 4, kring);
+                if (i + 2 < nl) stage(vh, i + 2, vring);
+                if (i + 3 < nl) stage(vh, i + 3, vring);
+            }
+            if (i < nw) step(i);
         }
-        if (i < nw) step(i);
+    };
+    run_pages();
+
+    if constexpr (PREP) {
+        if (new_keys) {
+            // ---- the last run: then the chunk's keys, from its rings ----
+            // Once every wave is done with the rings, the keys of the
+            // workgroup's rows (pages from the one holding key `position`
+            // on) are prepared into them, and the same loop runs over them
+            // with the rows' causal limits; keys before `position` are the
+            // cached runs' and are masked.  The softmax state carries on.
+            wait_vmcnt<0>();
+            lds_barrier();
+            from_lds = true;
+            p0 = a.position / 32;
+            n_keys = wg_keys;
+            nl = max(0, (wg_keys + 31) / 32 - p0);
+            nw = min(max((wave_keys + 31) / 32 - p0, 0), nl);
+            limit = a.position + row_token;
+            wave_first_limit = a.position + max(row0, 0) / a.group;
+            key_lo = a.position;
+            prep_new_keys();
+            s[0] = s[1] = f32x4{0.f, 0.f, 0.f, 0.f};
+            if (nl > 0) first_scores();
+            run_pages();
+        }
     }
 
     l = row_group_sum(l);
@@ -518,6 +742,19 @@ void attention_prefill(PrefillArgs a) {
     __shared__ __attribute__((aligned(16))) KV kring[4 * 32 * D];
     __shared__ __attribute__((aligned(16))) VT vring[4 * 32 * D];
     prefill_rows<D, KV, VT, PSPLIT, QSPLIT, MODE, ROWS>(a, kring, vring, a.v_pages, a.head_stride);
+}
+
+// The fused prefill chunk that prepares its own query and keys (PREP in
+// prefill_rows): fp16 pages, precise query, gated output, 128 rows per
+// workgroup.
+__global__ __launch_bounds__(kPreciseRows / 16 * kWave, 1)
+void attention_prefill_prep(PrefillArgs a) {
+    constexpr int D = kModelHeadDim;
+    __shared__ __attribute__((aligned(16))) _Float16 kring[4 * 32 * D];
+    __shared__ __attribute__((aligned(16))) _Float16 vring[4 * 32 * D];
+    __shared__ __attribute__((aligned(16))) float qn_stage[kPreciseRows / 16][D];
+    prefill_rows<D, _Float16, _Float16, true, true, kOutGated, kPreciseRows, -1, true>(a, kring, vring, a.v_pages,
+                                                                                      a.head_stride, &qn_stage[0][0]);
 }
 
 // The precise rows in two passes of eight waves (192 rows per workgroup):
@@ -803,6 +1040,112 @@ size_t prefill_workspace_bytes(const Shape &s, Dtype dtype, bool precise) {
     return plan_prefill(s, dtype, precise).bytes;
 }
 
+namespace {
+// The combine of a call whose rows' keys were split into `splits` runs.  Up
+// to kCombineWideBatch splits (many rows): combine_prefill, a wave per row,
+// in rounds of 8 splits up to 16 and in one round of up to 24 beyond (the
+// fused 64-token chunk at 16,384, 21 splits: 66.3 against 68.1 us per layer
+// with attention_combine; the wide batch gave nothing at 9-16 splits).  More
+// splits (then few row workgroups, few rows): attention_combine, whose four
+// waves per row request up to 64 splits in one round (62 splits of 96 rows:
+// 27.5 us per call against 31.1 us with combine_prefill's batches in turn).
+void launch_prefill_combine(const Shape &s, Dtype dtype, const float *part_o, const float *part_ml, int splits,
+                            void *out, bool out_f32, const float *gate, hipStream_t stream) {
+    const int rows = s.group() * s.tokens;
+    if (splits > kCombineWideBatch) {
+        SplitPlan cp = {};
+        cp.kind = SplitKind::Stream;   // fp32 partial rows, default-policy stores
+        cp.rows = rows;
+        cp.splits = splits;
+        launch_combine(s, cp, dtype, part_o, out, out_f32, gate, stream);
+        return;
+    }
+    CombinePrefillArgs c;
+    c.part_o = part_o;
+    c.part_ml = part_ml;
+    c.out = out;
+    c.gate = gate;
+    c.q_heads = s.q_heads;
+    c.group = s.group();
+    c.rows = rows;
+    c.kv_heads = s.kv_heads;
+    c.splits = splits;
+    const long long waves = (long long)rows * s.kv_heads;
+    const long long blocks = (waves + kCombineThreads / kWave - 1) / (kCombineThreads / kWave);
+    require(blocks < (1LL << 31), "prefill combine exceeds the grid");
+    const bool wide = splits > 2 * kCombineBatch;
+    const void *kernel = s.head_dim == 256 ? combine_prefill_kernel<256>(dtype, out_f32, gate != nullptr, wide)
+                                           : combine_prefill_kernel<128>(dtype, out_f32, gate != nullptr, wide);
+    void *cargs[] = {&c};
+    check(hipLaunchKernel(kernel, dim3((unsigned)blocks), dim3(kCombineThreads), cargs, 0, stream));
+}
+}  // namespace
+
+bool prefill_prep_fits(int tokens, int position) {
+    return tokens > kMaxFusedSplitTokens && position >= 0 &&
+           tokens + position % kPageTokens <= kPrepNewKeyPages * kPageTokens;
+}
+
+PrefillPlan plan_prefill_prep_for(int tokens, int position, int cus) {
+    const Shape s{kModelQHeads, kModelKvHeads, kModelHeadDim, tokens, position, 0};
+    PrefillPlan p;
+    p.rows = kPreciseRows;
+    p.row_wgs = (s.group() * tokens + p.rows - 1) / p.rows;
+    p.passes = 1;
+    // Runs over the cached pages as plan_prefill_for splits a call's pages
+    // (the last run, the shortest, also takes the chunk's keys).
+    const long long cached = ((long long)position + kPageTokens - 1) / kPageTokens;
+    const long long base = (long long)p.row_wgs * s.kv_heads;
+    p.splits = 1;
+    if (cached >= kPrefillMinSplitKeyPages && base < cus)
+        p.splits = (int)std::max(1LL, std::min<long long>({cus / base, cached / kPrefillMinSplitPages,
+                                                           kPrefillMaxSplits}));
+    p.part_offset = 0;
+    p.bytes = split_partial_bytes(s, p.splits);
+    return p;
+}
+
+size_t prefill_prep_workspace_bytes(int tokens, int position) {
+    return prefill_prep_fits(tokens, position) ? plan_prefill_prep_for(tokens, position, device_cu_count()).bytes : 0;
+}
+
+void launch_prefill_prep(const FusedToken &tok, float *out, void *workspace, hipStream_t stream) {
+    require(prefill_prep_fits(tok.tokens, tok.position), "the chunk's keys do not fit the prepared prefill's rings");
+    const Shape s{kModelQHeads, kModelKvHeads, kModelHeadDim, tok.tokens, tok.position, 0};
+    const PrefillPlan plan = plan_prefill_prep_for(tok.tokens, tok.position, device_cu_count());
+    require(plan.bytes == 0 || workspace != nullptr, "this prefill needs its workspace");
+    PrefillArgs a = {};
+    a.gate = tok.q_gate;
+    a.k_pages = tok.k_pages;
+    a.v_pages = tok.v_pages;
+    a.out = out;
+    a.head_stride = tok.head_stride;
+    a.q_heads = s.q_heads;
+    a.kv_heads = s.kv_heads;
+    a.group = s.group();
+    a.rows = s.group() * s.tokens;
+    a.position = s.position;
+    a.n_tiles = plan.row_wgs;
+    a.scale_log2 = (1.0f / 16.0f) * 1.4426950408889634f;
+    a.splits = plan.splits;
+    a.key = tok.key;
+    a.value = tok.value;
+    a.q_norm = tok.q_norm;
+    a.k_norm = tok.k_norm;
+    a.epsilon = tok.epsilon;
+    a.tokens = tok.tokens;
+    if (plan.splits > 1) {
+        a.part_o = static_cast<float *>(workspace);
+        a.part_ml = a.part_o + (size_t)s.kv_heads * plan.splits * a.rows * s.head_dim;
+    }
+    const long long grid = (long long)plan.row_wgs * s.kv_heads * plan.splits;
+    void *args[] = {&a};
+    check(hipLaunchKernel((const void *)&attention_prefill_prep, dim3((unsigned)grid), dim3(kPreciseRows / 16 * kWave),
+                          args, 0, stream));
+    if (plan.splits > 1)
+        launch_prefill_combine(s, Dtype::F16, a.part_o, a.part_ml, plan.splits, out, true, tok.q_gate, stream);
+}
+
 void launch_prefill(const Shape &s, Dtype dtype, bool precise, float scale, const void *q,
                     const void *q_lo, const void *k_pages, const void *v_pages, void *out, bool out_f32,
                     const float *gate, void *workspace, hipStream_t stream) {
@@ -836,43 +1179,9 @@ void launch_prefill(const Shape &s, Dtype dtype, bool precise, float scale, cons
     const long long grid = (long long)plan.row_wgs * s.kv_heads * plan.splits;
     require(grid * threads < (1LL << 32), "prefill launch exceeds 2^32 work-items");
     void *args[] = {&a};
-    // The combine of split calls.  Up to kCombineWideBatch splits (many
-    // rows): combine_prefill, a wave per row, in rounds of 8 splits up to
-    // 16 and in one round of up to 24 beyond (the fused 64-token chunk at
-    // 16,384, 21 splits: 66.3 against 68.1 us per layer with
-    // attention_combine; the wide batch gave nothing at 9-16 splits).
-    // More splits (then few row workgroups, few rows): attention_combine,
-    // whose four waves per row request up to 64 splits in one round (62
-    // splits of 96 rows: 27.5 us per call against 31.1 us with
-    // combine_prefill's batches in turn).
     auto combine = [&] {
-        if (plan.splits == 1) return;
-        if (plan.splits > kCombineWideBatch) {
-            SplitPlan cp = {};
-            cp.kind = SplitKind::Stream;   // fp32 partial rows, default-policy stores
-            cp.rows = a.rows;
-            cp.splits = plan.splits;
-            launch_combine(s, cp, dtype, a.part_o, out, out_f32, gate, stream);
-            return;
-        }
-        CombinePrefillArgs c;
-        c.part_o = a.part_o;
-        c.part_ml = a.part_ml;
-        c.out = out;
-        c.gate = gate;
-        c.q_heads = s.q_heads;
-        c.group = a.group;
-        c.rows = a.rows;
-        c.kv_heads = s.kv_heads;
-        c.splits = plan.splits;
-        const long long waves = (long long)a.rows * s.kv_heads;
-        const long long blocks = (waves + kCombineThreads / kWave - 1) / (kCombineThreads / kWave);
-        require(blocks < (1LL << 31), "prefill combine exceeds the grid");
-        const bool wide = plan.splits > 2 * kCombineBatch;
-        const void *kernel = d256 ? combine_prefill_kernel<256>(dtype, out_f32, gate != nullptr, wide)
-                                  : combine_prefill_kernel<128>(dtype, out_f32, gate != nullptr, wide);
-        void *cargs[] = {&c};
-        check(hipLaunchKernel(kernel, dim3((unsigned)blocks), dim3(kCombineThreads), cargs, 0, stream));
+        if (plan.splits > 1)
+            launch_prefill_combine(s, dtype, a.part_o, a.part_ml, plan.splits, out, out_f32, gate, stream);
     };
     if (precise) {
         const void *kernel = d256 ? precise_prefill_kernel<256>(gate != nullptr, plan.passes)

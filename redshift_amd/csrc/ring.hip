@@ -88,20 +88,6 @@ constexpr int kRingBuffers = 4;   // NBUF-1 pages in flight while one is consume
 constexpr int kStreamLoad = 2;
 constexpr float kLazy = 8.f;   // lazy row-max threshold, log2 units
 
-// A 4-byte global load that the compiler does not track (like
-// global_load16), and a 2- or 4-byte LDS write that it does not order against the
-// ring's direct loads (like lds_read); both are awaited explicitly.
-__device__ __forceinline__ void global_load4(float &v, const float *p) {
-    asm volatile("global_load_dword %0, %1, off" : "=v"(v) : "v"(p) : "memory");
-}
-__device__ __forceinline__ void lds_write4(uint32_t addr, float v) {
-    asm volatile("ds_write_b32 %0, %1" : : "v"(addr), "v"(v) : "memory");
-}
-__device__ __forceinline__ void lds_write2(uint32_t addr, _Float16 v) {
-    const unsigned u = __builtin_bit_cast(unsigned short, v);
-    asm volatile("ds_write_b16 %0, %1" : : "v"(addr), "v"(u) : "memory");
-}
-
 // OUT: kOutPartials stores the split's partial rows; a direct output
 // (kOutSame or kOutF32: one split per KV head) stores the final rows
 // instead, and no combine runs.

@@ -338,6 +338,43 @@ void prefill_planner_sweep() {
     std::printf("abi_sanitize: %d prefill plans checked\n", plans);
 }
 
+// The prepared prefill of a fused chunk (plan_prefill_prep_for): chunks of
+// 9 .. 128 - position % 32 tokens fit; 128-row workgroups; runs over the
+// cached pages as plan_prefill_for splits a call's pages (one below
+// kPrefillMinSplitKeyPages cached pages or with no idle CU, else as many as
+// the CUs, kPrefillMinSplitPages pages per run and kPrefillMaxSplits
+// allow); the chunk's keys span at most four pages; the workspace is the
+// documented partials.
+void prefill_prep_planner_sweep() {
+    int plans = 0;
+    for (int cus : {1, 8, 80, 256, 304})
+        for (int pos : {0, 1, 8, 31, 32, 33, 255, 1000, 6000, 16000, 16384, 139135})
+            for (int tokens = 1; tokens <= 200; ++tokens) {
+                const bool fits = rs::prefill_prep_fits(tokens, pos);
+                EXPECT(fits == (tokens > rs::kMaxFusedSplitTokens && tokens + pos % 32 <= 128));
+                if (!fits) continue;
+                const rs::PrefillPlan p = rs::plan_prefill_prep_for(tokens, pos, cus);
+                ++plans;
+                const long long R = 6LL * tokens, cached = (pos + 31LL) / 32;
+                const long long base = (R + 127) / 128 * 4;
+                EXPECT(p.rows == rs::kPreciseRows && p.passes == 1 && p.row_wgs == (R + 127) / 128);
+                EXPECT(p.splits >= 1 && p.splits <= rs::kPrefillMaxSplits);
+                if (cached < rs::kPrefillMinSplitKeyPages || base >= cus) {
+                    EXPECT(p.splits == 1);
+                } else {
+                    EXPECT(base * p.splits <= cus && p.splits * rs::kPrefillMinSplitPages <= cached);
+                    EXPECT(p.splits == rs::kPrefillMaxSplits || base * (p.splits + 1) > cus ||
+                           (p.splits + 1) * rs::kPrefillMinSplitPages > cached);
+                }
+                // The chunk's pages: from the one holding key pos to the last key's.
+                EXPECT((pos + tokens - 1) / 32 - pos / 32 + 1 <= rs::kPrepNewKeyPages);
+                const unsigned long long parts =
+                    p.splits > 1 ? (4ULL * p.splits * R * (256 + 2) * 4 + 255) / 256 * 256 : 0;
+                EXPECT(p.bytes == parts && p.part_offset == 0);
+            }
+    std::printf("abi_sanitize: %d prepared prefill plans checked\n", plans);
+}
+
 // ---- device mode -------------------------------------------------------------
 
 #define HIP_OK(call) EXPECT((call) == hipSuccess)
@@ -530,6 +567,7 @@ int main(int argc, char **argv) {
     device_entry_validation();
     planner_sweep();
     prefill_planner_sweep();
+    prefill_prep_planner_sweep();
     int devices = 0;
     const bool gpu = hipGetDeviceCount(&devices) == hipSuccess && devices > 0;
     std::printf("abi_sanitize: host checks done (%d checks, %d failed); %s\n", checks, failures,

@@ -385,21 +385,31 @@ def test_short_fused_appends_the_prepare_kernels_bits(gpu, position):
     assert_close(short.cpu().numpy(), chunk[:8].cpu().numpy(), 3e-5)
 
 
-@pytest.mark.parametrize('batch,position', [(100, 300), (57, 1), (64, 6000), (2048, 40)])
+@pytest.mark.parametrize('batch,position', [
+    (9, 0), (120, 8),          # prepared prefill, one run (no or few cached keys): the gated rows directly
+    (100, 300), (57, 1),       # prepared prefill: one run of the cached keys, then the chunk's
+    (64, 6000),                # prepared prefill: the cached keys in many runs, combine_prefill
+    (16, 16000),               # prepared prefill: 62 runs, merged by attention_combine
+    (121, 8), (2048, 40),      # the chunk's keys past four pages: prepare launch, then the prefill
+])
 def test_fused_prefill_chunk_matches_oracle(gpu, batch, position):
-    """A prefill chunk through the fused entry (more than 8 tokens: prepare,
-    append, the precise prefill kernel and the gate) on the reference's
-    sine-wave fixture (tests/test_cuda.py:201-216), with that test's
-    tolerances: output 3e-4, appended K 2e-3, V exact.  64 tokens after
-    6,000 split their keys over several workgroups and combine them (gated);
-    2048 tokens run two passes of 192 rows per workgroup (one round of
-    workgroups on 256 CUs)."""
+    """A prefill chunk through the fused entry (more than 8 tokens) on the
+    reference's sine-wave fixture (tests/test_cuda.py:201-216), with that
+    test's tolerances: output 3e-4, appended K 2e-3, V exact.  A chunk whose
+    keys fit four pages from the one holding key `position` runs the
+    prepared prefill (query and keys prepared in the kernel, no prepare
+    launch) and combines its splits (gated) when there are cached keys;
+    longer chunks take the prepare launch, and 2048 tokens run two passes of
+    192 rows per workgroup (one round of workgroups on 256 CUs)."""
     torch = gpu
     c = kat.sine_wave_case(batch=batch, position=position)
     expected = ref.fused_attention(c['key_cache'], c['value_cache'], c['q_gate'], c['key'], c['value'],
                                    c['q_norm'], c['k_norm'], batch, position, c['epsilon'])
     cache = A.PagedKV(4, 256, A.round_capacity(position + batch), torch.float16)
-    cache.pack(torch.from_numpy(c['key_cache']).cuda(), torch.from_numpy(c['value_cache']).cuda())
+    cache.k.fill_(float('nan'))
+    cache.v.fill_(float('nan'))
+    if position:
+        cache.pack(torch.from_numpy(c['key_cache']).cuda(), torch.from_numpy(c['value_cache']).cuda())
     dev = [torch.from_numpy(f32(c[name])).cuda() for name in ('q_gate', 'key', 'value', 'q_norm', 'k_norm')]
     q_parts = batch * 24 * 256 * 4
     if position < 1000:
@@ -701,7 +711,8 @@ def test_fused_random_shapes_against_oracle(gpu, batch, position, seed):
     assert_close(vcache.float().cpu().numpy(), expected[2], 0)
 
 
-@pytest.mark.parametrize('batch,position', [(1, 16000), (2, 3000), (5, 300), (8, 16000), (1400, 100), (64, 16000)])
+@pytest.mark.parametrize('batch,position', [(1, 16000), (2, 3000), (5, 300), (8, 16000), (1400, 100), (64, 16000),
+                                            (40, 0), (16, 16000)])
 def test_fused_graph_replay_matches_eager(gpu, batch, position):
     """The fused entry (prepare in the split kernels' prologue, the new keys
     appended by the kernels; for a prefill chunk the prepare launch, the
@@ -717,7 +728,8 @@ def test_fused_graph_replay_matches_eager(gpu, batch, position):
     cache = A.PagedKV(4, 256, A.round_capacity(position + batch), torch.float16)
     cache.k.fill_(float('nan'))
     cache.v.fill_(float('nan'))
-    cache.pack(torch.from_numpy(kc).cuda(), torch.from_numpy(vc).cuda())
+    if position:
+        cache.pack(torch.from_numpy(kc).cuda(), torch.from_numpy(vc).cuda())
     dev = [torch.from_numpy(x).cuda() for x in (
         rng.standard_normal((batch, 24, 512)).astype(np.float32),
         rng.standard_normal((batch, 4, 256)).astype(np.float32),
