@@ -33,10 +33,33 @@ TRAFFIC_FILE = ROOT / 'profiles' / 'attention_stream_decode_139k_traffic.txt'
 HBM_PEAK_GBS = 8000.0
 MFMA_BF16_PEAK = 2.5e15   # dense bf16 FLOP/s
 LAYERS = 16
+# Seconds of full load before every timed region (see settle).
+SETTLE_S = 0.25
 
 
 def log(msg):
     print(f'[bench] {msg}', file=sys.stderr, flush=True)
+
+
+def settle(torch, run, minimum, seconds=SETTLE_S):
+    """Runs `run` (one step) at least `minimum` times and until `seconds` of
+    wall time have passed, synchronising every 8 runs; returns the count.
+
+    The GPU's clock and board power ramp up over tens of milliseconds of full
+    load.  Measured on decode_139k graph replays after the eager loop: the
+    first ~15 replays (30 ms) took 90.3-91.2 us per layer while sclk rose
+    from 2121 to 2176 MHz and power from 556 to 630 W; from about 650 W and
+    2190 MHz on, every replay took 85.6-86.3 us.  A timed region that starts
+    inside the ramp measures the ramp, so every one starts after this."""
+    torch.cuda.synchronize()
+    t_end = time.perf_counter() + seconds
+    n = 0
+    while n < minimum or time.perf_counter() < t_end:
+        for _ in range(8):
+            run()
+            n += 1
+        torch.cuda.synchronize()
+    return n
 
 
 def make_layers(torch, A, w, layers, seed):
@@ -106,8 +129,7 @@ def time_workload(torch, A, w, layers, steps, warmup, seed, sample=None):
         torch.cuda.synchronize()
         return start.elapsed_time(end) / n
 
-    for _ in range(warmup):
-        step()
+    settled = settle(torch, step, warmup)
     ev = [[[torch.cuda.Event(enable_timing=True) for _ in range(2)] for _ in range(layers)]
           for _ in range(steps)]
     eager_ms = timed(lambda s: step(ev[s]), steps)
@@ -123,8 +145,7 @@ def time_workload(torch, A, w, layers, steps, warmup, seed, sample=None):
         with torch.cuda.graph(graph, stream=capture_stream):
             step()
     torch.cuda.current_stream().wait_stream(capture_stream)
-    for _ in range(warmup):
-        graph.replay()
+    settled_graph = settle(torch, graph.replay, warmup)
     # One event pair per replay as well (recorded between replays, outside
     # the graph): the spread of the step time over the timed steps.
     replay_ev = [[torch.cuda.Event(enable_timing=True) for _ in range(2)] for _ in range(steps)]
@@ -153,14 +174,14 @@ def time_workload(torch, A, w, layers, steps, warmup, seed, sample=None):
             with torch.cuda.graph(sgraph, stream=capture_stream):
                 splits_only()
         torch.cuda.current_stream().wait_stream(capture_stream)
-        for _ in range(warmup):
-            sgraph.replay()
+        settle(torch, sgraph.replay, warmup)
         split_graph_us = 1000.0 * timed(lambda s: sgraph.replay(), steps) / layers
         del sgraph
     del caches
     torch.cuda.empty_cache()
     return dict(ms_per_step=graph_ms, eager_ms_per_step=eager_ms, replay_ms=replay_ms,
                 device_before=device_before, device_after=device_after,
+                settle_steps=settled, settle_replays=settled_graph,
                 split_us=1000.0 * statistics.median(split_ms), split_us_mean=1000.0 * sum(split_ms) / len(split_ms),
                 split_graph_us=split_graph_us)
 
@@ -338,8 +359,7 @@ def read_probe(torch, A, w, sets=16, rounds=20, ahead=3):
             for c in caches:
                 launch(c)
     torch.cuda.current_stream().wait_stream(capture_stream)
-    graph.replay()
-    torch.cuda.synchronize()
+    settle(torch, graph.replay, 1)
     start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     start.record()
     for _ in range(rounds):
@@ -435,9 +455,7 @@ def time_fused(torch, A, w, layers, steps, warmup, seed):
         with torch.cuda.graph(graph, stream=capture_stream):
             step()
     torch.cuda.current_stream().wait_stream(capture_stream)
-    for _ in range(warmup):
-        graph.replay()
-    torch.cuda.synchronize()
+    settle(torch, graph.replay, warmup)
     start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     start.record()
     for _ in range(steps):
@@ -463,9 +481,7 @@ def time_kv_copy(torch, A, w, layers, steps, warmup, seed):
         for i in range(layers):
             copy_prefix(snaps[i], caches[i], w.keys)
 
-    for _ in range(warmup):
-        step()
-    torch.cuda.synchronize()
+    settle(torch, step, warmup)
     start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     start.record()
     for _ in range(steps):
@@ -612,7 +628,7 @@ def main():
                          'the timed graph replays of decode_139k')
     step_bytes = args.layers * w.kv_bytes()
     gbs = step_bytes / (r['ms_per_step'] * 1e-3) / 1e9
-    split_gbs = w.kv_bytes() / (r['split_us'] * 1e-6) / 1e9
+    split_gbs = w.kv_bytes() / (r['split_graph_us'] * 1e-6) / 1e9
     result = {
         'metric': METRIC, 'value': round(gbs, 1), 'unit': 'GB/s', 'n_gpus': 1,
         'steps': args.steps, 'warmup': args.warmup, 'ms_per_step': round(r['ms_per_step'], 4),
@@ -624,16 +640,23 @@ def main():
         'us_per_layer': round(1000 * r['ms_per_step'] / args.layers, 2),
         'eager_us_per_layer': round(1000 * r['eager_ms_per_step'] / args.layers, 2),
         'timing': 'step = 16 layers x (split-K kernel + combine kernel) replayed as one HIP graph; '
-                  'roofline kernel_us = split-K kernel alone, median of HIP-event-timed launches in an '
-                  'eager loop (kernel_us_mean: their mean)',
+                  'roofline kernel_us = the split-K kernel alone: a graph of its 16 launches (one per '
+                  'layer, back to back) timed by HIP events around each replay, per launch '
+                  '(kernel_us_eager_median: the median of event pairs around single eager launches, which '
+                  'include the dispatch gap); every timed region starts after the warmup '
+                  f'steps and at least {SETTLE_S} s of full load (settle_steps eager steps, '
+                  'settle_replays graph replays), past the clock and power ramp',
+        'settle_steps': r['settle_steps'], 'settle_replays': r['settle_replays'],
         'roofline': {'bound': 'hbm', 'kernel': 'attention_stream (decode split-K)',
                      'achieved': round(split_gbs, 1), 'peak': HBM_PEAK_GBS, 'unit': 'GB/s',
                      'frac': round(split_gbs / HBM_PEAK_GBS, 4), 'traffic': measured_traffic(),
-                     'kernel_us': round(r['split_us'], 2), 'kernel_us_mean': round(r['split_us_mean'], 2),
+                     'kernel_us': round(r['split_graph_us'], 2),
+                     'kernel_us_eager_median': round(r['split_us'], 2),
+                     'kernel_us_eager_mean': round(r['split_us_mean'], 2),
                      'bytes_per_launch': w.kv_bytes(),
                      'frac_step': round(gbs / HBM_PEAK_GBS, 4),
-                     'frac_is': 'frac: the split-K kernel alone (kernel_us); frac_step: the whole layer, '
-                                'split-K + combine kernels in the graph step (us_per_layer)'},
+                     'frac_is': 'frac: the split-K kernel alone (kernel_us, in its graph); frac_step: the '
+                                'whole layer, split-K + combine kernels in the graph step (us_per_layer)'},
         'step_spread': {**spread(r['replay_ms'], args.layers),
                         'what': 'us per layer of each timed graph replay (an event pair around each)'},
         'provenance': prov,
