@@ -376,6 +376,7 @@ def read_probe(torch, A, w, sets=16, rounds=20, ahead=3):
     us = sorted(1000 * e[0].elapsed_time(e[1]) for e in ev)
     del graph, caches, lib
     torch.cuda.empty_cache()
+    merge_reads = merge_read_probe(torch, probe)
     page_bytes = 2 * w.kv_heads * n_pages * 32 * w.head_dim * 2
     med = statistics.median(us)
     return {'workload': w.name, 'grid': f'{splits} splits x {w.kv_heads} KV heads, 512 threads',
@@ -385,8 +386,57 @@ def read_probe(torch, A, w, sets=16, rounds=20, ahead=3):
             'GB/s': round(w.kv_bytes() / (us_graph * 1e-6) / 1e9, 1),
             'frac_hbm': round(w.kv_bytes() / (us_graph * 1e-6) / 1e9 / HBM_PEAK_GBS, 4),
             'algorithmic_bytes': w.kv_bytes(), 'page_bytes': page_bytes,
+            'merge_reads': merge_reads,
             'what': 'plain non-temporal read of the pages one split-K launch of the workload streams; '
                     'GB/s and frac_hbm over the algorithmic K+V bytes and the in-graph time per launch'}
+
+
+def merge_read_probe(torch, probe, launches=16, rounds=20):
+    """rsp_read_rows: one workgroup per KV head reading that head's split-K
+    partials, the reads a merge by the last-arriving workgroup of each head
+    would make (4 heads; verify-8 at 16K: 57 splits x 48 fp16 O/l rows of
+    256 dims plus m and l; decode: 48 splits x 6 fp32 rows plus m and l),
+    with default loads and with device-coherent (sc1) loads.  Per launch in
+    a graph of `launches`, the buffers read again and again (so from the
+    Infinity Cache, as partials just written would be)."""
+    import ctypes as ct
+    probe.rsp_read_rows.argtypes = [ct.c_void_p, ct.c_int, ct.c_longlong, ct.c_int, ct.c_void_p, ct.c_void_p]
+    probe.rsp_read_rows.restype = ct.c_int
+    heads = 4
+    shapes = {'verify8_16k': 57 * (48 * 256 * 2 + 2 * 48 * 4), 'decode': 48 * (6 * 256 * 4 + 2 * 6 * 4)}
+    out = {}
+    sink = torch.zeros(heads * 512, dtype=torch.int32, device='cuda')
+    for name, per_head in shapes.items():
+        per_head = (per_head + 15) // 16 * 16
+        buf = torch.randint(0, 1 << 30, (heads * per_head // 4,), dtype=torch.int32, device='cuda')
+        for coherent in (0, 1):
+            def launch():
+                rc = probe.rsp_read_rows(buf.data_ptr(), heads, per_head, coherent, sink.data_ptr(),
+                                         torch.cuda.current_stream().cuda_stream)
+                assert rc == 0, 'rsp_read_rows refused its arguments'
+            launch()
+            torch.cuda.synchronize()
+            graph = torch.cuda.CUDAGraph()
+            side = torch.cuda.Stream()
+            side.wait_stream(torch.cuda.current_stream())
+            with torch.cuda.stream(side):
+                with torch.cuda.graph(graph, stream=side):
+                    for _ in range(launches):
+                        launch()
+            torch.cuda.current_stream().wait_stream(side)
+            settle(torch, graph.replay, 1)
+            start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            start.record()
+            for _ in range(rounds):
+                graph.replay()
+            end.record()
+            torch.cuda.synchronize()
+            us = 1000 * start.elapsed_time(end) / (rounds * launches)
+            out[f'{name}_{"coherent" if coherent else "default"}'] = {
+                'bytes_per_head': per_head, 'us_per_launch_in_graph': round(us, 2)}
+            del graph
+        del buf
+    return out
 
 
 def drop_in_rate(lib, cases=((1, 139263), (8, 16384), (1, 4095)), repeats=5):

@@ -67,6 +67,39 @@ void read_pages(const u32x4 *k_pages, const u32x4 *v_pages, size_t head_stride, 
     if (x == 0x9e3779b9u) sink[blockIdx.x * kThreads + threadIdx.x] = x;
 }
 
+// rsp_read_rows: the reads of a merge done by one workgroup per KV head,
+// as the last-arriving workgroup of a split-K launch would do it: workgroup
+// h reads `bytes` contiguous bytes at base + h * bytes (a head's partial
+// rows) with 16-byte loads, 8 per thread in flight, either with the default
+// policy or as device-coherent loads (sc1: what partials written by
+// workgroups on other XCDs need, the code an agent-scope atomic load
+// compiles to).  Its time bounds that merge from below.
+template <bool COHERENT>
+__global__ __launch_bounds__(kThreads)
+void read_rows(const u32x4 *base, size_t pieces, uint32_t *sink) {
+    const u32x4 *p = base + blockIdx.x * pieces;
+    u32x4 acc = {0u, 0u, 0u, 0u};
+    for (size_t i = threadIdx.x; i < pieces; i += 8 * kThreads) {
+        u32x4 v[8];
+#pragma unroll
+        for (int k = 0; k < 8; ++k) {
+            const size_t e = i + (size_t)k * kThreads < pieces ? i + (size_t)k * kThreads : i;
+            if constexpr (COHERENT)
+                asm volatile("global_load_dwordx4 %0, %1, off sc1" : "=v"(v[k]) : "v"(p + e) : "memory");
+            else
+                v[k] = p[e];
+        }
+        if constexpr (COHERENT) asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+#pragma unroll
+        for (int k = 0; k < 8; ++k) {
+            if constexpr (COHERENT) asm volatile("" : "+v"(v[k]));
+            acc ^= v[k];
+        }
+    }
+    const uint32_t x = acc[0] ^ acc[1] ^ acc[2] ^ acc[3];
+    if (x == 0x9e3779b9u) sink[blockIdx.x * kThreads + threadIdx.x] = x;
+}
+
 template <int D>
 const void *pick(int ahead) {
     switch (ahead) {
@@ -94,4 +127,15 @@ extern "C" int rsp_read_pages(const void *k_pages, const void *v_pages, int kv_h
     void *args[] = {&k_pages, &v_pages, &head_stride, &n_pages, &splits, &sink};
     return hipLaunchKernel(kernel, dim3(splits * kv_heads), dim3(kThreads), args, 0,
                            static_cast<hipStream_t>(stream)) == hipSuccess ? 0 : -1;
+}
+
+// heads workgroups of 512 threads, `bytes` (a multiple of 16) per head;
+// sink: heads * 512 words.
+extern "C" int rsp_read_rows(const void *base, int heads, long long bytes, int coherent, void *sink, void *stream) {
+    if (!base || !sink || heads < 1 || bytes < 16 || bytes % 16) return -1;
+    size_t pieces = (size_t)bytes / 16;
+    const void *kernel = coherent ? (const void *)&read_rows<true> : (const void *)&read_rows<false>;
+    void *args[] = {&base, &pieces, &sink};
+    return hipLaunchKernel(kernel, dim3(heads), dim3(kThreads), args, 0, static_cast<hipStream_t>(stream)) == hipSuccess
+               ? 0 : -1;
 }
