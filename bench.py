@@ -310,7 +310,7 @@ def copy_probe(mib, repeats=5):
     log(f'copy probe: {repeats} x {mib} MiB device-to-device copies')
 
 
-def read_probe(torch, A, w, sets=16, rounds=20, ahead=3):
+def read_probe(torch, A, w, sets=16, rounds=20, ahead=3, splits=None):
     """The plain read of one split-K launch's KV pages (rsp_read_pages in
     libredshift_probe.so): the grid, runs and page addresses of
     attention_ring for workload `w` (57 splits x 4 KV heads for verify8_16k),
@@ -318,7 +318,9 @@ def read_probe(torch, A, w, sets=16, rounds=20, ahead=3):
     workload's size rotate, so that the 256 MB Infinity Cache holds none of
     the pages a launch reads (16 x 67 MB).  Each launch is timed by an event
     pair, in graphs of `sets` launches replayed `rounds` times; returns the
-    median and mean us per launch and the read rate of the algorithmic bytes."""
+    median and mean us per launch and the read rate of the algorithmic bytes.
+    `splits` replaces the launch's own key splits (the same pages over
+    another grid); the merge reads are then not measured."""
     import ctypes as ct
 
     from redshift_amd.build import PROBE_LIBRARY
@@ -338,7 +340,8 @@ def read_probe(torch, A, w, sets=16, rounds=20, ahead=3):
     per_split = w.kv_heads * rows * (w.head_dim + 2) * 4
     ws = A.attention_workspace_bytes(w.q_heads, w.kv_heads, w.head_dim, w.tokens, w.position)
     assert rows <= A.MAX_CHUNK_ROWS and ws % per_split == 0, 'not a one-launch split-K workload'
-    n_pages, splits = -(-w.keys // 32), ws // per_split
+    own = splits is None
+    n_pages, splits = -(-w.keys // 32), ws // per_split if own else splits
     sink = torch.zeros(splits * w.kv_heads * 512, dtype=torch.int32, device='cuda')
     ev = [[torch.cuda.Event(enable_timing=True) for _ in range(2)] for _ in range(sets * rounds)]
 
@@ -376,7 +379,7 @@ def read_probe(torch, A, w, sets=16, rounds=20, ahead=3):
     us = sorted(1000 * e[0].elapsed_time(e[1]) for e in ev)
     del graph, caches, lib
     torch.cuda.empty_cache()
-    merge_reads = merge_read_probe(torch, probe)
+    merge_reads = merge_read_probe(torch, probe) if own else None
     page_bytes = 2 * w.kv_heads * n_pages * 32 * w.head_dim * 2
     med = statistics.median(us)
     return {'workload': w.name, 'grid': f'{splits} splits x {w.kv_heads} KV heads, 512 threads',
@@ -641,6 +644,9 @@ def main():
                     help='only time the plain read of the KV pages one split-K launch of WORKLOAD '
                          '(default verify8_16k) streams, and exit')
     ap.add_argument('--ahead', type=int, default=3, help='--read-probe: pages of loads in flight per wave (1-4)')
+    ap.add_argument('--probe-splits', metavar='S[,S...]',
+                    help='--read-probe: read the same pages over these key splits per KV head instead of '
+                         'the launch\'s own (one line each)')
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get('WORLD_SIZE', '1')) != 1:
         print('bench.py measures one GPU only: the attention path runs on a single MI355X; '
@@ -660,8 +666,10 @@ def main():
         return
     lib = load_library()
     if args.read_probe:
-        print(json.dumps({'read_probe': read_probe(torch, A, WORKLOADS[args.read_probe], ahead=args.ahead)}),
-              flush=True)
+        grids = [int(x) for x in args.probe_splits.split(',')] if args.probe_splits else [None]
+        for splits in grids:
+            r = read_probe(torch, A, WORKLOADS[args.read_probe], ahead=args.ahead, splits=splits)
+            print(json.dumps({'read_probe': r}), flush=True)
         return
     if args.drop_in:
         print(json.dumps({'drop_in': 'qv_test_attention, host buffers, median of 5 after 1 warm-up',
