@@ -310,7 +310,7 @@ def copy_probe(mib, repeats=5):
     log(f'copy probe: {repeats} x {mib} MiB device-to-device copies')
 
 
-def read_probe(torch, A, w, sets=16, rounds=20, ahead=3, splits=None):
+def read_probe(torch, A, w, sets=16, rounds=20, ahead=3, splits=None, merge=True):
     """The plain read of one split-K launch's KV pages (rsp_read_pages in
     libredshift_probe.so): the grid, runs and page addresses of
     attention_ring for workload `w` (57 splits x 4 KV heads for verify8_16k),
@@ -320,7 +320,8 @@ def read_probe(torch, A, w, sets=16, rounds=20, ahead=3, splits=None):
     pair, in graphs of `sets` launches replayed `rounds` times; returns the
     median and mean us per launch and the read rate of the algorithmic bytes.
     `splits` replaces the launch's own key splits (the same pages over
-    another grid); the merge reads are then not measured."""
+    another grid); the merge reads are then not measured, nor with
+    merge=False."""
     import ctypes as ct
 
     from redshift_amd.build import PROBE_LIBRARY
@@ -379,7 +380,7 @@ def read_probe(torch, A, w, sets=16, rounds=20, ahead=3, splits=None):
     us = sorted(1000 * e[0].elapsed_time(e[1]) for e in ev)
     del graph, caches, lib
     torch.cuda.empty_cache()
-    merge_reads = merge_read_probe(torch, probe) if own else None
+    merge_reads = merge_read_probe(torch, probe) if own and merge else None
     page_bytes = 2 * w.kv_heads * n_pages * 32 * w.head_dim * 2
     med = statistics.median(us)
     return {'workload': w.name, 'grid': f'{splits} splits x {w.kv_heads} KV heads, 512 threads',
@@ -719,6 +720,20 @@ def main():
                         'what': 'us per layer of each timed graph replay (an event pair around each)'},
         'provenance': prov,
     }
+    # A plain read of the same pages with the same grid, timed the same way
+    # (a graph of launches): what reading those bytes alone costs.
+    log('decode_139k: plain read of its pages')
+    try:
+        plain = read_probe(torch, A, w, sets=16, rounds=10, ahead=2, merge=False)
+        result['roofline']['plain_read'] = {
+            'us': plain['us_per_launch_in_graph'], 'frac_hbm': plain['frac_hbm'], 'grid': plain['grid'],
+            'kernel_over_plain_read': round(r['split_graph_us'] / plain['us_per_launch_in_graph'], 4),
+            'what': 'rsp_read_pages (libredshift_probe.so): non-temporal 16-byte loads of the same K and V '
+                    'pages with the same runs and grid, 512 threads per workgroup, 2 pages in flight per wave, '
+                    'no arithmetic, 16 rotating cache sets; us per launch in a graph. A reference point, not '
+                    'a bound: the split kernel pipelines its own loads and can read them as fast or faster'}
+    except Exception as e:   # a measurement aid: its absence does not void the line
+        log(f'plain read not measured: {e}')
     chosen = [] if args.no_extra else [x for x in args.extras.split(',') if x]
     if chosen:
         extra = {}
