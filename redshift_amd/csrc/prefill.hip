@@ -123,6 +123,14 @@ struct PrefillArgs {
     float *part_o;
     float *part_ml;
     int splits;
+    // Raw calls merged by combine_prefill: the partial rows as O / l in two
+    // 16-bit planes of the same layout, plane A at part_o and plane B right
+    // after it (the fp32 rows' bytes): fp16 values in plane A for a KV head
+    // whose V is fp16 (fp16 pages, or bf16 ones copied to fp16); for a head
+    // that takes the exact bf16 products, the fp32 values' top 16 bits in
+    // plane A and bottom 16 in plane B, and the row sums stored negated (so
+    // the combine knows the format from the sums it loads anyway).
+    int half_parts;
     // A fused prefill chunk that prepares its own query and keys
     // (attention_prefill_prep): the prepare kernel's inputs besides q_gate
     // (`gate`), and the chunk's token count.
@@ -701,13 +709,49 @@ __device__ __forceinline__ void prefill_rows(const PrefillArgs &a, KV *kring, VT
         if (row >= 0 && row < row_end) {
             const size_t part = (size_t)h * a.splits + split;
             const bool none = m == -INFINITY;   // no key of this split: empty
-            float *po = a.part_o + (part * R + row) * D + 4 * g;
+            constexpr bool EXACT_V = std::is_same<VT, __bf16>::value;
+            if (!QSPLIT && a.half_parts) {
+                // O / l (a convex combination of V rows: fp16 holds it to
+                // 2^-11 relative when V is fp16).  As in the other 16-bit
+                // partials, lane groups g and g^1 swap halves of each pair
+                // of 16-dim tiles so that every lane stores 8 consecutive
+                // dims (16 B; 64 contiguous bytes per row).  Swap partners
+                // share their row, so both take part or neither does.
+                typedef unsigned U2 __attribute__((ext_vector_type(2)));
+                typedef _Float16 H4 __attribute__((ext_vector_type(4)));
+                const float inv = none ? 0.f : 1.f / l;
+                uint16_t *pa = reinterpret_cast<uint16_t *>(a.part_o) + (part * R + row) * D + 16 * (g & 1) + 4 * (g & 2);
+                uint16_t *pb = pa + (size_t)a.kv_heads * a.splits * R * D;
+                auto store_pair = [&](uint16_t *dst, U2 x, U2 y) __attribute__((always_inline)) {
+                    const auto s0 = __builtin_amdgcn_permlane16_swap(x[0], y[0], false, false);
+                    const auto s1 = __builtin_amdgcn_permlane16_swap(x[1], y[1], false, false);
+                    *reinterpret_cast<U4 *>(dst) = U4{s0[0], s1[0], s0[1], s1[1]};
+                };
 #pragma unroll
-            for (int dt = 0; dt < DT; ++dt)
-                *reinterpret_cast<f32x4 *>(po + dt * 16) = none ? f32x4{0.f, 0.f, 0.f, 0.f} : acc[dt];
+                for (int dt = 0; dt < DT; dt += 2) {
+                    const f32x4 x = acc[dt] * inv, y = acc[dt + 1] * inv;
+                    if constexpr (EXACT_V) {
+                        const U4 bx = __builtin_bit_cast(U4, x), by = __builtin_bit_cast(U4, y);
+                        store_pair(pa + dt * 16, U2{(bx[0] >> 16) | (bx[1] & 0xFFFF0000u), (bx[2] >> 16) | (bx[3] & 0xFFFF0000u)},
+                                   U2{(by[0] >> 16) | (by[1] & 0xFFFF0000u), (by[2] >> 16) | (by[3] & 0xFFFF0000u)});
+                        store_pair(pb + dt * 16, U2{(bx[0] & 0xFFFFu) | (bx[1] << 16), (bx[2] & 0xFFFFu) | (bx[3] << 16)},
+                                   U2{(by[0] & 0xFFFFu) | (by[1] << 16), (by[2] & 0xFFFFu) | (by[3] << 16)});
+                    } else {
+                        store_pair(pa + dt * 16,
+                                   __builtin_bit_cast(U2, H4{(_Float16)x[0], (_Float16)x[1], (_Float16)x[2], (_Float16)x[3]}),
+                                   __builtin_bit_cast(U2, H4{(_Float16)y[0], (_Float16)y[1], (_Float16)y[2], (_Float16)y[3]}));
+                    }
+                }
+            } else {
+                float *po = a.part_o + (part * R + row) * D + 4 * g;
+#pragma unroll
+                for (int dt = 0; dt < DT; ++dt)
+                    *reinterpret_cast<f32x4 *>(po + dt * 16) = none ? f32x4{0.f, 0.f, 0.f, 0.f} : acc[dt];
+            }
             if (g == 0) {
+                const float sum = none ? 0.f : l;
                 a.part_ml[part * 2 * R + row] = m;
-                a.part_ml[part * 2 * R + R + row] = none ? 0.f : l;
+                a.part_ml[part * 2 * R + R + row] = !QSPLIT && a.half_parts && EXACT_V ? -sum : sum;
             }
         }
         return;
@@ -944,10 +988,11 @@ PrefillPlan plan_prefill(const Shape &s, Dtype dtype, bool precise) {
 
 // ---- combine of split prefill partials ----
 // One wave per (row, KV head), lane l head dims DV*l .. DV*l+DV-1: the splits'
-// (m, l) pairs (the same address in every lane) and partial rows are loaded
-// kCombineBatch at a time, all in flight together, and folded into a running
-// (max, sum, row) in base 2.  A split that saw no key of the row stored
-// max -inf, sum 0 and a zero row, and weighs 0.
+// (m, l) pairs (the same address in every lane) and partial rows (fp32, or
+// the 16-bit planes of PrefillArgs::half_parts) are loaded kCombineBatch at
+// a time, all in flight together, and folded into a running (max, sum, row)
+// in base 2.  A split that saw no key of the row stored max -inf, sum 0 and
+// a zero row, and weighs 0.
 struct CombinePrefillArgs {
     const float *part_o;
     const float *part_ml;
@@ -959,7 +1004,8 @@ struct CombinePrefillArgs {
 // kCombineWideBatch one round of all of them (more registers per wave).
 constexpr int kCombineBatch = 8, kCombineWideBatch = 24, kCombineThreads = 256;
 
-template <int D, typename KV, int MODE, int kCombineBatch>
+// HALF: the partial rows are PrefillArgs::half_parts planes (raw calls).
+template <int D, typename KV, int MODE, int kCombineBatch, bool HALF>
 __global__ __launch_bounds__(kCombineThreads)
 void combine_prefill(CombinePrefillArgs c) {
     constexpr int DV = D / kWave;
@@ -967,20 +1013,60 @@ void combine_prefill(CombinePrefillArgs c) {
     const int wave = blockIdx.x * (kCombineThreads / kWave) + (threadIdx.x >> 6), lane = threadIdx.x & 63;
     if (wave >= c.rows * c.kv_heads) return;
     const int h = wave / c.rows, row = wave - h * c.rows;
+    typedef uint16_t HV __attribute__((ext_vector_type(DV)));
     const float *ml = c.part_ml + (size_t)h * c.splits * 2 * c.rows + row;
-    const float *po = c.part_o + ((size_t)h * c.splits * c.rows + row) * D + lane * DV;
+    const size_t e0 = ((size_t)h * c.splits * c.rows + row) * D + lane * DV;
+    const float *po = c.part_o + e0;
+    const uint16_t *pa = reinterpret_cast<const uint16_t *>(c.part_o) + e0;
+    const uint16_t *pb = pa + (size_t)c.kv_heads * c.splits * c.rows * D;
     const size_t stride = (size_t)c.rows * D;
     float M = -INFINITY, L = 0.f;
     FV acc = {};
     for (int s0 = 0; s0 < c.splits; s0 += kCombineBatch) {
         float mv[kCombineBatch], lv[kCombineBatch];
         FV ov[kCombineBatch];
+        if constexpr (HALF) {
+            // Plane A with the sums; a negative sum (every split of a KV
+            // head alike) says the planes hold fp32 halves: then plane B.
+            HV av[kCombineBatch];
 #pragma unroll
-        for (int i = 0; i < kCombineBatch; ++i) {
-            const int sc = min(s0 + i, c.splits - 1);
-            mv[i] = ml[(size_t)sc * 2 * c.rows];
-            lv[i] = ml[(size_t)sc * 2 * c.rows + c.rows];
-            ov[i] = *reinterpret_cast<const FV *>(po + sc * stride);
+            for (int i = 0; i < kCombineBatch; ++i) {
+                const int sc = min(s0 + i, c.splits - 1);
+                mv[i] = ml[(size_t)sc * 2 * c.rows];
+                lv[i] = ml[(size_t)sc * 2 * c.rows + c.rows];
+                av[i] = *reinterpret_cast<const HV *>(pa + sc * stride);
+            }
+            if (__builtin_signbit(lv[0])) {
+                HV bv[kCombineBatch];
+#pragma unroll
+                for (int i = 0; i < kCombineBatch; ++i)
+                    bv[i] = *reinterpret_cast<const HV *>(pb + min(s0 + i, c.splits - 1) * stride);
+#pragma unroll
+                for (int i = 0; i < kCombineBatch; ++i) {
+                    lv[i] = -lv[i];
+#pragma unroll
+                    for (int d = 0; d < DV; ++d)
+                        ov[i][d] = __uint_as_float(((uint32_t)av[i][d] << 16) | bv[i][d]) * lv[i];
+                }
+            } else {
+                // (The whole vector reinterpreted: a bit cast of one element
+                // of a 16-bit vector compiled to its first element's value.)
+                typedef _Float16 FH __attribute__((ext_vector_type(DV)));
+#pragma unroll
+                for (int i = 0; i < kCombineBatch; ++i) {
+                    const FH fh = __builtin_bit_cast(FH, av[i]);
+#pragma unroll
+                    for (int d = 0; d < DV; ++d) ov[i][d] = (float)fh[d] * lv[i];
+                }
+            }
+        } else {
+#pragma unroll
+            for (int i = 0; i < kCombineBatch; ++i) {
+                const int sc = min(s0 + i, c.splits - 1);
+                mv[i] = ml[(size_t)sc * 2 * c.rows];
+                lv[i] = ml[(size_t)sc * 2 * c.rows + c.rows];
+                ov[i] = *reinterpret_cast<const FV *>(po + sc * stride);
+            }
         }
         float rm = M;
 #pragma unroll
@@ -1020,18 +1106,22 @@ void combine_prefill(CombinePrefillArgs c) {
     }
 }
 
+template <int D, int B>
+const void *combine_prefill_pick(Dtype dtype, bool out_f32, bool gated, bool half) {
+    // Gated (fused) and precise calls store fp32 rows, raw calls the planes.
+    if (gated) return half ? nullptr : (const void *)&combine_prefill<D, float, kOutGated, B, false>;
+    if (out_f32)
+        return half ? (const void *)&combine_prefill<D, float, kOutF32, B, true>
+                    : (const void *)&combine_prefill<D, float, kOutF32, B, false>;
+    if (!half) return nullptr;
+    return dtype == Dtype::BF16 ? (const void *)&combine_prefill<D, __bf16, kOutSame, B, true>
+                                : (const void *)&combine_prefill<D, _Float16, kOutSame, B, true>;
+}
+
 template <int D>
-const void *combine_prefill_kernel(Dtype dtype, bool out_f32, bool gated, bool wide) {
-    if (wide) {
-        if (gated) return (const void *)&combine_prefill<D, float, kOutGated, kCombineWideBatch>;
-        if (out_f32) return (const void *)&combine_prefill<D, float, kOutF32, kCombineWideBatch>;
-        return dtype == Dtype::BF16 ? (const void *)&combine_prefill<D, __bf16, kOutSame, kCombineWideBatch>
-                                    : (const void *)&combine_prefill<D, _Float16, kOutSame, kCombineWideBatch>;
-    }
-    if (gated) return (const void *)&combine_prefill<D, float, kOutGated, kCombineBatch>;
-    if (out_f32) return (const void *)&combine_prefill<D, float, kOutF32, kCombineBatch>;
-    return dtype == Dtype::BF16 ? (const void *)&combine_prefill<D, __bf16, kOutSame, kCombineBatch>
-                                : (const void *)&combine_prefill<D, _Float16, kOutSame, kCombineBatch>;
+const void *combine_prefill_kernel(Dtype dtype, bool out_f32, bool gated, bool wide, bool half) {
+    return wide ? combine_prefill_pick<D, kCombineWideBatch>(dtype, out_f32, gated, half)
+                : combine_prefill_pick<D, kCombineBatch>(dtype, out_f32, gated, half);
 }
 
 }  // namespace
@@ -1050,9 +1140,10 @@ namespace {
 // waves per row request up to 64 splits in one round (62 splits of 96 rows:
 // 27.5 us per call against 31.1 us with combine_prefill's batches in turn).
 void launch_prefill_combine(const Shape &s, Dtype dtype, const float *part_o, const float *part_ml, int splits,
-                            void *out, bool out_f32, const float *gate, hipStream_t stream) {
+                            bool half_parts, void *out, bool out_f32, const float *gate, hipStream_t stream) {
     const int rows = s.group() * s.tokens;
     if (splits > kCombineWideBatch) {
+        require(!half_parts, "16-bit partial rows go to combine_prefill");
         SplitPlan cp = {};
         cp.kind = SplitKind::Stream;   // fp32 partial rows, default-policy stores
         cp.rows = rows;
@@ -1074,8 +1165,9 @@ void launch_prefill_combine(const Shape &s, Dtype dtype, const float *part_o, co
     const long long blocks = (waves + kCombineThreads / kWave - 1) / (kCombineThreads / kWave);
     require(blocks < (1LL << 31), "prefill combine exceeds the grid");
     const bool wide = splits > 2 * kCombineBatch;
-    const void *kernel = s.head_dim == 256 ? combine_prefill_kernel<256>(dtype, out_f32, gate != nullptr, wide)
-                                           : combine_prefill_kernel<128>(dtype, out_f32, gate != nullptr, wide);
+    const void *kernel = s.head_dim == 256 ? combine_prefill_kernel<256>(dtype, out_f32, gate != nullptr, wide, half_parts)
+                                           : combine_prefill_kernel<128>(dtype, out_f32, gate != nullptr, wide, half_parts);
+    require(kernel != nullptr, "no prefill combine for this partial format");
     void *cargs[] = {&c};
     check(hipLaunchKernel(kernel, dim3((unsigned)blocks), dim3(kCombineThreads), cargs, 0, stream));
 }
@@ -1143,7 +1235,7 @@ void launch_prefill_prep(const FusedToken &tok, float *out, void *workspace, hip
     check(hipLaunchKernel((const void *)&attention_prefill_prep, dim3((unsigned)grid), dim3(kPreciseRows / 16 * kWave),
                           args, 0, stream));
     if (plan.splits > 1)
-        launch_prefill_combine(s, Dtype::F16, a.part_o, a.part_ml, plan.splits, out, true, tok.q_gate, stream);
+        launch_prefill_combine(s, Dtype::F16, a.part_o, a.part_ml, plan.splits, false, out, true, tok.q_gate, stream);
 }
 
 void launch_prefill(const Shape &s, Dtype dtype, bool precise, float scale, const void *q,
@@ -1173,6 +1265,8 @@ void launch_prefill(const Shape &s, Dtype dtype, bool precise, float scale, cons
     if (plan.splits > 1) {
         a.part_o = reinterpret_cast<float *>(static_cast<char *>(workspace) + plan.part_offset);
         a.part_ml = a.part_o + (size_t)s.kv_heads * plan.splits * a.rows * s.head_dim;
+        // Raw rows that combine_prefill merges travel as 16-bit planes.
+        a.half_parts = !precise && plan.splits <= kCombineWideBatch;
     }
     const bool d256 = s.head_dim == 256;
     const int threads = (plan.passes == 2 ? 8 : plan.rows / 16) * kWave;
@@ -1181,7 +1275,8 @@ void launch_prefill(const Shape &s, Dtype dtype, bool precise, float scale, cons
     void *args[] = {&a};
     auto combine = [&] {
         if (plan.splits > 1)
-            launch_prefill_combine(s, dtype, a.part_o, a.part_ml, plan.splits, out, out_f32, gate, stream);
+            launch_prefill_combine(s, dtype, a.part_o, a.part_ml, plan.splits, a.half_parts != 0, out, out_f32, gate,
+                                   stream);
     };
     if (precise) {
         const void *kernel = d256 ? precise_prefill_kernel<256>(gate != nullptr, plan.passes)
