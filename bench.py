@@ -297,6 +297,35 @@ def measured_traffic():
     return None
 
 
+def trace_summary(db_path, gap=1.6):
+    """Median kernel durations of a rocprofv3 kernel trace (the rocpd SQLite
+    database `-o run` writes as run_results.db), per kernel name, grid and
+    work-group size, each such group split into duration clusters where
+    consecutive sorted durations jump by more than `gap` times (the same
+    kernel and grid serving workloads of different sizes, e.g. decode at
+    139,264 and at 16,392 keys).  Prints one line per cluster."""
+    import sqlite3
+    con = sqlite3.connect(f'file:{db_path}?mode=ro', uri=True)
+    groups = {}
+    for name, grid, wg, duration in con.execute(
+            'select name, grid_x, workgroup_x, duration from kernels order by start'):
+        groups.setdefault((name, grid, wg), []).append(duration)
+    con.close()
+    for (name, grid, wg), durations in groups.items():
+        durations.sort()
+        clusters, cur = [], [durations[0]]
+        for d in durations[1:]:
+            if d > gap * cur[-1] and len(cur) > 2:
+                clusters.append(cur)
+                cur = [d]
+            else:
+                cur.append(d)
+        clusters.append(cur)
+        for c in clusters:
+            print(f'{name[:110]}  grid_x={grid} wg={wg} calls={len(c)} '
+                  f'median_ns={statistics.median(c):.0f} mean_ns={statistics.mean(c):.0f}')
+
+
 def copy_probe(mib, repeats=5):
     """A plain device copy of `mib` MiB, `repeats` times: the calibration
     kernel for the FETCH_SIZE / WRITE_SIZE counters (bytes known exactly)."""
@@ -645,10 +674,15 @@ def main():
                     help='only time the plain read of the KV pages one split-K launch of WORKLOAD '
                          '(default verify8_16k) streams, and exit')
     ap.add_argument('--ahead', type=int, default=3, help='--read-probe: pages of loads in flight per wave (1-4)')
+    ap.add_argument('--trace-summary', metavar='DB',
+                    help='only print the median kernel durations of a rocprofv3 kernel trace database, and exit')
     ap.add_argument('--probe-splits', metavar='S[,S...]',
                     help='--read-probe: read the same pages over these key splits per KV head instead of '
                          'the launch\'s own (one line each)')
     args = ap.parse_args()
+    if args.trace_summary:
+        trace_summary(args.trace_summary)
+        return
     if args.gpus != 1 or int(os.environ.get('WORLD_SIZE', '1')) != 1:
         print('bench.py measures one GPU only: the attention path runs on a single MI355X; '
               'multi-GPU sharding is a design note, not a measured configuration.', file=sys.stderr)
