@@ -42,8 +42,10 @@
 // whose L2s then hold that head's pages for all of its workgroups).  A call
 // with too few row workgroups to occupy every CU (a short chunk on a long
 // prefix) splits each row workgroup's pages into equal runs, one workgroup
-// per run; their fp32 partial rows are merged by combine_prefill (below) or,
-// for many runs, attention_combine, as in split-K decode.
+// per run; their partial rows are merged by combine_prefill (below) or, for
+// many runs, attention_combine, as in split-K decode.  A raw call merged by
+// combine_prefill stores them as O / l in 16-bit planes (PrefillArgs::
+// half_parts), the precise and gated calls and the many-run ones as fp32.
 #include "combine.hpp"
 #include "kernels.hpp"
 #include "lds.hpp"
