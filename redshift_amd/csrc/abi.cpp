@@ -174,9 +174,10 @@ size_t fused_partials_bytes(int batch, int position) {
 // the prepared prefill, whose workgroups prepare their query rows, its
 // cached runs attend to keys 0 .. position-1 and one split per row
 // workgroup prepares, appends and attends to the chunk's keys, then the
-// gated combine.  A longer chunk: the prepare kernel writes the query's hi +
-// lo parts to q_hilo (2 * batch * 24 * 256 fp16) and appends the new K/V to
-// the pages, then attention (with the sigmoid gate) runs on them: its
+// gated combine.  A longer chunk: the prepare kernel appends the new K/V to
+// the pages (keys only; q_hilo is not written), then the precise prefill,
+// which prepares its query rows from q_gate itself (RMSNorm, RoPE, hi + lo
+// parts, the prepare kernel's functions) and applies the sigmoid gate: its
 // workgroups read new keys that other workgroups would append, so the append
 // stays a launch of its own there.
 void fused_attention(float *out, void *k_pages, void *v_pages, const float *q_gate, const float *key,
@@ -213,11 +214,12 @@ void fused_attention(float *out, void *k_pages, void *v_pages, const float *q_ga
         rs::launch_prefill_prep(fused_token(), out, partials, stream);
         return;
     }
-    const rs::Shape s{H, HKV, D, batch, position, capacity};
+    // Longer chunks: the keys and values appended first (every workgroup
+    // reads keys that others would append), then the prefill, which
+    // prepares its query rows from q_gate itself.
     rs::launch_prepare(q_hilo, k_pages, v_pages, q_gate, key, value, q_norm, k_norm, batch, position,
-                       capacity, epsilon, stream);
-    run_attention(s, rs::Dtype::F16, true, 1.0f / 16.0f, q_hilo, q_hilo + (size_t)batch * H * D, k_pages,
-                  v_pages, partials, out, true, q_gate, stream);
+                       capacity, epsilon, stream, true);
+    rs::launch_prefill_fused(fused_token(), out, partials, stream);
 }
 
 [[noreturn]] void not_in_library(const char *name) {

@@ -213,6 +213,12 @@ bool prefill_prep_fits(int tokens, int position);
 PrefillPlan plan_prefill_prep_for(int tokens, int position, int cus);
 size_t prefill_prep_workspace_bytes(int tokens, int position);
 void launch_prefill_prep(const FusedToken &tok, float *out, void *workspace, hipStream_t stream);
+// A fused prefill chunk too long for launch_prefill_prep, after its keys and
+// values were appended (launch_prepare, keys_only): the precise, gated
+// prefill with its query prepared from q_gate in the kernel, then the gated
+// combine when its keys are split.  workspace: prefill_workspace_bytes of
+// the chunk's precise fp16 shape.
+void launch_prefill_fused(const FusedToken &tok, float *out, void *workspace, hipStream_t stream);
 
 // Whole pages 0 .. pages-1 of every KV head, K and V, from caches of
 // src_capacity tokens to caches of dst_capacity tokens (checkpoint/restore).
@@ -234,10 +240,11 @@ void launch_split_query(void *q_hilo, const float *q, size_t n, hipStream_t stre
 // RMSNorm + RoPE of q and k, fp16 append of k and v into the pages at
 // position..position+batch-1 (the reference's attn_prepare semantics for the
 // fixed 24/4/256 model).  Writes the prepared fp32 q as two fp16 arrays
-// [2][batch][24][256]: hi = fp16(q), lo = fp16(q - hi).
+// [2][batch][24][256]: hi = fp16(q), lo = fp16(q - hi); keys_only: k and v
+// alone (q_hilo unused), for a prefill that prepares its query itself.
 void launch_prepare(void *q_hilo, void *k_pages, void *v_pages, const float *q_gate,
                     const float *key, const float *value, const float *q_norm,
                     const float *k_norm, int batch, int position, int capacity,
-                    float epsilon, hipStream_t stream);
+                    float epsilon, hipStream_t stream, bool keys_only = false);
 
 }  // namespace rs

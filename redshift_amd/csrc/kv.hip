@@ -58,10 +58,10 @@ void convert(void *k_pages, void *v_pages, const void *k_rows, const void *v_row
 __global__ __launch_bounds__(kWave)
 void prepare_kernel(_Float16 *q_hilo, _Float16 *k_pages, _Float16 *v_pages, const float *q_gate,
                     const float *key, const float *value, const float *q_norm,
-                    const float *k_norm, int position, size_t head_stride, float epsilon) {
+                    const float *k_norm, int position, size_t head_stride, float epsilon, int head0) {
     constexpr int D = kModelHeadDim, H = kModelQHeads, HKV = kModelKvHeads;
     static_assert(D == 4 * kWave, "four dims per lane");
-    const int h = blockIdx.x, t = blockIdx.y, lane = threadIdx.x;
+    const int h = head0 + blockIdx.x, t = blockIdx.y, lane = threadIdx.x;
     const bool is_q = h < H;
     const int kh = h - H;
     const float *src = is_q ? q_gate + ((size_t)t * H + h) * 2 * D : key + ((size_t)t * HKV + kh) * D;
@@ -180,12 +180,13 @@ void launch_split_query(void *q_hilo, const float *q, size_t n, hipStream_t stre
 void launch_prepare(void *q_hilo, void *k_pages, void *v_pages, const float *q_gate,
                     const float *key, const float *value, const float *q_norm,
                     const float *k_norm, int batch, int position, int capacity,
-                    float epsilon, hipStream_t stream) {
-    hipLaunchKernelGGL(prepare_kernel, dim3(kModelQHeads + kModelKvHeads, batch),
+                    float epsilon, hipStream_t stream, bool keys_only) {
+    const int head0 = keys_only ? kModelQHeads : 0;
+    hipLaunchKernelGGL(prepare_kernel, dim3(kModelQHeads + kModelKvHeads - head0, batch),
                        dim3(kWave), 0, stream, static_cast<_Float16 *>(q_hilo),
                        static_cast<_Float16 *>(k_pages),
                        static_cast<_Float16 *>(v_pages), q_gate, key, value, q_norm, k_norm,
-                       position, (size_t)capacity * kModelHeadDim, epsilon);
+                       position, (size_t)capacity * kModelHeadDim, epsilon, head0);
     check(hipGetLastError());
 }
 

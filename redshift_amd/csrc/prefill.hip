@@ -98,6 +98,9 @@ __device__ __forceinline__ float unpack_hi(uint32_t w, _Float16) {
 }
 
 constexpr float kLazy = 8.f;
+// prefill_rows' PREP bits: the query prepared from q_gate in the kernel; the
+// chunk's own keys prepared and appended in the kernel too.
+constexpr int kPrepQuery = 1, kPrepKeys = 2;
 
 
 struct PrefillArgs {
@@ -158,16 +161,18 @@ __device__ __forceinline__ int v_slot_token(int g, int j) {
 // the two passes of the two-pass instance (eight waves over ROWS = 192 rows:
 // pass 0 gives waves 0-3 the round-0 tiles and waves 4-7 the round-1 tiles,
 // pass 1 gives waves 0-3 the round-2 tiles and waves 4-7 none).
-// PREP (attention_prefill_prep, the fused chunk of 9 .. 128 - position % 32
-// tokens): the query rows are prepared here from q_gate (RMSNorm, gamma,
-// RoPE, hi + lo parts); the splits are runs over the cached keys 0 ..
-// position-1, which every row sees, and the last run then attends to the
-// chunk's own keys as well: it prepares them into its LDS rings (the prepare
-// kernel's functions, so the same bits) and its workgroup 0 appends them to
-// the pages.  No workgroup reads a key that another one appends.
-// (PREP: qn_stage is 1 KiB of LDS per wave, for the q_norm weights.)
+// PREP, bit kPrepQuery (the fused path's precise prefill): the query rows
+// are prepared here from q_gate (RMSNorm, gamma, RoPE, hi + lo parts) rather
+// than read as prepared hi + lo parts.  Bit kPrepKeys as well
+// (attention_prefill_prep, the fused chunk of 9 .. 128 - position % 32
+// tokens): the splits are runs over the cached keys 0 .. position-1, which
+// every row sees, and the last run then attends to the chunk's own keys as
+// well: it prepares them into its LDS rings (the prepare kernel's functions,
+// so the same bits) and its workgroup 0 appends them to the pages.  No
+// workgroup reads a key that another one appends.  (kPrepQuery: qn_stage is
+// 1 KiB of LDS per wave, for the q_norm weights.)
 template <int D, typename KV, typename VT, bool PSPLIT, bool QSPLIT, int MODE, int ROWS, int PASS = -1,
-          bool PREP = false>
+          int PREP = 0>
 __device__ __forceinline__ void prefill_rows(const PrefillArgs &a, KV *kring, VT *vring, const void *v_pages,
                                              size_t v_head_stride, float *qn_stage = nullptr) {
     using V8 = typename Vec8<KV>::type;
@@ -177,9 +182,11 @@ __device__ __forceinline__ void prefill_rows(const PrefillArgs &a, KV *kring, VT
     using PV8 = typename Vec8<PT>::type;
     constexpr int kPWaves = PASS < 0 ? ROWS / 16 : 8;
     static_assert(PASS < 0 || ROWS == 3 * 4 * 16, "two passes of eight waves over three rounds of tiles");
-    static_assert(!PREP || (D == kModelHeadDim && QSPLIT && PSPLIT && MODE == kOutGated && PASS < 0 &&
-                            std::is_same<KV, _Float16>::value && std::is_same<VT, _Float16>::value),
-                  "the prepared chunk is the fused model's: fp32 query as hi + lo parts, gated output");
+    constexpr bool PQ = (PREP & kPrepQuery) != 0, PK = (PREP & kPrepKeys) != 0;
+    static_assert(!PQ || (D == kModelHeadDim && QSPLIT && PSPLIT && MODE == kOutGated &&
+                          std::is_same<KV, _Float16>::value && std::is_same<VT, _Float16>::value),
+                  "the prepared query is the fused model's: fp32 query as hi + lo parts, gated output");
+    static_assert(!PK || (PQ && PASS < 0), "the chunk's own keys come with its prepared query, in one pass");
     constexpr int KS = D / 32, DT = D / 16;
     constexpr int PAGE = 32 * D;                       // elements of one K (or V) page
     constexpr int PAGE_BYTES = PAGE * 2;
@@ -207,8 +214,8 @@ __device__ __forceinline__ void prefill_rows(const PrefillArgs &a, KV *kring, VT
     const int R = a.rows;
     const int rest = blockIdx.x / a.kv_heads;
     const int j = rest % a.n_tiles, split = rest / a.n_tiles;
-    // PREP: the last run attends to the chunk's keys too (uniform per workgroup).
-    const bool new_keys = PREP && split == a.splits - 1;
+    // kPrepKeys: the last run attends to the chunk's keys too (uniform per workgroup).
+    const bool new_keys = PK && split == a.splits - 1;
     static_assert(kPWaves % 4 == 0 && kPWaves / 4 <= 3, "one to three rounds of four waves");
     const int T = (R + 15) / 16, K = 4 * a.n_tiles, slot = 4 * j + (w & 3);
     const int round = PASS == 1 ? (w < 4 ? 2 : 3) : w >> 2;   // round 3: no tile
@@ -228,19 +235,19 @@ __device__ __forceinline__ void prefill_rows(const PrefillArgs &a, KV *kring, VT
     V8 qf[KS], qlo[QSPLIT ? KS : 1];
     int limit;
     [[maybe_unused]] int row_token;
-    // PREP: the row's fp32 query in the same layout (k-step ks: two float4),
+    // kPrepQuery: the row's fp32 query in the same layout (k-step ks: two float4),
     // and the q_norm weights as the prepare kernel holds them (lane l: dims
     // 64i + l); prepared once they have landed (prep_query).
-    [[maybe_unused]] f32x4 qx[PREP ? KS : 1][2];
+    [[maybe_unused]] f32x4 qx[PQ ? KS : 1][2];
     [[maybe_unused]] float gw[4];
     [[maybe_unused]] int qpos = 0, tile_pos = 0;
     {
         const int row = min(max(row0 + (lane & 15), 0), max(row_end, 1) - 1);
         const int t = row / a.group, gg = row - t * a.group;
-        // PREP's cached runs: every row sees every cached key.
+        // kPrepKeys' cached runs: every row sees every cached key.
         row_token = t;
-        limit = PREP ? a.position - 1 : a.position + t;
-        if constexpr (PREP) {
+        limit = PK ? a.position - 1 : a.position + t;
+        if constexpr (PQ) {
             qpos = a.position + t;
             // The position of the tile's first (clamped) row's token; the
             // tile's rows span at most four tokens (16 rows of 6 heads).
@@ -268,10 +275,10 @@ __device__ __forceinline__ void prefill_rows(const PrefillArgs &a, KV *kring, VT
     // Keys this workgroup can see: 0 .. position + (token of its last row:
     // the last valid row of tile T-1-4j, or in the second pass of tile
     // T-3K+4j+3; none when that tile is padding).
-    // (PREP: the cached keys 0 .. position-1 first.)
+    // (kPrepKeys: the cached keys 0 .. position-1 first.)
     const int last_tile = PASS == 1 ? T - 3 * K + 4 * j + 3 : T - 1 - 4 * j;
     const int wg_keys = last_tile < 0 ? 0 : a.position + (min(16 * (last_tile + 1), R) - 1) / a.group + 1;
-    int n_keys = PREP && last_tile >= 0 ? a.position : wg_keys;
+    int n_keys = PK && last_tile >= 0 ? a.position : wg_keys;
     const int n = (n_keys + 31) / 32;
     // This split's pages: p0 + i for i = 0 .. nl-1 (local index i, ring
     // buffer i % 4).  nl is uniform over the workgroup; nl = 0 leaves empty
@@ -282,14 +289,14 @@ __device__ __forceinline__ void prefill_rows(const PrefillArgs &a, KV *kring, VT
     // Pages of this wave: those its last valid row sees (none without one).
     const int wave_last = min(row0 + 15, row_end - 1);
     const int wave_keys = wave_last < max(row0, 0) ? 0 : a.position + wave_last / a.group + 1;
-    int nw = min(max((PREP && wave_keys ? n : (wave_keys + 31) / 32) - p0, 0), nl);
+    int nw = min(max((PK && wave_keys ? n : (wave_keys + 31) / 32) - p0, 0), nl);
     // Pages from which on some row of this wave masks keys (every row sees
-    // the keys up to position + its first row's token; PREP's cached keys:
-    // up to position - 1).  Keys before key_lo are masked too (PREP's
+    // the keys up to position + its first row's token; kPrepKeys' cached keys:
+    // up to position - 1).  Keys before key_lo are masked too (kPrepKeys'
     // chunk keys: the cached ones of their first page).
-    int wave_first_limit = PREP ? a.position - 1 : a.position + max(row0, 0) / a.group;
+    int wave_first_limit = PK ? a.position - 1 : a.position + max(row0, 0) / a.group;
     int key_lo = 0;
-    // PREP: pages come from the LDS rings as the workgroup prepared them
+    // kPrepKeys: pages come from the LDS rings as the workgroup prepared them
     // (the chunk's keys) rather than from global memory.
     [[maybe_unused]] bool from_lds = false;
 
@@ -372,12 +379,12 @@ __device__ __forceinline__ void prefill_rows(const PrefillArgs &a, KV *kring, VT
         float x[8];
 #pragma unroll
         for (int j = 0; j < 8; ++j) x[j] = s[j >> 2][j & 3] * a.scale_log2;
-        if (key0 + 31 > wave_first_limit || (PREP && key0 < key_lo)) {
+        if (key0 + 31 > wave_first_limit || (PK && key0 < key_lo)) {
             keep_branch();
 #pragma unroll
             for (int j = 0; j < 8; ++j) {
                 const int key = key0 + 16 * (j >> 2) + 4 * g + (j & 3);
-                if (key > limit || (PREP && key < key_lo)) x[j] = -INFINITY;
+                if (key > limit || (PK && key < key_lo)) x[j] = -INFINITY;
             }
         }
         float mx = __builtin_fmaxf(max3(x[0], x[1], x[2]), max3(x[3], x[4], x[5]));
@@ -473,7 +480,7 @@ __device__ __forceinline__ void prefill_rows(const PrefillArgs &a, KV *kring, VT
         s[1] = sn[1];
     };
 
-    // ---- PREP: the query's hi + lo fragments from its fp32 row ----
+    // ---- kPrepQuery: the query's hi + lo fragments from its fp32 row ----
     // RMSNorm over the row's 256 dims (each lane holds 64 of them; the four
     // lanes of a row sum theirs with lane swaps), times q_norm, RoPE on the
     // pairs (i, i+32), i < 32 (dims 8g + e of k-step 0 and 1 of the same
@@ -484,7 +491,7 @@ __device__ __forceinline__ void prefill_rows(const PrefillArgs &a, KV *kring, VT
     // angles, pair lane % 32 of the tile's tokens 0 + lane / 32 and
     // 2 + lane / 32, and every lane takes its eight from those lanes.
     [[maybe_unused]] auto prep_query = [&]() __attribute__((always_inline)) {
-      if constexpr (PREP) {
+      if constexpr (PQ) {
 #pragma clang fp contract(off)
         static_for<0, KS>([&](auto ks) { pin(qx[ks][0], qx[ks][1]); });
         pin(gw[0], gw[1], gw[2], gw[3]);
@@ -542,7 +549,7 @@ __device__ __forceinline__ void prefill_rows(const PrefillArgs &a, KV *kring, VT
             }
       }
     };
-    // ---- PREP, the last run: the chunk's keys in the rings ----
+    // ---- kPrepKeys, the last run: the chunk's keys in the rings ----
     // The K and V buffers of those pages (at most four) are zeroed, then wave
     // w prepares keys w, w+8, ... (lane l: dims 64i + l, the prepare
     // kernel's functions, so the bits it appends) and writes those this
@@ -553,7 +560,7 @@ __device__ __forceinline__ void prefill_rows(const PrefillArgs &a, KV *kring, VT
     // `position` on of the page they share, so reading them while they are
     // written is harmless.
     [[maybe_unused]] auto prep_new_keys = [&]() __attribute__((always_inline)) {
-      if constexpr (PREP) {
+      if constexpr (PK) {
             U4 *kz = reinterpret_cast<U4 *>(kring), *vz = reinterpret_cast<U4 *>(vring);
             for (int e = threadIdx.x; e < nl * PAGE / 8; e += kPWaves * kWave) {
                 kz[e] = U4{0u, 0u, 0u, 0u};
@@ -606,7 +613,7 @@ __device__ __forceinline__ void prefill_rows(const PrefillArgs &a, KV *kring, VT
         if (nl > 1) { stage(kh, 1, kring); stage(vh, 1, vring); }
         if (nl > 2) stage(kh, 2, kring);
     }
-    if constexpr (PREP) {
+    if constexpr (PQ) {
         // The query's loads precede the pages' (loads complete in order):
         // wait for them alone and prepare the query while the pages are in
         // flight.
@@ -631,7 +638,7 @@ __device__ __forceinline__ void prefill_rows(const PrefillArgs &a, KV *kring, VT
         else if (nl > 1) wait_vmcnt<3 * H>();
         else wait_vmcnt<H>();
         first_scores();
-    } else if constexpr (!PREP) {
+    } else if constexpr (!PQ) {
         wait_vmcnt<0>();   // no page of this split: the query loads only
     }
 
@@ -679,7 +686,7 @@ __device__ __forceinline__ void prefill_rows(const PrefillArgs &a, KV *kring, VT
     };
     run_pages();
 
-    if constexpr (PREP) {
+    if constexpr (PK) {
         if (new_keys) {
             // ---- the last run: then the chunk's keys, from its rings ----
             // Once every wave is done with the rings, the keys of the
@@ -782,12 +789,16 @@ __device__ __forceinline__ void prefill_rows(const PrefillArgs &a, KV *kring, VT
     }
 }
 
-template <int D, typename KV, typename VT, bool PSPLIT, bool QSPLIT, int MODE, int ROWS>
+// PREP = kPrepQuery: the fused path's chunk, its query prepared from q_gate
+// (its keys appended by a launch before).
+template <int D, typename KV, typename VT, bool PSPLIT, bool QSPLIT, int MODE, int ROWS, int PREP = 0>
 __global__ __launch_bounds__(ROWS / 16 * kWave, 1)
 void attention_prefill(PrefillArgs a) {
     __shared__ __attribute__((aligned(16))) KV kring[4 * 32 * D];
     __shared__ __attribute__((aligned(16))) VT vring[4 * 32 * D];
-    prefill_rows<D, KV, VT, PSPLIT, QSPLIT, MODE, ROWS>(a, kring, vring, a.v_pages, a.head_stride);
+    __shared__ __attribute__((aligned(16))) float qn_stage[PREP ? ROWS / 16 : 1][PREP ? D : 1];
+    prefill_rows<D, KV, VT, PSPLIT, QSPLIT, MODE, ROWS, -1, PREP>(a, kring, vring, a.v_pages, a.head_stride,
+                                                                  &qn_stage[0][0]);
 }
 
 // The fused prefill chunk that prepares its own query and keys (PREP in
@@ -799,24 +810,27 @@ void attention_prefill_prep(PrefillArgs a) {
     __shared__ __attribute__((aligned(16))) _Float16 kring[4 * 32 * D];
     __shared__ __attribute__((aligned(16))) _Float16 vring[4 * 32 * D];
     __shared__ __attribute__((aligned(16))) float qn_stage[kPreciseRows / 16][D];
-    prefill_rows<D, _Float16, _Float16, true, true, kOutGated, kPreciseRows, -1, true>(a, kring, vring, a.v_pages,
-                                                                                      a.head_stride, &qn_stage[0][0]);
+    prefill_rows<D, _Float16, _Float16, true, true, kOutGated, kPreciseRows, -1, kPrepQuery | kPrepKeys>(
+        a, kring, vring, a.v_pages, a.head_stride, &qn_stage[0][0]);
 }
 
 // The precise rows in two passes of eight waves (192 rows per workgroup):
 // one round of workgroups where 128-row ones would take two.  Between the
 // passes every wave's output stores complete (the second pass's waits count
 // its page loads only) and every wave has finished reading the rings.
-template <int D, typename KV, typename VT, bool PSPLIT, bool QSPLIT, int MODE>
+template <int D, typename KV, typename VT, bool PSPLIT, bool QSPLIT, int MODE, int PREP = 0>
 __global__ __launch_bounds__(8 * kWave, 1)
 void attention_prefill_2pass(PrefillArgs a) {
     constexpr int ROWS = kPreciseTwoPassRows;
     __shared__ __attribute__((aligned(16))) KV kring[4 * 32 * D];
     __shared__ __attribute__((aligned(16))) VT vring[4 * 32 * D];
-    prefill_rows<D, KV, VT, PSPLIT, QSPLIT, MODE, ROWS, 0>(a, kring, vring, a.v_pages, a.head_stride);
+    __shared__ __attribute__((aligned(16))) float qn_stage[PREP ? 8 : 1][PREP ? D : 1];
+    prefill_rows<D, KV, VT, PSPLIT, QSPLIT, MODE, ROWS, 0, PREP>(a, kring, vring, a.v_pages, a.head_stride,
+                                                                 &qn_stage[0][0]);
     wait_vmcnt<0>();
     ring_barrier();
-    prefill_rows<D, KV, VT, PSPLIT, QSPLIT, MODE, ROWS, 1>(a, kring, vring, a.v_pages, a.head_stride);
+    prefill_rows<D, KV, VT, PSPLIT, QSPLIT, MODE, ROWS, 1, PREP>(a, kring, vring, a.v_pages, a.head_stride,
+                                                                 &qn_stage[0][0]);
 }
 
 // bf16 pages: the workgroups of a KV head that the conversion pass did not
@@ -1236,6 +1250,46 @@ void launch_prefill_prep(const FusedToken &tok, float *out, void *workspace, hip
     void *args[] = {&a};
     check(hipLaunchKernel((const void *)&attention_prefill_prep, dim3((unsigned)grid), dim3(kPreciseRows / 16 * kWave),
                           args, 0, stream));
+    if (plan.splits > 1)
+        launch_prefill_combine(s, Dtype::F16, a.part_o, a.part_ml, plan.splits, false, out, true, tok.q_gate, stream);
+}
+
+void launch_prefill_fused(const FusedToken &tok, float *out, void *workspace, hipStream_t stream) {
+    const Shape s{kModelQHeads, kModelKvHeads, kModelHeadDim, tok.tokens, tok.position, 0};
+    const PrefillPlan plan = plan_prefill(s, Dtype::F16, true);
+    require(plan.bytes == 0 || workspace != nullptr, "this prefill needs its workspace");
+    PrefillArgs a = {};
+    a.gate = tok.q_gate;
+    a.k_pages = tok.k_pages;
+    a.v_pages = tok.v_pages;
+    a.out = out;
+    a.head_stride = tok.head_stride;
+    a.q_heads = s.q_heads;
+    a.kv_heads = s.kv_heads;
+    a.group = s.group();
+    a.rows = s.group() * s.tokens;
+    a.position = s.position;
+    a.n_tiles = plan.row_wgs;
+    a.scale_log2 = (1.0f / 16.0f) * 1.4426950408889634f;
+    a.splits = plan.splits;
+    a.q_norm = tok.q_norm;
+    a.k_norm = tok.k_norm;
+    a.epsilon = tok.epsilon;
+    a.tokens = tok.tokens;
+    if (plan.splits > 1) {
+        a.part_o = reinterpret_cast<float *>(static_cast<char *>(workspace) + plan.part_offset);
+        a.part_ml = a.part_o + (size_t)s.kv_heads * plan.splits * a.rows * s.head_dim;
+    }
+    const int threads = (plan.passes == 2 ? 8 : plan.rows / 16) * kWave;
+    const long long grid = (long long)plan.row_wgs * s.kv_heads * plan.splits;
+    require(grid * threads < (1LL << 32), "prefill launch exceeds 2^32 work-items");
+    constexpr int D = kModelHeadDim;
+    const void *kernel =
+        plan.passes == 2
+            ? (const void *)&attention_prefill_2pass<D, _Float16, _Float16, true, true, kOutGated, kPrepQuery>
+            : (const void *)&attention_prefill<D, _Float16, _Float16, true, true, kOutGated, kPreciseRows, kPrepQuery>;
+    void *args[] = {&a};
+    check(hipLaunchKernel(kernel, dim3((unsigned)grid), dim3(threads), args, 0, stream));
     if (plan.splits > 1)
         launch_prefill_combine(s, Dtype::F16, a.part_o, a.part_ml, plan.splits, false, out, true, tok.q_gate, stream);
 }
