@@ -1003,12 +1003,18 @@ PrefillPlan plan_prefill(const Shape &s, Dtype dtype, bool precise) {
 }
 
 // ---- combine of split prefill partials ----
-// One wave per (row, KV head), lane l head dims DV*l .. DV*l+DV-1: the splits'
-// (m, l) pairs (the same address in every lane) and partial rows (fp32, or
-// the 16-bit planes of PrefillArgs::half_parts) are loaded kCombineBatch at
-// a time, all in flight together, and folded into a running (max, sum, row)
-// in base 2.  A split that saw no key of the row stored max -inf, sum 0 and
-// a zero row, and weighs 0.
+// One wave per (row, KV head), lane l head dims DV*l .. DV*l+DV-1: the
+// splits' (m, l) pairs (lane s holding split s's) and partial rows (fp32, or
+// the 16-bit planes of PrefillArgs::half_parts, kCombineBatch at a time, all
+// in flight together) are merged in base 2 against the splits' largest max.
+// A split that saw no key of the row stored max -inf, sum 0 and a zero row,
+// and weighs 0.  Up to 64 splits (one per lane); the launcher sends at most
+// kCombineWideBatch.  (Loading every split's m and l in every lane, the
+// same address across the wave, took 72 loads per wave at 24 splits, each
+// with a 64-bit address of its own, and the compiler then issued the rows in
+// several rounds.  Fused 64-token chunk at 16,384, 21 splits: 63.36 -> 62.73
+// us per layer; 512 bf16 tokens at 6144, 4 splits: 99.33 -> 97.89 us;
+// medians of 5 in-process rounds each.)
 struct CombinePrefillArgs {
     const float *part_o;
     const float *part_ml;
@@ -1019,8 +1025,13 @@ struct CombinePrefillArgs {
 // Up to 2 kCombineBatch splits take rounds of 8 loads; up to
 // kCombineWideBatch one round of all of them (more registers per wave).
 constexpr int kCombineBatch = 8, kCombineWideBatch = 24, kCombineThreads = 256;
+static_assert(kCombineWideBatch <= kWave, "combine_prefill holds one split's (m, l) per lane");
 
 // HALF: the partial rows are PrefillArgs::half_parts planes (raw calls).
+// Lane s < splits loads split s's max and sum (one load each for the wave),
+// so the row loads are the wave's only other loads and all of them are in
+// flight together: the global max and the weights exp2(m_s - M) come from
+// lane reductions, and each split's weight reaches every lane by readlane.
 template <int D, typename KV, int MODE, int kCombineBatch, bool HALF>
 __global__ __launch_bounds__(kCombineThreads)
 void combine_prefill(CombinePrefillArgs c) {
@@ -1036,71 +1047,64 @@ void combine_prefill(CombinePrefillArgs c) {
     const uint16_t *pa = reinterpret_cast<const uint16_t *>(c.part_o) + e0;
     const uint16_t *pb = pa + (size_t)c.kv_heads * c.splits * c.rows * D;
     const size_t stride = (size_t)c.rows * D;
-    float M = -INFINITY, L = 0.f;
+    const int sl = min(lane, c.splits - 1);
+    const float ms = ml[(size_t)sl * 2 * c.rows];
+    const float ls = ml[(size_t)sl * 2 * c.rows + c.rows];
     FV acc = {};
+    float L = 0.f;
     for (int s0 = 0; s0 < c.splits; s0 += kCombineBatch) {
-        float mv[kCombineBatch], lv[kCombineBatch];
         FV ov[kCombineBatch];
-        if constexpr (HALF) {
-            // Plane A with the sums; a negative sum (every split of a KV
-            // head alike) says the planes hold fp32 halves: then plane B.
-            HV av[kCombineBatch];
+        HV av[kCombineBatch];
 #pragma unroll
-            for (int i = 0; i < kCombineBatch; ++i) {
-                const int sc = min(s0 + i, c.splits - 1);
-                mv[i] = ml[(size_t)sc * 2 * c.rows];
-                lv[i] = ml[(size_t)sc * 2 * c.rows + c.rows];
-                av[i] = *reinterpret_cast<const HV *>(pa + sc * stride);
-            }
-            if (__builtin_signbit(lv[0])) {
+        for (int i = 0; i < kCombineBatch; ++i) {
+            const int sc = min(s0 + i, c.splits - 1);
+            if constexpr (HALF) av[i] = *reinterpret_cast<const HV *>(pa + sc * stride);
+            else ov[i] = *reinterpret_cast<const FV *>(po + sc * stride);
+        }
+        // The weights (the same every round).
+        const float mv = lane < c.splits ? ms : -INFINITY;
+        float M = fmaxf(mv, dpp_get<0xb1>(mv));
+        M = fmaxf(M, dpp_get<0x4e>(M));
+        M = fmaxf(M, dpp_get<0x141>(M));
+        M = fmaxf(M, dpp_get<0x140>(M));
+        M = row_group_max(M);
+        const float mu = M == -INFINITY ? 0.f : M;
+        // A negative sum (every split of a KV head alike) says the planes
+        // hold fp32 halves.
+        const bool exact = HALF && __builtin_signbit(__int_as_float(__builtin_amdgcn_readfirstlane(__float_as_int(ls))));
+        const float lv = lane < c.splits ? (exact ? -ls : ls) : 0.f;
+        const float wl = lane < c.splits ? __builtin_amdgcn_exp2f(mv - mu) : 0.f;
+        if (s0 == 0) L = wave_sum_dpp(wl * lv);
+        // HALF rows are O / l: weighted by l as well.
+        const float wo = HALF ? wl * lv : wl;
+        if constexpr (HALF) {
+            if (exact) {
                 HV bv[kCombineBatch];
 #pragma unroll
                 for (int i = 0; i < kCombineBatch; ++i)
                     bv[i] = *reinterpret_cast<const HV *>(pb + min(s0 + i, c.splits - 1) * stride);
 #pragma unroll
-                for (int i = 0; i < kCombineBatch; ++i) {
-                    lv[i] = -lv[i];
+                for (int i = 0; i < kCombineBatch; ++i)
 #pragma unroll
                     for (int d = 0; d < DV; ++d)
-                        ov[i][d] = __uint_as_float(((uint32_t)av[i][d] << 16) | bv[i][d]) * lv[i];
-                }
+                        ov[i][d] = __uint_as_float(((uint32_t)av[i][d] << 16) | bv[i][d]);
             } else {
-                // (The whole vector reinterpreted: a bit cast of one element
-                // of a 16-bit vector compiled to its first element's value.)
                 typedef _Float16 FH __attribute__((ext_vector_type(DV)));
 #pragma unroll
                 for (int i = 0; i < kCombineBatch; ++i) {
                     const FH fh = __builtin_bit_cast(FH, av[i]);
 #pragma unroll
-                    for (int d = 0; d < DV; ++d) ov[i][d] = (float)fh[d] * lv[i];
+                    for (int d = 0; d < DV; ++d) ov[i][d] = (float)fh[d];
                 }
             }
-        } else {
+        }
 #pragma unroll
-            for (int i = 0; i < kCombineBatch; ++i) {
-                const int sc = min(s0 + i, c.splits - 1);
-                mv[i] = ml[(size_t)sc * 2 * c.rows];
-                lv[i] = ml[(size_t)sc * 2 * c.rows + c.rows];
-                ov[i] = *reinterpret_cast<const FV *>(po + sc * stride);
+        for (int i = 0; i < kCombineBatch; ++i) {
+            if (s0 + i < c.splits) {
+                const float w = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(wo), s0 + i));
+                acc += w * ov[i];
             }
         }
-        float rm = M;
-#pragma unroll
-        for (int i = 0; i < kCombineBatch; ++i) {
-            if (s0 + i >= c.splits) mv[i] = -INFINITY;
-            rm = fmaxf(rm, mv[i]);
-        }
-        const float mu = rm == -INFINITY ? 0.f : rm;
-        const float f = __builtin_amdgcn_exp2f(M - mu);
-        L *= f;
-        acc *= f;
-#pragma unroll
-        for (int i = 0; i < kCombineBatch; ++i) {
-            const float w = s0 + i < c.splits ? __builtin_amdgcn_exp2f(mv[i] - mu) : 0.f;
-            L += w * lv[i];
-            acc += w * ov[i];
-        }
-        M = rm;
     }
     const float inv = 1.f / L;
     const int t = row / c.group, hq = h * c.group + (row - t * c.group);
