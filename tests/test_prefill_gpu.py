@@ -73,12 +73,17 @@ def test_ordinary_values_take_the_converted_products(gpu):
     assert np.all(words == 0), words
 
 
-@pytest.mark.parametrize('case', ['huge_page', 'tiny_head', 'dead_dim', 'huge_page_d128'])
+@pytest.mark.parametrize('case', ['huge_page', 'tiny_head', 'dead_dim', 'huge_page_d128', 'huge_page_split21'])
 def test_values_outside_the_fp16_range(gpu, case):
     """V values the fp16 conversion cannot hold: the KV heads that have
-    them take the exact bf16 products."""
+    them take the exact bf16 products.  (400 tokens at 700 split their keys
+    in 4 runs; huge_page_split21, 70 tokens at 9,000, in 21, whose partial
+    rows the combine requests in one round: flagged heads' rows as fp32
+    halves in two planes, the others as fp16.)"""
     if case == 'huge_page_d128':
         w, q, k, v = inputs(300, 500, q_heads=16, kv_heads=2, head_dim=128, seed=12)
+    elif case == 'huge_page_split21':
+        w, q, k, v = inputs(70, 9000, seed=14)
     else:
         w, q, k, v = inputs(400, 700, seed=13)
     scale = 1.0
