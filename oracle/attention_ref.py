@@ -12,6 +12,11 @@ Follows ``tests/cpu_reference.py`` of the reference:
                             GQA softmax with kv head h // 6, scale 1/16, times
                             sigmoid(gate)); the order of operations follows
                             src/kernels.cu:416-434 (prepare) and 466-503.
+  * ``fused_attention_rows`` <- the same function on selected tokens of a
+                            long chunk: its prepare and fp16 append steps,
+                            then ``gqa_attention`` on the selected rows, times
+                            sigmoid(gate) (checked against ``fused_attention``
+                            in tests/test_oracle.py)
   * ``gqa_attention``    <- the raw core inside the same function
                             (tests/cpu_reference.py:79-87 without prepare and
                             gate), parametric in heads, head_dim and scale, as
@@ -111,6 +116,33 @@ def fused_attention(key_cache, value_cache, q_gate, key, value, q_norm, k_norm,
             out[t, g * G:(g + 1) * G, :] = (scores @ v_g) / scores.sum(axis=1, keepdims=True)
     out *= sigmoid(gate)
     return out.reshape(-1), kc.reshape(-1), vc.reshape(-1)
+
+
+def fused_attention_rows(key_cache, value_cache, q_gate, key, value, q_norm, k_norm,
+                         batch, position, epsilon, rows):
+    """``fused_attention`` on the tokens ``rows`` of the chunk only, for
+    chunks too long for its per-token loop: the same prepare and fp16 append
+    steps (tests/cpu_reference.py:61-76) for every new token, the causal GQA
+    softmax (``gqa_attention``, scale 1/16, kv head h // 6) for the selected
+    rows, times sigmoid(gate) (tests/cpu_reference.py:79-88).  Returns
+    ``(out, kc, vc)``: out is float64 [len(rows), 24, 256], kc/vc token-major
+    [position+batch, 4, 256] float64 caches with the appended rows.
+    """
+    H, HKV, D = Q_HEADS, KV_HEADS, HEAD_DIM
+    kc = np.asarray(key_cache, np.float64).reshape(-1)[:position * HKV * D].reshape(position, HKV, D)
+    vc = np.asarray(value_cache, np.float64).reshape(-1)[:position * HKV * D].reshape(position, HKV, D)
+    qg = np.asarray(q_gate, np.float64).reshape(batch, H, 2 * D)
+    key = np.asarray(key, np.float64).reshape(batch, HKV, D)
+    value = np.asarray(value, np.float64).reshape(batch, HKV, D)
+    pos = position + np.arange(batch)
+    kc = np.concatenate([kc, half(prepare(key, k_norm, pos[:, None], epsilon))], axis=0)
+    vc = np.concatenate([vc, half(value)], axis=0)
+    rows = np.asarray(rows).reshape(-1)
+    query = prepare(qg[rows, :, :D], q_norm, pos[rows][:, None], epsilon)
+    full = np.zeros((batch, H, D), np.float64)
+    full[rows] = query
+    out = gqa_attention(full, kc, vc, position, FUSED_SCALE, rows=rows)
+    return out * sigmoid(qg[rows, :, D:]), kc, vc
 
 
 def gqa_attention(q, k, v, position, scale, rows=None):

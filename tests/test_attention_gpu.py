@@ -424,6 +424,53 @@ def test_fused_prefill_chunk_matches_oracle(gpu, batch, position):
     assert_close(vc.float().cpu().numpy(), expected[2], 0)
 
 
+@pytest.mark.parametrize('batch,position', [(8192, 0), (2048, 139264 - 2048)])
+def test_fused_chunk_at_its_limits(gpu, batch, position):
+    """The fused entry at its documented limits: the largest chunk (8,192
+    tokens, the prepare launch then the precise prefill) and a 2048-token
+    chunk that fills the 139,264-token capacity to its last slot.  Random
+    inputs as in test_fused_random_shapes_against_oracle, except that the
+    cached keys have standard deviation 3 (so that a few of the 137,216 keys
+    dominate each row, rather than a near-uniform softmax averaging V to
+    almost zero); 16 token rows (the first and last, page edges, the middle
+    and random ones) against the oracle's selected-rows form with the
+    reference test's tolerance (output 3e-4) and relative L2 1e-3, every
+    appended K row within 2e-3 and V row exact, and the prefix unchanged bit
+    for bit."""
+    torch = gpu
+    rng = np.random.default_rng(batch + position)
+    kc = (rng.standard_normal((position, 4, 256), dtype=np.float32) * 3).astype(np.float16)
+    vc = (rng.standard_normal((position, 4, 256), dtype=np.float32) * .5).astype(np.float16)
+    q_gate = rng.standard_normal((batch, 24, 512), dtype=np.float32)
+    key = rng.standard_normal((batch, 4, 256), dtype=np.float32)
+    value = rng.standard_normal((batch, 4, 256), dtype=np.float32)
+    q_norm = (1 + .25 * rng.uniform(-1, 1, 256)).astype(np.float32)
+    k_norm = (1 + .25 * rng.uniform(-1, 1, 256)).astype(np.float32)
+    eps = 1e-6
+    rows = sorted({0, 1, 31, 32, batch // 2, batch - 2, batch - 1, *rng.choice(batch, 9, replace=False).tolist()})
+    print(f'fused limits: batch={batch} position={position} rows={rows}', flush=True)
+    want, k_all, v_all = ref.fused_attention_rows(kc, vc, q_gate, key, value, q_norm, k_norm, batch, position,
+                                                  eps, rows)
+    cache = A.PagedKV(4, 256, A.round_capacity(position + batch), torch.float16)
+    cache.k.fill_(float('nan'))
+    cache.v.fill_(float('nan'))
+    if position:
+        cache.pack(torch.from_numpy(kc).cuda(), torch.from_numpy(vc).cuda())
+    dev = [torch.from_numpy(x).cuda() for x in (q_gate, key, value, q_norm, k_norm)]
+    out = A.attention_fused(*dev, cache, position, eps)
+    new_k, new_v = cache.unpack(position, batch)
+    torch.cuda.synchronize()
+    got = out.cpu().numpy()[rows].astype(np.float64)
+    assert_close(got, want, 3e-4)
+    assert np.linalg.norm(got - want) / np.linalg.norm(want) <= 1e-3
+    assert_close(new_k.float().cpu().numpy(), k_all[position:], 2e-3)
+    assert_close(new_v.float().cpu().numpy(), v_all[position:], 0)
+    if position:
+        old_k, old_v = cache.unpack(0, position)
+        np.testing.assert_array_equal(old_k.cpu().numpy().view(np.uint16), kc.view(np.uint16))
+        np.testing.assert_array_equal(old_v.cpu().numpy().view(np.uint16), vc.view(np.uint16))
+
+
 @pytest.mark.parametrize('position', [200, 3000])
 def test_fused_prefill_chunk_equals_eight_token_steps(gpu, position):
     """One 64-token chunk (prefill kernel; after 3,000 tokens with its keys

@@ -94,6 +94,28 @@ def test_fused_attention_grouped_equals_sequential():
     np.testing.assert_array_equal(vc, seq_v)
 
 
+@pytest.mark.parametrize('batch,position,rows', [(12, 40, [0, 5, 11]), (40, 0, [0, 1, 31, 32, 39]),
+                                               (9, 300, list(range(9)))])
+def test_fused_attention_rows_equals_fused_attention(batch, position, rows):
+    """The selected-rows form (for chunks too long for the per-token loop)
+    against the per-token restatement on random inputs: the same rows to
+    float64 rounding, the same appended caches bit for bit."""
+    rng = np.random.default_rng(batch + position)
+    kc = ref.half(rng.standard_normal((position, 4, 256)) * .5)
+    vc = ref.half(rng.standard_normal((position, 4, 256)) * .5)
+    q_gate = rng.standard_normal((batch, 24, 512))
+    key = rng.standard_normal((batch, 4, 256))
+    value = rng.standard_normal((batch, 4, 256))
+    q_norm = 1 + .25 * rng.uniform(-1, 1, 256)
+    k_norm = 1 + .25 * rng.uniform(-1, 1, 256)
+    out, k_all, v_all = ref.fused_attention(kc, vc, q_gate, key, value, q_norm, k_norm, batch, position, 1e-6)
+    sel, k_sel, v_sel = ref.fused_attention_rows(kc, vc, q_gate, key, value, q_norm, k_norm, batch, position,
+                                                 1e-6, rows)
+    np.testing.assert_allclose(sel, out.reshape(batch, 24, 256)[rows], rtol=0, atol=1e-12)
+    np.testing.assert_array_equal(k_sel.reshape(-1), k_all)
+    np.testing.assert_array_equal(v_sel.reshape(-1), v_all)
+
+
 def _sdpa_reference(q, k, v, position, scale):
     """torch float64 SDPA with an explicit causal mask and kv heads repeated."""
     T, Hq, D = q.shape
