@@ -144,20 +144,20 @@ def test_full_context_other_precisions(gpu, T, dtype):
     assert_parity(got, want)
 
 
+@pytest.mark.parametrize('T,position', [(2048, 139264 - 2048), (8192, 0)])
 @pytest.mark.parametrize('dtype', ['f16', 'bf16'])
-def test_prefill_chunk_fills_the_capacity(gpu, dtype):
+def test_prefill_chunk_fills_the_capacity(gpu, dtype, T, position):
     """A 2048-token raw chunk whose last key is the 139,264-token capacity's
     last slot (the prefill kernel; bf16 through the V conversion pass over
-    all 4,352 pages), 64 outlier keys, slots past the last key NaN: 24 token
-    rows (the first and last, page edges, the middle and random ones) against
-    the oracle to both bounds, float32 output."""
-    T = 2048
-    position = 139264 - T
+    all 4,352 pages), and 8,192 tokens on an empty cache (1,024 row
+    workgroups: four rounds over 256 CUs), 64 outlier keys, slots past the
+    last key NaN: 24 token rows (the first and last, page edges, the middle
+    and random ones) against the oracle to both bounds, float32 output."""
     w = Workload('full_prefill', 24, 4, 256, T, position, 1 / 16, dtype, 950, 1.0, 0.5, 64, 8.0)
     q, k, v, _ = make_inputs(w)
     rng = np.random.default_rng(951)
     rows = sorted({0, 1, 31, 32, 1023, 1024, T - 2, T - 1, *rng.choice(T, 16, replace=False).tolist()})
-    print(f'prefill at capacity: {dtype} rows={rows}', flush=True)
+    print(f'prefill limits: {dtype} T={T} position={position} rows={rows}', flush=True)
     got = gpu_attention(w, q, k, v, gpu, fill_nan=True, out_dtype=gpu.float32)[rows]
     want = ref.gqa_attention(to_float(q, dtype), to_float(k, dtype), to_float(v, dtype), position, w.scale,
                              rows=rows)
