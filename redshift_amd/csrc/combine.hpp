@@ -14,8 +14,16 @@ namespace rs {
 // workgroup (every wave must call it, `valid` or not: it holds a workgroup
 // barrier).  Lane l owns head dims DV*l .. DV*l+DV-1 (DV = D/64);
 // wave w4 takes splits w4, w4+4, ... and issues the loads of up to kBatch of
-// them (their m, l and partial row) at once, so a combine over up to
-// 4*kBatch splits costs one memory round trip.  The waves then merge through
+// them at once, so a combine over up to 4*kBatch splits costs one memory
+// round trip: their partial rows, and their m and l held one split per lane
+// (lane i: split w4 + 4i), two loads for the wave.  The round's max and sum
+// come from lane reductions over the 16 lanes of the first row, and each
+// split's weight reaches every lane by readlane.  (One m and one l load per
+// split in every lane, the same address across the wave, took 0.06-0.38 us
+// more per layer: decode at 139,264 keys 86.50 -> 86.35, at 4,096 10.80 ->
+// 10.50, verify-8 at 16K 19.91 -> 19.85, the fused decode 88.32 -> 87.94
+// and the fused verify-8 25.23 -> 24.95 us; medians of 3 in-process
+// rounds.)  The waves then merge through
 // `scratch` (4*(D+1) + 4 floats of LDS per group), each thread one head dim.
 // PT is the type of the partial rows: float (unnormalised O) or _Float16
 // (O / l, weighted by l here).  NT: the partial rows are loaded
@@ -37,6 +45,7 @@ __device__ __forceinline__ void combine_row(const PT *part_o, const float *part_
                                             const FusedToken *tok = nullptr, float scale_log2 = 0.f) {
     constexpr int DV = D / kWave;
     constexpr int kBatch = 16;
+    static_assert(kBatch <= 16, "a round's (m, l) pairs sit in the 16 lanes of one DPP row");
     float *part = scratch;                   // [4][D + 1]
     float *wmax = scratch + 4 * (D + 1);     // [4]
     const int rc = valid ? row : rows - 1;   // in-bounds reads for a padding group
@@ -88,13 +97,14 @@ __device__ __forceinline__ void combine_row(const PT *part_o, const float *part_
         // the last one) so that all of them are in flight together; the
         // surplus ones are discarded afterwards.
         typedef PT OV __attribute__((ext_vector_type(DV)));
-        float mv[kBatch], lv[kBatch];
         OV ov[kBatch];
+        // Lane i < kBatch: the max and sum of split s0 + w4 + 4i (two loads
+        // for the wave instead of two per split).
+        const int sl = min(s0 + w4 + 4 * min(lane, kBatch - 1), splits - 1);
+        const float ms = ml[(size_t)sl * 2 * rows], ls = ml[(size_t)sl * 2 * rows + rows];
 #pragma unroll
         for (int i = 0; i < kBatch; ++i) {
             const int sc = min(s0 + w4 + 4 * i, splits - 1);
-            mv[i] = ml[(size_t)sc * 2 * rows];
-            lv[i] = ml[(size_t)sc * 2 * rows + rows];
             const OV *src = reinterpret_cast<const OV *>(po + (size_t)sc * stride);
             if constexpr (NT)
                 ov[i] = __builtin_nontemporal_load(src);
@@ -116,30 +126,34 @@ __device__ __forceinline__ void combine_row(const PT *part_o, const float *part_
                 }
             }
         }
-#pragma unroll
-        for (int i = 0; i < kBatch; ++i) {
-            if (s0 + w4 + 4 * i >= splits) {
-                mv[i] = -INFINITY;
-                lv[i] = 0.f;
-                ov[i] = OV{};
-            }
-        }
-        // Fold this round into the running (M, L, acc) of the wave.
-        float rm = M;
-#pragma unroll
-        for (int i = 0; i < kBatch; ++i) rm = fmaxf(rm, mv[i]);
+        const bool live = lane < kBatch && s0 + w4 + 4 * lane < splits;
+        const float mv = live ? ms : -INFINITY, lv = live ? ls : 0.f;
+        // The round's max over lanes 0..15 (one row of 16 lanes), then
+        // uniform.
+        float bm = fmaxf(mv, dpp_get<0xb1>(mv));
+        bm = fmaxf(bm, dpp_get<0x4e>(bm));
+        bm = fmaxf(bm, dpp_get<0x141>(bm));
+        bm = fmaxf(bm, dpp_get<0x140>(bm));
+        const float rm = fmaxf(M, __int_as_float(__builtin_amdgcn_readfirstlane(__float_as_int(bm))));
         const float mu = rm == -INFINITY ? 0.f : rm;
         const float f = __builtin_amdgcn_exp2f(M - mu);
-        L *= f;
+        const float wl = __builtin_amdgcn_exp2f(mv - mu);
+        float sl_ = wl * lv;
+        sl_ = sl_ + dpp_get<0xb1>(sl_);
+        sl_ = sl_ + dpp_get<0x4e>(sl_);
+        sl_ = sl_ + dpp_get<0x141>(sl_);
+        sl_ = sl_ + dpp_get<0x140>(sl_);
+        L = L * f + __int_as_float(__builtin_amdgcn_readfirstlane(__float_as_int(sl_)));
 #pragma unroll
         for (int d = 0; d < DV; ++d) acc[d] *= f;
+        const float wo_l = kNormalised ? wl * lv : wl;
 #pragma unroll
         for (int i = 0; i < kBatch; ++i) {
-            const float wgt = __builtin_amdgcn_exp2f(mv[i] - mu);
-            L += wgt * lv[i];
-            const float wo = kNormalised ? wgt * lv[i] : wgt;
+            if (s0 + w4 + 4 * i < splits) {
+                const float wo = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(wo_l), i));
 #pragma unroll
-            for (int d = 0; d < DV; ++d) acc[d] += wo * (float)ov[i][d];
+                for (int d = 0; d < DV; ++d) acc[d] += wo * (float)ov[i][d];
+            }
         }
         M = rm;
     }
