@@ -12,7 +12,9 @@ namespace rs {
 
 // One row of one KV head, combined by the four waves w4 = 0..3 of a
 // workgroup (every wave must call it, `valid` or not: it holds a workgroup
-// barrier).  Lane l owns head dims DV*l .. DV*l+DV-1 (DV = D/64);
+// barrier); with QD > 1, head dims dq*D/QD .. of that row only (a workgroup
+// per (row, dq)).  Lane l owns head dims DV*l .. DV*l+DV-1 of them (DV =
+// D/QD/64);
 // wave w4 takes splits w4, w4+4, ... and issues the loads of up to kBatch of
 // them at once, so a combine over up to 4*kBatch splits costs one memory
 // round trip: their partial rows, and their m and l held one split per lane
@@ -37,20 +39,23 @@ namespace rs {
 // t) and folds each in as one more split: score q . k_j with the prepared
 // fp32 query (tok->q_prep) and the fp16 key the split kernel appended at
 // position + j, weight 1 at its own max, value the appended fp16 v_j.
-template <int D, typename KV, typename PT, bool NT, bool NEWKEY = false>
+template <int D, typename KV, typename PT, bool NT, bool NEWKEY = false, int QD = 1>
 __device__ __forceinline__ void combine_row(const PT *part_o, const float *part_ml, int splits,
                                             int rows, int group, int q_heads, int row, int h,
                                             bool valid, int w4, int lane, float *scratch,
                                             void *out, const float *gate, int out_mode,
-                                            const FusedToken *tok = nullptr, float scale_log2 = 0.f) {
-    constexpr int DV = D / kWave;
+                                            const FusedToken *tok = nullptr, float scale_log2 = 0.f, int dq = 0) {
+    static_assert(QD == 1 || !NEWKEY, "the new keys' scores need every head dim");
+    constexpr int DW = D / QD;            // head dims of this workgroup: dq*DW ..
+    constexpr int DV = DW / kWave;
+    static_assert(DV >= 1, "a lane owns at least one head dim");
     constexpr int kBatch = 16;
     static_assert(kBatch <= 16, "a round's (m, l) pairs sit in the 16 lanes of one DPP row");
-    float *part = scratch;                   // [4][D + 1]
-    float *wmax = scratch + 4 * (D + 1);     // [4]
+    float *part = scratch;                   // [4][DW + 1]
+    float *wmax = scratch + 4 * (DW + 1);    // [4]
     const int rc = valid ? row : rows - 1;   // in-bounds reads for a padding group
     const float *ml = part_ml + (size_t)h * splits * 2 * rows + rc;
-    const PT *po = part_o + ((size_t)h * splits * rows + rc) * D + lane * DV;
+    const PT *po = part_o + ((size_t)h * splits * rows + rc) * D + dq * DW + lane * DV;
     constexpr bool kNormalised = !std::is_same<PT, float>::value;
     const size_t stride = (size_t)rows * D;
 
@@ -60,8 +65,8 @@ __device__ __forceinline__ void combine_row(const PT *part_o, const float *part_
     // store instead of costing one more round trip.
     const int jd = w4 * kWave + lane;
     float gv = 0.f;
-    if (out_mode == kOutGated && valid && jd < D)
-        gv = gate[((size_t)t * q_heads + hq) * 2 * D + D + jd];
+    if (out_mode == kOutGated && valid && jd < DW)
+        gv = gate[((size_t)t * q_heads + hq) * 2 * D + D + dq * DW + jd];
 
     float M = -INFINITY, L = 0.f, acc[DV] = {};
     // NEWKEY: this wave's new keys (lane l: dims DV*l .. +DV-1 of the query
@@ -175,24 +180,24 @@ __device__ __forceinline__ void combine_row(const PT *part_o, const float *part_
     // accumulators in its slot; then thread j of the workgroup merges head
     // dim j of the four slots and stores it.
 #pragma unroll
-    for (int d = 0; d < DV; ++d) part[w4 * (D + 1) + lane * DV + d] = acc[d];
+    for (int d = 0; d < DV; ++d) part[w4 * (DW + 1) + lane * DV + d] = acc[d];
     if (lane == 0) {
         wmax[w4] = M;
-        part[w4 * (D + 1) + D] = L;
+        part[w4 * (DW + 1) + DW] = L;
     }
     __syncthreads();
-    if (valid && jd < D) {
+    if (valid && jd < DW) {
         const float G = fmaxf(fmaxf(wmax[0], wmax[1]), fmaxf(wmax[2], wmax[3]));
         const float gu = G == -INFINITY ? 0.f : G;
         float Lt = 0.f, o = 0.f;
 #pragma unroll
         for (int ww = 0; ww < 4; ++ww) {
             const float f = __builtin_amdgcn_exp2f(wmax[ww] - gu);
-            Lt += part[ww * (D + 1) + D] * f;
-            o += part[ww * (D + 1) + jd] * f;
+            Lt += part[ww * (DW + 1) + DW] * f;
+            o += part[ww * (DW + 1) + jd] * f;
         }
         o /= Lt;
-        const size_t idx = ((size_t)t * q_heads + hq) * D + jd;
+        const size_t idx = ((size_t)t * q_heads + hq) * D + dq * DW + jd;
         if (out_mode == kOutGated) {
             static_cast<float *>(out)[idx] = o * (1.f / (1.f + expf(-gv)));
         } else if (out_mode == kOutF32) {
