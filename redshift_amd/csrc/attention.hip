@@ -756,10 +756,13 @@ void launch_fused_tokens(const FusedToken &tok, int capacity, void *workspace, f
     c.tok = ft;
     // The stream kernel stores its partials with the default policy, the
     // ring kernel non-temporally; the combine loads them the same way.
+    // The stream kernel's rows (one or two tokens) take a workgroup per
+    // quarter of the head dims, as the raw decode's combine does.
     const void *combine = ring ? (const void *)&attention_combine<D, _Float16, kOutGated, float, true, false>
-                               : (const void *)&attention_combine<D, _Float16, kOutGated, float, false, true>;
+                               : (const void *)&attention_combine<D, _Float16, kOutGated, float, false, true, D / kWave>;
     void *combine_args[] = {&c};
-    check(hipLaunchKernel(combine, dim3(plan.rows, kv_heads), dim3(kWaves * kWave), combine_args, 0, stream));
+    check(hipLaunchKernel(combine, dim3(plan.rows, kv_heads, ring ? 1 : D / kWave), dim3(kWaves * kWave), combine_args,
+                          0, stream));
 }
 
 }  // namespace rs

@@ -45,7 +45,6 @@ __device__ __forceinline__ void combine_row(const PT *part_o, const float *part_
                                             bool valid, int w4, int lane, float *scratch,
                                             void *out, const float *gate, int out_mode,
                                             const FusedToken *tok = nullptr, float scale_log2 = 0.f, int dq = 0) {
-    static_assert(QD == 1 || !NEWKEY, "the new keys' scores need every head dim");
     constexpr int DW = D / QD;            // head dims of this workgroup: dq*DW ..
     constexpr int DV = DW / kWave;
     static_assert(DV >= 1, "a lane owns at least one head dim");
@@ -69,9 +68,10 @@ __device__ __forceinline__ void combine_row(const PT *part_o, const float *part_
         gv = gate[((size_t)t * q_heads + hq) * 2 * D + D + dq * DW + jd];
 
     float M = -INFINITY, L = 0.f, acc[DV] = {};
-    // NEWKEY: this wave's new keys (lane l: dims DV*l .. +DV-1 of the query
-    // and of each key and value), requested with the partials.
-    constexpr int NK = 2;
+    // NEWKEY: this wave's new keys (lane l: dims 4l .. 4l+3 of the query and
+    // of each key, for the score over every head dim; dims DV*l .. +DV-1 of
+    // this workgroup's head dims of each value), requested with the partials.
+    constexpr int NK = 2, DQK = D / kWave;
     typedef _Float16 H4 __attribute__((ext_vector_type(4)));
     f32x4 qn = {};
     H4 kn[NK] = {};
@@ -79,20 +79,20 @@ __device__ __forceinline__ void combine_row(const PT *part_o, const float *part_
     float m_new[NK] = {-INFINITY, -INFINITY};
     bool has[NK] = {};
     if constexpr (NEWKEY) {
-        static_assert(D == 4 * kWave && DV == 4, "the fused model's 256-dim heads");
+        static_assert(D == 4 * kWave && DQK == 4, "the fused model's 256-dim heads");
 #pragma unroll
         for (int k = 0; k < NK; ++k) has[k] = w4 + 4 * k < tok->tokens && w4 + 4 * k <= t;
-        if (has[0]) qn = *reinterpret_cast<const f32x4 *>(tok->q_prep + ((size_t)h * rows + rc) * D + lane * DV);
+        if (has[0]) qn = *reinterpret_cast<const f32x4 *>(tok->q_prep + ((size_t)h * rows + rc) * D + lane * DQK);
         const _Float16 *kp = static_cast<const _Float16 *>(tok->k_pages) + (size_t)h * tok->head_stride;
         const _Float16 *vp = static_cast<const _Float16 *>(tok->v_pages) + (size_t)h * tok->head_stride;
 #pragma unroll
         for (int k = 0; k < NK; ++k) {
             if (has[k]) {
                 const int pos = tok->position + w4 + 4 * k;
-                // Dims DV*l .. +3 of a key are contiguous in its page.
-                kn[k] = *reinterpret_cast<const H4 *>(kp + k_page_offset(pos, lane * DV, D));
+                // Dims 4l .. 4l+3 of a key are contiguous in its page.
+                kn[k] = *reinterpret_cast<const H4 *>(kp + k_page_offset(pos, lane * DQK, D));
 #pragma unroll
-                for (int d = 0; d < DV; ++d) vh[k][d] = vp[v_page_offset(pos, lane * DV + d, D)];
+                for (int d = 0; d < DV; ++d) vh[k][d] = vp[v_page_offset(pos, dq * DW + lane * DV + d, D)];
             }
         }
     }
@@ -125,7 +125,7 @@ __device__ __forceinline__ void combine_row(const PT *part_o, const float *part_
                     if (has[k]) {
                         float dot = 0.f;
 #pragma unroll
-                        for (int d = 0; d < DV; ++d) dot += qn[d] * (float)kn[k][d];
+                        for (int d = 0; d < DQK; ++d) dot += qn[d] * (float)kn[k][d];
                         m_new[k] = wave_sum_dpp(dot) * scale_log2;
                     }
                 }
