@@ -26,7 +26,8 @@ namespace rs {
 // 10.50, verify-8 at 16K 19.91 -> 19.85, the fused decode 88.32 -> 87.94
 // and the fused verify-8 25.23 -> 24.95 us; medians of 3 in-process
 // rounds.)  The waves then merge through
-// `scratch` (4*(D+1) + 4 floats of LDS per group), each thread one head dim.
+// `scratch` (4*(D/QD+1) + 4 floats of LDS per group), each thread one head
+// dim.
 // PT is the type of the partial rows: float (unnormalised O) or _Float16
 // (O / l, weighted by l here).  NT: the partial rows are loaded
 // non-temporally, matching partials that were stored that way (the load
