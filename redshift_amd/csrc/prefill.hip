@@ -1022,9 +1022,12 @@ struct CombinePrefillArgs {
     const float *gate;
     int q_heads, group, rows, kv_heads, splits;
 };
-// Up to 2 kCombineBatch splits take rounds of 8 loads; up to
+// Up to kCombineNarrowBatch splits take one round of 4 loads (no surplus
+// loads, fewer registers: the 512-token bf16 chunk's 4-split combine took
+// 6.84 against 7.16 us per call with rounds of 8, by a kernel trace of both
+// in one process), up to 2 kCombineBatch rounds of 8, up to
 // kCombineWideBatch one round of all of them (more registers per wave).
-constexpr int kCombineBatch = 8, kCombineWideBatch = 24, kCombineThreads = 256;
+constexpr int kCombineBatch = 8, kCombineWideBatch = 24, kCombineNarrowBatch = 4, kCombineThreads = 256;
 static_assert(kCombineWideBatch <= kWave, "combine_prefill holds one split's (m, l) per lane");
 
 // HALF: the partial rows are PrefillArgs::half_parts planes (raw calls).
@@ -1139,9 +1142,10 @@ const void *combine_prefill_pick(Dtype dtype, bool out_f32, bool gated, bool hal
 }
 
 template <int D>
-const void *combine_prefill_kernel(Dtype dtype, bool out_f32, bool gated, bool wide, bool half) {
-    return wide ? combine_prefill_pick<D, kCombineWideBatch>(dtype, out_f32, gated, half)
-                : combine_prefill_pick<D, kCombineBatch>(dtype, out_f32, gated, half);
+const void *combine_prefill_kernel(Dtype dtype, bool out_f32, bool gated, int splits, bool half) {
+    return splits > 2 * kCombineBatch ? combine_prefill_pick<D, kCombineWideBatch>(dtype, out_f32, gated, half)
+         : splits > kCombineNarrowBatch ? combine_prefill_pick<D, kCombineBatch>(dtype, out_f32, gated, half)
+                                        : combine_prefill_pick<D, kCombineNarrowBatch>(dtype, out_f32, gated, half);
 }
 
 }  // namespace
@@ -1184,9 +1188,8 @@ void launch_prefill_combine(const Shape &s, Dtype dtype, const float *part_o, co
     const long long waves = (long long)rows * s.kv_heads;
     const long long blocks = (waves + kCombineThreads / kWave - 1) / (kCombineThreads / kWave);
     require(blocks < (1LL << 31), "prefill combine exceeds the grid");
-    const bool wide = splits > 2 * kCombineBatch;
-    const void *kernel = s.head_dim == 256 ? combine_prefill_kernel<256>(dtype, out_f32, gate != nullptr, wide, half_parts)
-                                           : combine_prefill_kernel<128>(dtype, out_f32, gate != nullptr, wide, half_parts);
+    const void *kernel = s.head_dim == 256 ? combine_prefill_kernel<256>(dtype, out_f32, gate != nullptr, splits, half_parts)
+                                           : combine_prefill_kernel<128>(dtype, out_f32, gate != nullptr, splits, half_parts);
     require(kernel != nullptr, "no prefill combine for this partial format");
     void *cargs[] = {&c};
     check(hipLaunchKernel(kernel, dim3((unsigned)blocks), dim3(kCombineThreads), cargs, 0, stream));
