@@ -240,6 +240,9 @@ __device__ __forceinline__ void prefill_rows(const PrefillArgs &a, KV *kring, VT
     // 64i + l); prepared once they have landed (prep_query).
     [[maybe_unused]] f32x4 qx[PQ ? KS : 1][2];
     [[maybe_unused]] float gw[4];
+    // kPrepQuery: the RoPE cosines and sines of the tile's tokens (see
+    // prep_query), evaluated while the query loads are in flight.
+    [[maybe_unused]] float ca = 0.f, sa = 0.f, cb = 0.f, sb = 0.f;
     [[maybe_unused]] int qpos = 0, tile_pos = 0;
     {
         const int row = min(max(row0 + (lane & 15), 0), max(row_end, 1) - 1);
@@ -512,10 +515,6 @@ __device__ __forceinline__ void prefill_rows(const PrefillArgs &a, KV *kring, VT
                 lds_wait<2 * (KS / 2 - 1 - decltype(k_)::value)>(qg[ks][0], qg[ks][1]);
             });
         });
-        const double fq = rope_freq(lane & 31);
-        float ca, sa, cb, sb;
-        rope_cos_sin(tile_pos + (lane >> 5), fq, ca, sa);
-        rope_cos_sin(tile_pos + 2 + (lane >> 5), fq, cb, sb);
         float sq = 0.f;
 #pragma unroll
         for (int ks = 0; ks < KS; ++ks)
@@ -614,6 +613,16 @@ __device__ __forceinline__ void prefill_rows(const PrefillArgs &a, KV *kring, VT
         if (nl > 2) stage(kh, 2, kring);
     }
     if constexpr (PQ) {
+        // Each lane's two RoPE angles depend on the tile's position only, so
+        // they are evaluated before the wait for the query rows (fused
+        // 64-token chunk at 16,384: 62.75 -> 62.52 us per layer, medians of
+        // 7 in-process rounds; 66.12 -> 65.79 on another box).
+        {
+#pragma clang fp contract(off)
+            const double fq = rope_freq(lane & 31);
+            rope_cos_sin(tile_pos + (lane >> 5), fq, ca, sa);
+            rope_cos_sin(tile_pos + 2 + (lane >> 5), fq, cb, sb);
+        }
         // The query's loads precede the pages' (loads complete in order):
         // wait for them alone and prepare the query while the pages are in
         // flight.
