@@ -159,6 +159,8 @@ def test_random_prefill_shapes(gpu, q_heads, kv_heads, head_dim, T, position, dt
     (24, 4, 256, 300, 300, 'f16'),     # 19 pages: not split
     (24, 4, 256, 96, 16000, 'f16'),    # 12 row workgroups: 21 splits, one combine round of 24
     (24, 4, 256, 70, 9000, 'bf16'),    # 12 row workgroups: 21 splits, V through the fp16 copy
+    (24, 4, 256, 800, 2000, 'bf16'),   # 25 row workgroups: 2 splits (the combine's 4-split batch)
+    (24, 4, 256, 600, 1000, 'f16'),    # 19 row workgroups: 3 splits
 ])
 def test_split_prefill_against_oracle(gpu, q_heads, kv_heads, head_dim, T, position, dtype):
     """Calls with too few row workgroups to fill the device split their keys
