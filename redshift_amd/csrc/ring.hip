@@ -267,12 +267,20 @@ void attention_ring(SplitArgs a) {
                     if (key0 + r >= a.n_keys) vf[dt][r] = (KV)0.f;
             });
         }
-        // O^T += V^T P^T over the 16 keys.
+        // O^T += V^T P^T over the 16 keys.  With hi + lo P, both parts go
+        // through one 16x16x32 product: its k = 8g + r takes P_hi of key
+        // 4g + r and k = 8g + 4 + r P_lo of the same key (lane group g's own
+        // registers), and V^T holds those four keys in both halves, so the
+        // product sums V (P_hi + P_lo) over the 16 keys in one instruction
+        // instead of two 16x16x16 ones.
         static_for<0, DT>([&](auto dt_) {
             constexpr int dt = decltype(dt_)::value;
             lds_wait<DT - 1 - dt>(vf[dt]);
-            acc[dt] = mfma(vf[dt], ph, acc[dt]);
-            if constexpr (PSPLIT) acc[dt] = mfma(vf[dt], pl, acc[dt]);
+            if constexpr (PSPLIT)
+                acc[dt] = mfma(__builtin_shufflevector(vf[dt], vf[dt], 0, 1, 2, 3, 0, 1, 2, 3),
+                               __builtin_shufflevector(ph, pl, 0, 1, 2, 3, 4, 5, 6, 7), acc[dt]);
+            else
+                acc[dt] = mfma(vf[dt], ph, acc[dt]);
         });
     };
 
