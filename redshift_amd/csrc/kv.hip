@@ -105,30 +105,40 @@ void split_query(_Float16 *hi, _Float16 *lo, const float *q, size_t n) {
     }
 }
 
-// Copy of whole pages: for every KV head, elements [0, n) of its run (the
-// pages of tokens 0 .. n/D-1) from a cache of stride src_stride to one of
-// stride dst_stride.  Each thread moves kCopyUnroll 16-byte pieces of one
+// Copy of whole pages: for every KV head of K and of V, elements [0, n) of
+// its run (the pages of tokens 0 .. n/D-1) from a cache of stride src_stride
+// to one of stride dst_stride, both tensors in one launch (chunks of K's heads
+// first, then V's).  Each thread moves kCopyUnroll 16-byte pieces of one
 // head, all loads issued before the stores, non-temporal (every byte is
 // touched once).  n is a whole number of pages, so per_head (16-byte pieces
 // per head) is a multiple of 32 * D / 8 = 512 (D = 128) or 1024 (D = 256):
 // the launch takes kCopyThreads threads when kCopyUnroll * kCopyThreads
 // divides it, else half as many.  A sweep on the 139,264-token K and V
-// prefix (4 KV heads, D = 256; per call, K and V): 2 x 512 174.4 us, 4 x 256
-// 177.7, 2 x 256 180.2, 4 x 128 184.8, 4 x 512 185.4, default-policy
-// loads and stores 202.1.
+// prefix (4 KV heads, D = 256; per call, with a launch per tensor): 2 x 512
+// 174.4 us, 4 x 256 177.7, 2 x 256 180.2, 4 x 128 184.8, 4 x 512 185.4,
+// default-policy loads and stores 202.1.  One launch for both measured the
+// same (176.47 against 176.81 us) and saves a launch per call.
 constexpr int kCopyUnroll = 2, kCopyThreads = 512;
+struct CopyArgs {
+    uint4 *dst_k, *dst_v;
+    const uint4 *src_k, *src_v;
+    size_t dst_stride, src_stride, n;
+    int kv_heads;
+};
 __global__ __launch_bounds__(kCopyThreads)
-void copy_pages(uint4 *dst, const uint4 *src, size_t dst_stride, size_t src_stride, size_t n,
-                int kv_heads) {
-    const size_t per_head = n / 8;   // uint4 per head
+void copy_pages(CopyArgs a) {
+    const size_t per_head = a.n / 8;   // uint4 per head
     const size_t chunk = (size_t)kCopyUnroll * blockDim.x;
-    const size_t chunks = per_head / chunk * kv_heads;
+    const size_t chunks = per_head / chunk * 2 * a.kv_heads;
     for (size_t c = blockIdx.x; c < chunks; c += gridDim.x) {
         const size_t first = c * chunk;
-        const size_t h = first / per_head, i0 = first - h * per_head + threadIdx.x;
+        size_t h = first / per_head;
+        const size_t i0 = first - h * per_head + threadIdx.x;
+        const bool v_half = h >= (size_t)a.kv_heads;   // uniform per chunk
+        if (v_half) h -= a.kv_heads;
         typedef unsigned u32x4 __attribute__((ext_vector_type(4)));
-        const u32x4 *s = reinterpret_cast<const u32x4 *>(src + h * (src_stride / 8) + i0);
-        u32x4 *d = reinterpret_cast<u32x4 *>(dst + h * (dst_stride / 8) + i0);
+        const u32x4 *s = reinterpret_cast<const u32x4 *>((v_half ? a.src_v : a.src_k) + h * (a.src_stride / 8) + i0);
+        u32x4 *d = reinterpret_cast<u32x4 *>((v_half ? a.dst_v : a.dst_k) + h * (a.dst_stride / 8) + i0);
         u32x4 v[kCopyUnroll];
 #pragma unroll
         for (int u = 0; u < kCopyUnroll; ++u) v[u] = __builtin_nontemporal_load(s + u * blockDim.x);
@@ -145,14 +155,12 @@ void launch_copy(void *dst_k, void *dst_v, const void *src_k, const void *src_v,
     if (!n) return;
     const int threads = (n / 8) % (kCopyUnroll * kCopyThreads) == 0 ? kCopyThreads : kCopyThreads / 2;
     require((n / 8) % (kCopyUnroll * threads) == 0, "page copy needs whole chunks of 16-byte pieces per head");
-    const size_t chunks = n / 8 / (kCopyUnroll * threads) * kv_heads;
-    const unsigned blocks = (unsigned)std::min<size_t>(chunks, 16384);
-    const size_t ds = (size_t)dst_capacity * head_dim, ss = (size_t)src_capacity * head_dim;
-    hipLaunchKernelGGL(copy_pages, dim3(blocks), dim3(threads), 0, stream, static_cast<uint4 *>(dst_k),
-                       static_cast<const uint4 *>(src_k), ds, ss, n, kv_heads);
-    check(hipGetLastError());
-    hipLaunchKernelGGL(copy_pages, dim3(blocks), dim3(threads), 0, stream, static_cast<uint4 *>(dst_v),
-                       static_cast<const uint4 *>(src_v), ds, ss, n, kv_heads);
+    const size_t chunks = n / 8 / (kCopyUnroll * threads) * 2 * kv_heads;
+    const unsigned blocks = (unsigned)std::min<size_t>(chunks, 32768);
+    CopyArgs a = {static_cast<uint4 *>(dst_k), static_cast<uint4 *>(dst_v), static_cast<const uint4 *>(src_k),
+                  static_cast<const uint4 *>(src_v), (size_t)dst_capacity * head_dim,
+                  (size_t)src_capacity * head_dim, n, kv_heads};
+    hipLaunchKernelGGL(copy_pages, dim3(blocks), dim3(threads), 0, stream, a);
     check(hipGetLastError());
 }
 
