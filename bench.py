@@ -554,7 +554,7 @@ def time_kv_copy(torch, A, w, layers, steps, warmup, seed):
     """The KV-cache manager's checkpoint copy (qv_kv_copy, the reference's
     copy_state prefix copy, src/runtime.cu:455-485) of a full `w.keys`-token
     prefix, every page of K and V, from each of `layers` caches to a snapshot
-    cache.  Returns microseconds per layer (one copy: two kernels, K and V)."""
+    cache.  Returns microseconds per layer (one copy: one kernel, K and V)."""
     from redshift_amd.kvcache import copy_prefix
     caches, _ = make_layers(torch, A, w, layers, seed)
     dtype = caches[0].dtype
