@@ -1014,8 +1014,8 @@ PrefillPlan plan_prefill(const Shape &s, Dtype dtype, bool precise) {
 // ---- combine of split prefill partials ----
 // One wave per (row, KV head), lane l head dims DV*l .. DV*l+DV-1: the
 // splits' (m, l) pairs (lane s holding split s's) and partial rows (fp32, or
-// the 16-bit planes of PrefillArgs::half_parts, kCombineBatch at a time, all
-// in flight together) are merged in base 2 against the splits' largest max.
+// the 16-bit planes of PrefillArgs::half_parts, BATCH at a time, all in
+// flight together) are merged in base 2 against the splits' largest max.
 // A split that saw no key of the row stored max -inf, sum 0 and a zero row,
 // and weighs 0.  Up to 64 splits (one per lane); the launcher sends at most
 // kCombineWideBatch.  (Loading every split's m and l in every lane, the
@@ -1044,7 +1044,7 @@ static_assert(kCombineWideBatch <= kWave, "combine_prefill holds one split's (m,
 // so the row loads are the wave's only other loads and all of them are in
 // flight together: the global max and the weights exp2(m_s - M) come from
 // lane reductions, and each split's weight reaches every lane by readlane.
-template <int D, typename KV, int MODE, int kCombineBatch, bool HALF>
+template <int D, typename KV, int MODE, int BATCH, bool HALF>
 __global__ __launch_bounds__(kCombineThreads)
 void combine_prefill(CombinePrefillArgs c) {
     constexpr int DV = D / kWave;
@@ -1064,11 +1064,11 @@ void combine_prefill(CombinePrefillArgs c) {
     const float ls = ml[(size_t)sl * 2 * c.rows + c.rows];
     FV acc = {};
     float L = 0.f;
-    for (int s0 = 0; s0 < c.splits; s0 += kCombineBatch) {
-        FV ov[kCombineBatch];
-        HV av[kCombineBatch];
+    for (int s0 = 0; s0 < c.splits; s0 += BATCH) {
+        FV ov[BATCH];
+        HV av[BATCH];
 #pragma unroll
-        for (int i = 0; i < kCombineBatch; ++i) {
+        for (int i = 0; i < BATCH; ++i) {
             const int sc = min(s0 + i, c.splits - 1);
             if constexpr (HALF) av[i] = *reinterpret_cast<const HV *>(pa + sc * stride);
             else ov[i] = *reinterpret_cast<const FV *>(po + sc * stride);
@@ -1091,19 +1091,19 @@ void combine_prefill(CombinePrefillArgs c) {
         const float wo = HALF ? wl * lv : wl;
         if constexpr (HALF) {
             if (exact) {
-                HV bv[kCombineBatch];
+                HV bv[BATCH];
 #pragma unroll
-                for (int i = 0; i < kCombineBatch; ++i)
+                for (int i = 0; i < BATCH; ++i)
                     bv[i] = *reinterpret_cast<const HV *>(pb + min(s0 + i, c.splits - 1) * stride);
 #pragma unroll
-                for (int i = 0; i < kCombineBatch; ++i)
+                for (int i = 0; i < BATCH; ++i)
 #pragma unroll
                     for (int d = 0; d < DV; ++d)
                         ov[i][d] = __uint_as_float(((uint32_t)av[i][d] << 16) | bv[i][d]);
             } else {
                 typedef _Float16 FH __attribute__((ext_vector_type(DV)));
 #pragma unroll
-                for (int i = 0; i < kCombineBatch; ++i) {
+                for (int i = 0; i < BATCH; ++i) {
                     const FH fh = __builtin_bit_cast(FH, av[i]);
 #pragma unroll
                     for (int d = 0; d < DV; ++d) ov[i][d] = (float)fh[d];
@@ -1111,7 +1111,7 @@ void combine_prefill(CombinePrefillArgs c) {
             }
         }
 #pragma unroll
-        for (int i = 0; i < kCombineBatch; ++i) {
+        for (int i = 0; i < BATCH; ++i) {
             if (s0 + i < c.splits) {
                 const float w = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(wo), s0 + i));
                 acc += w * ov[i];
