@@ -198,23 +198,21 @@ def sha256_of(paths):
     return h.hexdigest()
 
 
-def git_head():
-    """The checked-out commit, read from .git as plain files (None where the
-    tree was copied without it)."""
+def commit_of(lib_sha256):
+    """The commit the line was measured at and where that is known from:
+    the checkout's .git, else the commit recorded when the library was built
+    (redshift_amd/lib/build_info.json), if it describes the loaded library."""
+    from redshift_amd.build import BUILD_INFO, git_head
+    head = git_head(ROOT)
+    if head is not None:
+        return head, 'checkout'
     try:
-        head = (ROOT / '.git' / 'HEAD').read_text().strip()
-        if head.startswith('ref: '):
-            ref = head[5:]
-            path = ROOT / '.git' / ref
-            if path.exists():
-                return path.read_text().strip()
-            for line in (ROOT / '.git' / 'packed-refs').read_text().splitlines():
-                if line.endswith(' ' + ref):
-                    return line.split()[0]
-            return None
-        return head
-    except OSError:
-        return None
+        info = json.loads(BUILD_INFO.read_text())
+    except (OSError, ValueError):
+        return None, None
+    if info.get('library_sha256') == lib_sha256 and info.get('git_head'):
+        return info['git_head'], 'build'
+    return None, None
 
 
 def gpu_card(torch):
@@ -271,9 +269,11 @@ def provenance(torch, lib_path):
         sorted((ROOT / 'redshift_amd').glob('*.py')) + [ROOT / 'bench.py']
     props = torch.cuda.get_device_properties(0)
     card = gpu_card(torch)
-    return {'library_sha256': sha256_of([Path(lib_path)]), 'sources_sha256': sha256_of(sources),
+    lib_sha = sha256_of([Path(lib_path)])
+    head, head_from = commit_of(lib_sha)
+    return {'library_sha256': lib_sha, 'sources_sha256': sha256_of(sources),
             'sources': 'redshift_amd/csrc/*, include/*.h, redshift_amd/*.py, bench.py',
-            'git_head': git_head(), 'device': props.name, 'arch': props.gcnArchName,
+            'git_head': head, 'git_head_from': head_from, 'device': props.name, 'arch': props.gcnArchName,
             'cus': props.multi_processor_count, 'torch': torch.__version__,
             'hip': getattr(torch.version, 'hip', None),
             'drm_card': card.name if card is not None else None}

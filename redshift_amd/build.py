@@ -4,6 +4,8 @@ Usage: ``python -m redshift_amd.build`` (or ``__graft_entry__.build()``).
 Objects go to ``redshift_amd/_build/``, the library to
 ``redshift_amd/lib/libredshift_hip.so``.  Every call recompiles.
 """
+import hashlib
+import json
 import os
 import shutil
 import subprocess
@@ -19,6 +21,10 @@ LIBRARY = PACKAGE / 'lib' / 'libredshift_hip.so'
 # out of the attention library.
 PROBE_SOURCES = ['probe.hip']
 PROBE_LIBRARY = PACKAGE / 'lib' / 'libredshift_probe.so'
+# The commit the library was built from and the library's SHA-256, written
+# beside it by build(), for trees copied without their .git (bench.py's
+# provenance).
+BUILD_INFO = PACKAGE / 'lib' / 'build_info.json'
 ARCH = 'gfx950'
 # The host-sanitizer gate: the library's sources and a driver over its C ABI,
 # with AddressSanitizer and UndefinedBehaviorSanitizer on the host code only
@@ -144,7 +150,28 @@ def build(verbose=False, jobs=None):
     objects = dict(zip(names, (o for o, _ in results)))
     _link([objects[name] for name in SOURCES], LIBRARY)
     _link([objects[name] for name in PROBE_SOURCES], PROBE_LIBRARY)
+    BUILD_INFO.write_text(json.dumps({'git_head': git_head(),
+                                      'library_sha256': hashlib.sha256(LIBRARY.read_bytes()).hexdigest()}) + '\n')
     return LIBRARY
+
+
+def git_head(root=ROOT):
+    """The checked-out commit, read from .git as plain files (None where the
+    tree was copied without it)."""
+    try:
+        head = (root / '.git' / 'HEAD').read_text().strip()
+        if head.startswith('ref: '):
+            ref = head[5:]
+            path = root / '.git' / ref
+            if path.exists():
+                return path.read_text().strip()
+            for line in (root / '.git' / 'packed-refs').read_text().splitlines():
+                if line.endswith(' ' + ref):
+                    return line.split()[0]
+            return None
+        return head
+    except OSError:
+        return None
 
 
 def build_sanitizer(verbose=False, jobs=None):
